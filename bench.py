@@ -1,0 +1,218 @@
+"""Expert-FFN decode benchmark on one MI355X.
+
+Workload (one "step"): one decode token through one MoE layer at
+Qwen3-30B-A3B shape -- hidden 2048, 128 experts, expert FFN 768, top-8; gate
+and up Q4_K, down Q6_K, quantized from N(0, 0.02) fp32; x ~ N(0, 1) fp32,
+router logits ~ N(0, 1).  A step is the hot path on the device: softmax/top-8
+routing, then the fused expert block (gate/up, SiLU, down, router-weighted
+sum), inputs already resident in HBM.
+
+The layer is replicated R times in HBM (R x 391.6 MB) and step i uses replica
+i % R, so the routed experts of consecutive steps are cold in the 256 MB
+Infinity Cache: the number reported is cold-HBM streaming.
+
+value = algorithmic bytes (the 8 routed experts' weight bytes, 24,477,696 per
+step) x steps / timed seconds.
+"""
+import argparse
+import ctypes
+import importlib.util
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+PKG_DIR = os.path.join(ROOT, "eahmmf_inference_prototype_v-0.1.0_amd")
+HBM_PEAK_GBS = 8000.0
+D, FF, E, K = 2048, 768, 128, 8
+Q4_K, Q6_K = 12, 14
+
+
+def load_binding():
+    spec = importlib.util.spec_from_file_location("eahmmf_hip_bench", os.path.join(PKG_DIR, "eahmmf_hip.py"))
+    mod = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(mod)
+    return mod
+
+
+def build_layer(b, rng):
+    """One layer's 128 experts: gate/up [E][FF rows x Q4_K(D)], down [E][D rows x Q6_K(FF)]."""
+    grb, drb = b.row_bytes(Q4_K, D), b.row_bytes(Q6_K, FF)
+    gate = np.empty((E, FF * grb), np.uint8)
+    up = np.empty((E, FF * grb), np.uint8)
+    down = np.empty((E, D * drb), np.uint8)
+    for e in range(E):
+        gate[e] = b.quantize_rows(Q4_K, rng.normal(0, .02, (FF, D)).astype(np.float32)).reshape(-1)
+        up[e] = b.quantize_rows(Q4_K, rng.normal(0, .02, (FF, D)).astype(np.float32)).reshape(-1)
+        down[e] = b.quantize_rows(Q6_K, rng.normal(0, .02, (D, FF)).astype(np.float32)).reshape(-1)
+    return gate, up, down
+
+
+def cpu_baseline(gate, up, down, xs, logits, budget_s):
+    """Times the reference CPU expert path on a bounded sample of layer-tokens:
+    the compiled reference's own matmul (oracle/_ref) when present, else the
+    oracle's restatement; routing, SiLU and the weighted sum are the same
+    host loop as qwen3moe.cpp:1011-1067."""
+    sys.path.insert(0, ROOT)
+    import oracle
+    kind = "reference"
+    if oracle.ref_available(oracle.REF_PORTABLE_SO):
+        R = oracle.ref(oracle.REF_PORTABLE_SO)
+
+        def mm(t, w, ne0, ne1, rb, x, out):
+            R.ref_matmul(t, ne0, ne1, rb, w.ctypes.data, x.ctypes.data, 1, ne0, out.ctypes.data, ne1)
+    else:
+        kind = "port"
+        L = oracle.lib()
+
+        def mm(t, w, ne0, ne1, rb, x, out):
+            L.orc_matmul(t, ne0, ne1, rb, w.ctypes.data, x.ctypes.data, 1, ne0, out.ctypes.data, ne1)
+    grb, drb = gate.shape[1] // FF, down.shape[1] // D
+    g = np.empty(FF, np.float32)
+    u = np.empty(FF, np.float32)
+    y = np.empty(D, np.float32)
+    n = 0
+    t0 = time.perf_counter()
+    while True:
+        s = n % len(xs)
+        ids, w = oracle.route_topk(logits[s:s + 1], K)
+        acc = np.zeros(D, np.float32)
+        x = np.ascontiguousarray(xs[s])
+        for j in range(K):
+            e = int(ids[0, j])
+            mm(Q4_K, gate[e], D, FF, grb, x, g)
+            mm(Q4_K, up[e], D, FF, grb, x, u)
+            h = (g / (1.0 + np.exp(-g)) * u).astype(np.float32)
+            mm(Q6_K, down[e], FF, D, drb, h, y)
+            acc += w[0, j] * y
+        n += 1
+        el = time.perf_counter() - t0
+        if el >= budget_s:
+            break
+    bytes_per = K * (2 * FF * grb + D * drb)
+    threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+    return {"value": round(n * bytes_per / el / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": kind,
+            "sample": f"{n} single-token C2 layer evaluations (8 experts each) in {el:.1f} s, "
+                      f"OpenMP threads={threads}"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=2000)
+    ap.add_argument("--warmup", type=int, default=100)
+    ap.add_argument("--replicas", type=int, default=16)
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py runs on one GPU only (asked for --gpus {args.gpus}); the expert path shards by expert "
+              "across GPUs, which this build does not run", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    b = load_binding()
+    hip = b.lib()
+    torch.cuda.set_device(0)
+    rng = np.random.default_rng(0)
+    t_gen = time.perf_counter()
+    gate, up, down = build_layer(b, rng)
+    print(f"# quantized one layer ({gate.nbytes + up.nbytes + down.nbytes} B) in "
+          f"{time.perf_counter() - t_gen:.1f} s", file=sys.stderr, flush=True)
+    R = args.replicas
+    dgate = torch.empty((R,) + gate.shape, dtype=torch.uint8, device="cuda")
+    dup = torch.empty((R,) + up.shape, dtype=torch.uint8, device="cuda")
+    ddown = torch.empty((R,) + down.shape, dtype=torch.uint8, device="cuda")
+    hg, hu, hd = (torch.from_numpy(a).pin_memory() for a in (gate, up, down))
+    for r in range(R):
+        dgate[r].copy_(hg)
+        dup[r].copy_(hu)
+        ddown[r].copy_(hd)
+    torch.cuda.synchronize()
+    tables = []
+    for r in range(R):
+        t = np.array([[dgate[r, e].data_ptr(), dup[r, e].data_ptr(), ddown[r, e].data_ptr()] for e in range(E)],
+                     dtype=np.uint64)
+        tables.append(torch.from_numpy(t.view(np.int64)).cuda())
+    NS = 64
+    xs = rng.normal(0, 1, (NS, D)).astype(np.float32)
+    logits = rng.normal(0, 1, (NS, E)).astype(np.float32)
+    dx = torch.from_numpy(xs).cuda()
+    dlog = torch.from_numpy(logits).cuda()
+    dids = torch.empty((NS, K), dtype=torch.int32, device="cuda")
+    dw = torch.empty((NS, K), dtype=torch.float32, device="cuda")
+    dy = torch.empty((NS, D), dtype=torch.float32, device="cuda")
+    shape = b.MoeShape(Q4_K, Q4_K, Q6_K, D, FF, b.row_bytes(Q4_K, D), b.row_bytes(Q4_K, D), b.row_bytes(Q6_K, FF))
+    stream = torch.cuda.current_stream()
+    sp = ctypes.c_void_p(stream.cuda_stream)
+    vp = ctypes.c_void_p
+
+    def route(i):
+        s = i % NS
+        rc = hip.eahmmf_hip_route_topk_async(vp(dlog[s].data_ptr()), 1, E, K, vp(dids[s].data_ptr()),
+                                            vp(dw[s].data_ptr()), sp)
+        assert rc == 0, b.last_error()
+
+    def experts(i):
+        s = i % NS
+        rc = hip.eahmmf_hip_moe_decode_routed_async(ctypes.byref(shape), vp(tables[i % R].data_ptr()), E,
+                                                    vp(dids[s].data_ptr()), vp(dw[s].data_ptr()), K,
+                                                    vp(dx[s].data_ptr()), vp(dy[s].data_ptr()), sp)
+        assert rc == 0, b.last_error()
+
+    def step(i):
+        route(i)
+        experts(i)
+
+    for i in range(args.warmup):
+        step(i)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        step(args.warmup + i)
+    torch.cuda.synchronize()
+    el = time.perf_counter() - t0
+    bytes_step = K * (2 * FF * b.row_bytes(Q4_K, D) + D * b.row_bytes(Q6_K, FF))
+    value = bytes_step * args.steps / el / 1e9
+    ms = el * 1e3 / args.steps
+
+    # expert block alone, HIP events on the launch stream
+    n_ev = 200
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(n_ev)]
+    for i in range(n_ev):
+        route(i)
+        ev[i][0].record(stream)
+        experts(i)
+        ev[i][1].record(stream)
+    torch.cuda.synchronize()
+    durs = np.array([a.elapsed_time(z) for a, z in ev]) * 1e3  # us
+    kern_us = float(np.mean(durs))
+    achieved = bytes_step / (kern_us * 1e-6) / 1e9
+
+    out = {
+        "metric": "expert-FFN HBM GB/s (% of peak) + decode tokens/s at Qwen3-30B-A3B Q4_K_M",
+        "value": round(value, 2), "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(ms, 5), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "f32", "data": "synthetic",
+        "config": {"workload": "single MoE layer, one decode token, Qwen3-30B-A3B shape: D=2048 FF=768 128 experts "
+                               "top-8, gate/up Q4_K + down Q6_K (Q4_K_M), routing on device",
+                   "bytes_per_step": bytes_step, "layer_replicas": R, "hbm_resident_bytes": int(
+                       R * (gate.nbytes + up.nbytes + down.nbytes))},
+        "pct_of_hbm_peak": round(100 * value / HBM_PEAK_GBS, 2),
+        "expert_only_decode_tokens_per_s_48_layers": round(1.0 / (48 * ms * 1e-3), 1),
+        "roofline": {"bound": "hbm", "kernel": "expert block (moe_gate_up + moe_down)",
+                     "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "avg_us": round(kern_us, 3), "p10_us": round(float(np.percentile(durs, 10)), 3),
+                     "p90_us": round(float(np.percentile(durs, 90)), 3)},
+    }
+    if not args.no_cpu_baseline:
+        out["cpu_baseline"] = cpu_baseline(gate, up, down, xs, logits, args.cpu_seconds)
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,372 @@
+// capi.hip - the C ABI of libeahmmf_hip.so (include/eahmmf_hip.h).
+//
+// Per device the library keeps one non-blocking stream, device scratch for
+// activations/outputs and pinned host staging buffers, all grown on demand
+// and reused (the reference's wrappers keep the same kind of static scratch,
+// expert_cuda.cu:269-301, 363-392).  Synchronous entry points stage pageable
+// host data through the pinned buffers, enqueue copies and kernels on the
+// stream, and always drain the stream before returning, also after an error,
+// so a caller may release its expert leases as soon as the call returns.
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include <map>
+#include <mutex>
+#include <string>
+
+#include "../../include/eahmmf_hip.h"
+#include "internal.h"
+#include "kquant.h"
+
+using namespace eahmmf;
+
+namespace {
+
+thread_local std::string g_last_error;
+
+void set_error(const char* fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    g_last_error = buf;
+}
+
+bool hip_ok(hipError_t e, const char* what) {
+    if (e == hipSuccess) return true;
+    set_error("%s: %s (%d)", what, hipGetErrorString(e), (int)e);
+    return false;
+}
+
+struct DeviceBuf {
+    void* p = nullptr;
+    size_t cap = 0;
+};
+
+struct DevCtx {
+    hipStream_t stream = nullptr;
+    DeviceBuf dx, dy, dy2, dh, dids, dw;  // device scratch
+    DeviceBuf px, py, py2;                // pinned host staging
+};
+
+std::mutex g_mu;
+std::map<int, DevCtx> g_ctx;
+
+DevCtx* ctx_for_current_device() {
+    int dev = 0;
+    if (!hip_ok(hipGetDevice(&dev), "hipGetDevice")) return nullptr;
+    std::lock_guard<std::mutex> g(g_mu);
+    DevCtx& c = g_ctx[dev];
+    if (!c.stream && !hip_ok(hipStreamCreateWithFlags(&c.stream, hipStreamNonBlocking), "hipStreamCreate"))
+        return nullptr;
+    return &c;
+}
+
+bool grow_device(DeviceBuf& b, size_t need) {
+    if (need <= b.cap) return true;
+    if (b.p) (void)hipFree(b.p);
+    b.p = nullptr;
+    b.cap = 0;
+    size_t cap = need < 4096 ? 4096 : need;
+    if (!hip_ok(hipMalloc(&b.p, cap), "hipMalloc(scratch)")) return false;
+    b.cap = cap;
+    return true;
+}
+
+bool grow_pinned(DeviceBuf& b, size_t need) {
+    if (need <= b.cap) return true;
+    if (b.p) (void)hipHostFree(b.p);
+    b.p = nullptr;
+    b.cap = 0;
+    size_t cap = need < 4096 ? 4096 : need;
+    if (!hip_ok(hipHostMalloc(&b.p, cap, hipHostMallocDefault), "hipHostMalloc(staging)")) return false;
+    b.cap = cap;
+    return true;
+}
+
+// Drain the stream; a failure here also fails the call.
+bool drain(DevCtx* c, bool ok) {
+    const hipError_t e = hipStreamSynchronize(c->stream);
+    if (e != hipSuccess) {
+        set_error("hipStreamSynchronize: %s (%d)", hipGetErrorString(e), (int)e);
+        return false;
+    }
+    return ok;
+}
+
+bool matmul_args_ok(const uint8_t* w, int type, int ne0, int ne1, size_t row_bytes, int ldx, int ldo) {
+    if (!w) return set_error("null weight pointer"), false;
+    if (!type_supported(type)) return set_error("unsupported ggml type %d", type), false;
+    if (ne0 <= 0 || ne1 <= 0) return set_error("bad shape %d x %d", ne1, ne0), false;
+    if (ne0 % type_blck(type)) return set_error("ne0 %d not a multiple of the block size", ne0), false;
+    if (row_bytes != (size_t)(ne0 / type_blck(type)) * type_bytes(type))
+        return set_error("row_bytes %zu does not match type %d, ne0 %d", row_bytes, type, ne0), false;
+    if (ldx < ne0 || ldo < ne1) return set_error("ldx/ldo smaller than the row length"), false;
+    return true;
+}
+
+// host x[nb][ldx] (first ne0 of each row) -> device dense [nb][ne0]
+bool stage_x(DevCtx* c, const float* host_x, int nb, int ne0, int ldx) {
+    const size_t bytes = (size_t)nb * ne0 * sizeof(float);
+    if (!grow_pinned(c->px, bytes) || !grow_device(c->dx, bytes)) return false;
+    float* px = (float*)c->px.p;
+    for (int t = 0; t < nb; t++) memcpy(px + (size_t)t * ne0, host_x + (size_t)t * ldx, sizeof(float) * ne0);
+    return hip_ok(hipMemcpyAsync(c->dx.p, px, bytes, hipMemcpyHostToDevice, c->stream), "hipMemcpyAsync(x)");
+}
+
+void unstage_rows(const float* dense, int nb, int n, float* host, int ld) {
+    for (int t = 0; t < nb; t++) memcpy(host + (size_t)t * ld, dense + (size_t)t * n, sizeof(float) * n);
+}
+
+bool weight_ok(const eahmmf_hip_weight& w) { return w.dev && type_supported(w.type) && w.ne0 > 0 && w.ne1 > 0; }
+
+}  // namespace
+
+extern "C" {
+
+const char* eahmmf_hip_last_error(void) { return g_last_error.c_str(); }
+
+int eahmmf_hip_device_count(void) {
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess) return 0;
+    return n;
+}
+
+bool eahmmf_hip_matmul(const uint8_t* device_weights, int type, int ne0, int ne1, size_t row_bytes,
+                       const float* host_x, int nb, int ldx, float* host_out, int ldo) {
+    if (!host_x || !host_out || nb <= 0) return set_error("null host buffer or nb <= 0"), false;
+    if (!matmul_args_ok(device_weights, type, ne0, ne1, row_bytes, ldx, ldo)) return false;
+    DevCtx* c = ctx_for_current_device();
+    if (!c) return false;
+    const size_t obytes = (size_t)nb * ne1 * sizeof(float);
+    bool ok = grow_device(c->dy, obytes) && grow_pinned(c->py, obytes) && stage_x(c, host_x, nb, ne0, ldx);
+    if (ok) ok = hip_ok(launch_matmul(type, device_weights, ne0, ne1, row_bytes, (const float*)c->dx.p, nb, ne0,
+                                      (float*)c->dy.p, ne1, c->stream), "matmul launch");
+    if (ok) ok = hip_ok(hipMemcpyAsync(c->py.p, c->dy.p, obytes, hipMemcpyDeviceToHost, c->stream), "hipMemcpyAsync(out)");
+    ok = drain(c, ok);
+    if (ok) unstage_rows((const float*)c->py.p, nb, ne1, host_out, ldo);
+    return ok;
+}
+
+bool eahmmf_hip_matmul_pair(const uint8_t* gw, int gt, int gne0, int gne1, size_t grb,
+                            const uint8_t* uw, int ut, int une0, int une1, size_t urb,
+                            const float* host_x, int nb, int ldx,
+                            float* host_g, int ldg, float* host_u, int ldu) {
+    if (!host_x || !host_g || !host_u || nb <= 0) return set_error("null host buffer or nb <= 0"), false;
+    if (gne0 != une0 || gne1 != une1) return set_error("gate/up shape mismatch"), false;
+    if (!matmul_args_ok(gw, gt, gne0, gne1, grb, ldx, ldg) || !matmul_args_ok(uw, ut, une0, une1, urb, ldx, ldu))
+        return false;
+    DevCtx* c = ctx_for_current_device();
+    if (!c) return false;
+    const size_t obytes = (size_t)nb * gne1 * sizeof(float);
+    bool ok = grow_device(c->dy, obytes) && grow_device(c->dy2, obytes) && grow_pinned(c->py, obytes) &&
+              grow_pinned(c->py2, obytes) && stage_x(c, host_x, nb, gne0, ldx);
+    if (ok) ok = hip_ok(launch_matmul(gt, gw, gne0, gne1, grb, (const float*)c->dx.p, nb, gne0, (float*)c->dy.p, gne1,
+                                      c->stream), "gate launch");
+    if (ok) ok = hip_ok(launch_matmul(ut, uw, une0, une1, urb, (const float*)c->dx.p, nb, une0, (float*)c->dy2.p,
+                                      une1, c->stream), "up launch");
+    if (ok) ok = hip_ok(hipMemcpyAsync(c->py.p, c->dy.p, obytes, hipMemcpyDeviceToHost, c->stream), "copy g");
+    if (ok) ok = hip_ok(hipMemcpyAsync(c->py2.p, c->dy2.p, obytes, hipMemcpyDeviceToHost, c->stream), "copy u");
+    ok = drain(c, ok);
+    if (ok) {
+        unstage_rows((const float*)c->py.p, nb, gne1, host_g, ldg);
+        unstage_rows((const float*)c->py2.p, nb, une1, host_u, ldu);
+    }
+    return ok;
+}
+
+bool eahmmf_hip_moe_decode(const eahmmf_hip_expert* experts, const float* w, int k, const float* host_x,
+                           float* host_y) {
+    if (!experts || !w || !host_x || !host_y) return set_error("null argument"), false;
+    if (k <= 0 || k > kMaxSlots) return set_error("k=%d outside 1..%d", k, kMaxSlots), false;
+    const eahmmf_hip_expert& e0 = experts[0];
+    MoeShape s{};
+    s.gate_type = e0.gate.type;
+    s.up_type = e0.up.type;
+    s.down_type = e0.down.type;
+    s.D = e0.gate.ne0;
+    s.FF = e0.gate.ne1;
+    s.gate_rb = e0.gate.row_bytes;
+    s.up_rb = e0.up.row_bytes;
+    s.down_rb = e0.down.row_bytes;
+    DecodeSlots slots{};
+    slots.k = k;
+    for (int j = 0; j < k; j++) {
+        const eahmmf_hip_expert& e = experts[j];
+        if (!weight_ok(e.gate) || !weight_ok(e.up) || !weight_ok(e.down))
+            return set_error("expert slot %d: missing device pointer or unsupported type", j), false;
+        if (e.gate.type != s.gate_type || e.up.type != s.up_type || e.down.type != s.down_type ||
+            e.gate.ne0 != s.D || e.gate.ne1 != s.FF || e.up.ne0 != s.D || e.up.ne1 != s.FF || e.down.ne0 != s.FF ||
+            e.down.ne1 != s.D || e.gate.row_bytes != s.gate_rb || e.up.row_bytes != s.up_rb ||
+            e.down.row_bytes != s.down_rb)
+            return set_error("expert slot %d: shape/type differs from slot 0", j), false;
+        slots.gate[j] = e.gate.dev;
+        slots.up[j] = e.up.dev;
+        slots.down[j] = e.down.dev;
+        slots.w[j] = w[j];
+    }
+    if (!moe_shape_ok(s)) return set_error("unsupported expert shape/type combination"), false;
+    DevCtx* c = ctx_for_current_device();
+    if (!c) return false;
+    const size_t ybytes = (size_t)s.D * sizeof(float);
+    bool ok = grow_device(c->dy, ybytes) && grow_pinned(c->py, ybytes) &&
+              grow_device(c->dh, (size_t)k * s.FF * sizeof(float)) && stage_x(c, host_x, 1, s.D, s.D);
+    if (ok) ok = hip_ok(launch_moe_decode(s, slots, (const float*)c->dx.p, (float*)c->dh.p, (float*)c->dy.p, c->stream),
+                        "moe decode launch");
+    if (ok) ok = hip_ok(hipMemcpyAsync(c->py.p, c->dy.p, ybytes, hipMemcpyDeviceToHost, c->stream), "copy y");
+    ok = drain(c, ok);
+    if (ok) memcpy(host_y, c->py.p, ybytes);
+    return ok;
+}
+
+static bool shape_from_abi(const eahmmf_hip_moe_shape* sh, MoeShape& s) {
+    if (!sh) return set_error("null shape"), false;
+    s.gate_type = sh->gate_type;
+    s.up_type = sh->up_type;
+    s.down_type = sh->down_type;
+    s.D = sh->D;
+    s.FF = sh->FF;
+    s.gate_rb = sh->gate_row_bytes;
+    s.up_rb = sh->up_row_bytes;
+    s.down_rb = sh->down_row_bytes;
+    if (!moe_shape_ok(s)) return set_error("unsupported expert shape/type combination"), false;
+    return true;
+}
+
+int eahmmf_hip_moe_decode_async(const eahmmf_hip_moe_shape* shape, const eahmmf_hip_expert_ptrs* experts,
+                                const float* w, int k, const float* dev_x, float* dev_y, void* stream) {
+    MoeShape s{};
+    if (!shape_from_abi(shape, s)) return -1;
+    if (!experts || !w || !dev_x || !dev_y) return set_error("null argument"), -1;
+    if (k <= 0 || k > kMaxSlots) return set_error("k=%d outside 1..%d", k, kMaxSlots), -1;
+    DecodeSlots slots{};
+    slots.k = k;
+    for (int j = 0; j < k; j++) {
+        if (!experts[j].gate || !experts[j].up || !experts[j].down)
+            return set_error("expert slot %d has a null pointer", j), -1;
+        slots.gate[j] = experts[j].gate;
+        slots.up[j] = experts[j].up;
+        slots.down[j] = experts[j].down;
+        slots.w[j] = w[j];
+    }
+    DevCtx* c = ctx_for_current_device();
+    if (!c) return -2;
+    if (!grow_device(c->dh, (size_t)k * s.FF * sizeof(float))) return -2;
+    if (!hip_ok(launch_moe_decode(s, slots, dev_x, (float*)c->dh.p, dev_y, (hipStream_t)stream), "moe decode launch"))
+        return -3;
+    return 0;
+}
+
+int eahmmf_hip_moe_decode_routed_async(const eahmmf_hip_moe_shape* shape, const eahmmf_hip_expert_ptrs* dev_table,
+                                       int n_expert, const int* dev_ids, const float* dev_w, int k,
+                                       const float* dev_x, float* dev_y, void* stream) {
+    MoeShape s{};
+    if (!shape_from_abi(shape, s)) return -1;
+    if (!dev_table || !dev_ids || !dev_w || !dev_x || !dev_y || n_expert <= 0)
+        return set_error("null argument"), -1;
+    if (k <= 0 || k > kMaxSlots) return set_error("k=%d outside 1..%d", k, kMaxSlots), -1;
+    DevCtx* c = ctx_for_current_device();
+    if (!c) return -2;
+    if (!grow_device(c->dh, (size_t)k * s.FF * sizeof(float))) return -2;
+    if (!hip_ok(launch_moe_decode_routed(s, (const ExpertEntry*)dev_table, n_expert, dev_ids, dev_w, k, dev_x,
+                                         (float*)c->dh.p, dev_y, (hipStream_t)stream),
+                "routed moe decode launch"))
+        return -3;
+    return 0;
+}
+
+bool eahmmf_hip_route_topk(const float* host_logits, int nb, int n_expert, int k, int* host_ids, float* host_w) {
+    if (!host_logits || !host_ids || !host_w) return set_error("null argument"), false;
+    if (nb <= 0 || n_expert <= 0 || n_expert > 512 || k <= 0 || k > kMaxSlots || k > n_expert)
+        return set_error("bad routing shape nb=%d n_expert=%d k=%d", nb, n_expert, k), false;
+    DevCtx* c = ctx_for_current_device();
+    if (!c) return false;
+    const size_t out = (size_t)nb * k;
+    bool ok = grow_device(c->dids, out * sizeof(int)) && grow_device(c->dw, out * sizeof(float)) &&
+              grow_pinned(c->py, out * sizeof(int)) && grow_pinned(c->py2, out * sizeof(float)) &&
+              stage_x(c, host_logits, nb, n_expert, n_expert);
+    if (ok) ok = hip_ok(launch_route_topk((const float*)c->dx.p, nb, n_expert, k, (int*)c->dids.p, (float*)c->dw.p,
+                                          c->stream), "route launch");
+    if (ok) ok = hip_ok(hipMemcpyAsync(c->py.p, c->dids.p, out * sizeof(int), hipMemcpyDeviceToHost, c->stream), "copy ids");
+    if (ok) ok = hip_ok(hipMemcpyAsync(c->py2.p, c->dw.p, out * sizeof(float), hipMemcpyDeviceToHost, c->stream), "copy w");
+    ok = drain(c, ok);
+    if (ok) {
+        memcpy(host_ids, c->py.p, out * sizeof(int));
+        memcpy(host_w, c->py2.p, out * sizeof(float));
+    }
+    return ok;
+}
+
+int eahmmf_hip_route_topk_async(const float* dev_logits, int nb, int n_expert, int k, int* dev_ids, float* dev_w,
+                                void* stream) {
+    if (!dev_logits || !dev_ids || !dev_w) return set_error("null argument"), -1;
+    const hipError_t e = launch_route_topk(dev_logits, nb, n_expert, k, dev_ids, dev_w, (hipStream_t)stream);
+    if (e == hipErrorInvalidValue) return set_error("bad routing shape nb=%d n_expert=%d k=%d", nb, n_expert, k), -1;
+    return hip_ok(e, "route launch") ? 0 : -3;
+}
+
+int eahmmf_hip_dequantize(const uint8_t* dev_w, int type, int64_t ne0, int64_t nrows, size_t row_bytes,
+                          float* dev_out, void* stream) {
+    if (!dev_w || !dev_out || nrows < 0) return set_error("null argument"), -1;
+    if (!(type_supported(type) || type == kF32)) return set_error("unsupported ggml type %d", type), -1;
+    if (ne0 <= 0 || ne0 % type_blck(type)) return set_error("bad row length %lld", (long long)ne0), -1;
+    if (row_bytes != (size_t)(ne0 / type_blck(type)) * type_bytes(type)) return set_error("row_bytes mismatch"), -1;
+    return hip_ok(launch_dequant(type, dev_w, ne0, nrows, row_bytes, dev_out, (hipStream_t)stream), "dequant launch")
+               ? 0
+               : -3;
+}
+
+int eahmmf_hip_alloc(void** dev_ptr, size_t bytes) {
+    if (!dev_ptr) return set_error("null argument"), -1;
+    *dev_ptr = nullptr;
+    return hip_ok(hipMalloc(dev_ptr, bytes), "hipMalloc") ? 0 : -2;
+}
+
+int eahmmf_hip_free(void* dev_ptr) { return hip_ok(hipFree(dev_ptr), "hipFree") ? 0 : -2; }
+
+int eahmmf_hip_h2d(void* dev_dst, const void* host_src, size_t n) {
+    DevCtx* c = ctx_for_current_device();
+    if (!c) return -2;
+    return hip_ok(hipMemcpyAsync(dev_dst, host_src, n, hipMemcpyHostToDevice, c->stream), "h2d") ? 0 : -2;
+}
+
+int eahmmf_hip_d2h(void* host_dst, const void* dev_src, size_t n) {
+    DevCtx* c = ctx_for_current_device();
+    if (!c) return -2;
+    bool ok = hip_ok(hipMemcpyAsync(host_dst, dev_src, n, hipMemcpyDeviceToHost, c->stream), "d2h");
+    return drain(c, ok) ? 0 : -2;
+}
+
+int eahmmf_hip_sync(void) {
+    DevCtx* c = ctx_for_current_device();
+    if (!c) return -2;
+    return drain(c, true) ? 0 : -2;
+}
+
+int eahmmf_hip_mem_info(size_t* free_bytes, size_t* total_bytes) {
+    size_t f = 0, t = 0;
+    if (!hip_ok(hipMemGetInfo(&f, &t), "hipMemGetInfo")) return -2;
+    if (free_bytes) *free_bytes = f;
+    if (total_bytes) *total_bytes = t;
+    return 0;
+}
+
+void eahmmf_hip_shutdown(void) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return;
+    std::lock_guard<std::mutex> g(g_mu);
+    auto it = g_ctx.find(dev);
+    if (it == g_ctx.end()) return;
+    DevCtx& c = it->second;
+    if (c.stream) (void)hipStreamSynchronize(c.stream);
+    for (DeviceBuf* b : {&c.dx, &c.dy, &c.dy2, &c.dh, &c.dids, &c.dw})
+        if (b->p) (void)hipFree(b->p);
+    for (DeviceBuf* b : {&c.px, &c.py, &c.py2})
+        if (b->p) (void)hipHostFree(b->p);
+    if (c.stream) (void)hipStreamDestroy(c.stream);
+    g_ctx.erase(it);
+}
+
+}  // extern "C"

@@ -1,0 +1,52 @@
+// internal.h - launchers shared between the kernel files and the C ABI.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace eahmmf {
+
+constexpr int kMaxSlots = 16;  // routed experts per token handled by one fused launch
+
+// Shape of one MoE layer's expert components (all experts of a layer share it).
+struct MoeShape {
+    int gate_type, up_type, down_type;
+    int D, FF;
+    size_t gate_rb, up_rb, down_rb;  // row bytes
+};
+
+// The k routed experts of one token, by value in the kernel arguments.
+struct DecodeSlots {
+    const uint8_t* gate[kMaxSlots];
+    const uint8_t* up[kMaxSlots];
+    const uint8_t* down[kMaxSlots];
+    float w[kMaxSlots];
+    int k;
+};
+
+// Device-resident per-layer table, one entry per expert id (for routed launches).
+struct ExpertEntry {
+    const uint8_t* gate;
+    const uint8_t* up;
+    const uint8_t* down;
+};
+
+hipError_t launch_dequant(int type, const uint8_t* w, int64_t ne0, int64_t nrows, size_t row_bytes, float* out,
+                          hipStream_t st);
+hipError_t launch_matmul(int type, const uint8_t* w, int ne0, int ne1, size_t row_bytes, const float* x, int nb,
+                         int ldx, float* out, int ldo, hipStream_t st);
+
+// Fused single-token decode: h[k][FF] scratch, y[D] = sum_j w_j down_j(silu(gate_j x) * up_j x).
+hipError_t launch_moe_decode(const MoeShape& s, const DecodeSlots& slots, const float* x, float* h, float* y,
+                             hipStream_t st);
+// Same with the routing taken from device memory: ids/w [k], table [n_expert].
+hipError_t launch_moe_decode_routed(const MoeShape& s, const ExpertEntry* table, int n_expert, const int* ids,
+                                    const float* w, int k, const float* x, float* h, float* y, hipStream_t st);
+
+// softmax -> top-k (e desc, index asc) -> renormalise; logits [nb][n_expert].
+hipError_t launch_route_topk(const float* logits, int nb, int n_expert, int k, int* ids, float* w, hipStream_t st);
+
+bool moe_shape_ok(const MoeShape& s);
+bool type_supported(int t);
+
+}  // namespace eahmmf

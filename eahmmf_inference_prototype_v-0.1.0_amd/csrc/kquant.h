@@ -1,0 +1,182 @@
+// kquant.h - device-side decoding of the GGML block formats used by MoE
+// expert weights on gfx950: Q8_0 (type 8), Q4_K (12), Q5_K (13), Q6_K (14),
+// plus F32 (0) for router matrices.
+//
+// Byte layouts and value formulas follow the reference CPU decoder
+// (qwen3moe.cpp:128-202) so that dequantized values are bit-identical:
+//   Q8_0  y = d*q                                  (34 B / 32 values)
+//   Q4_K  y = fma(d*sc, q, -(dmin*m))              (144 B / 256 values)
+//   Q5_K  y = fma(d*sc, q + 16*hbit, -(dmin*m))    (176 B / 256 values)
+//   Q6_K  y = (d*sc)*q                             (210 B / 256 values)
+// The FMA in Q4_K/Q5_K is the single rounding the reference binary performs
+// after GCC contracts `d1 * q - m1` under its -O3 -march=native build.
+//
+// The unit of work is a 32-value "segment":
+//   Q4_K/Q5_K  sub-block j of a super-block (its own 6-bit scale and min)
+//   Q6_K       quarter u of half n (two 16-value int8 scales)
+//   Q8_0       one block
+//   F32        32 consecutive floats
+// Super-blocks are read in place with 16-byte loads; Q6_K and Q8_0 blocks sit
+// at 2-byte alignment and are read through 2-byte-aligned packed structs (the
+// amdhsa target runs in unaligned-access mode, so these stay single vector
+// loads).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace eahmmf {
+
+enum : int { kF32 = 0, kQ8_0 = 8, kQ4_K = 12, kQ5_K = 13, kQ6_K = 14 };
+
+template <int T> struct Fmt;
+template <> struct Fmt<kF32>  { static constexpr int blck = 32,  bytes = 128, segs = 1; };
+template <> struct Fmt<kQ8_0> { static constexpr int blck = 32,  bytes = 34,  segs = 1; };
+template <> struct Fmt<kQ4_K> { static constexpr int blck = 256, bytes = 144, segs = 8; };
+template <> struct Fmt<kQ5_K> { static constexpr int blck = 256, bytes = 176, segs = 8; };
+template <> struct Fmt<kQ6_K> { static constexpr int blck = 256, bytes = 210, segs = 8; };
+
+__host__ __device__ inline int type_blck(int t) {
+    return t == kQ4_K || t == kQ5_K || t == kQ6_K ? 256 : (t == kQ8_0 || t == kF32 ? 32 : 0);
+}
+__host__ __device__ inline int type_bytes(int t) {
+    switch (t) {
+        case kF32: return 128;
+        case kQ8_0: return 34;
+        case kQ4_K: return 144;
+        case kQ5_K: return 176;
+        case kQ6_K: return 210;
+        default: return 0;
+    }
+}
+
+struct __attribute__((packed, aligned(2))) Bytes16A2 { uint32_t w[4]; };
+struct __attribute__((packed, aligned(2))) Bytes32A2 { uint32_t w[8]; };
+
+__device__ __forceinline__ uint4 ld16(const uint8_t* p) {  // 16-byte aligned
+    return *reinterpret_cast<const uint4*>(p);
+}
+__device__ __forceinline__ Bytes32A2 ld32_a2(const uint8_t* p) {  // 2-byte aligned
+    return *reinterpret_cast<const Bytes32A2*>(p);
+}
+__device__ __forceinline__ uint16_t ld_u16(const uint8_t* p) {
+    return *reinterpret_cast<const uint16_t*>(p);
+}
+
+// Exact half -> float.  Finite values and infinities convert exactly in
+// hardware; NaN is canonicalised (sign kept) as the reference's table does
+// (qwen3moe.cpp:59).
+__device__ __forceinline__ float half_to_float(uint32_t h) {
+    float v = (float)__builtin_bit_cast(_Float16, (uint16_t)h);
+    if ((h & 0x7C00u) == 0x7C00u && (h & 0x3FFu)) v = __builtin_bit_cast(float, 0x7FC00000u | ((h & 0x8000u) << 16));
+    return v;
+}
+
+__device__ __forceinline__ uint32_t byte_of(uint32_t w, int i) { return (w >> (8 * i)) & 0xFFu; }
+
+// 12 scale bytes held in three words -> 6-bit (scale, min) of sub-block j
+// (qwen3moe.cpp:133-141).
+__device__ __forceinline__ void scale_min_k4(int j, uint32_t s0, uint32_t s1, uint32_t s2, uint32_t& sc, uint32_t& mn) {
+    // bytes q[0..3] = s0, q[4..7] = s1, q[8..11] = s2
+    if (j < 4) {
+        sc = byte_of(s0, j) & 63u;
+        mn = byte_of(s1, j) & 63u;
+    } else {
+        const uint32_t qj4 = byte_of(s2, j - 4);   // q[j+4]
+        const uint32_t qjm4 = byte_of(s0, j - 4);  // q[j-4]
+        const uint32_t qj = byte_of(s1, j - 4);    // q[j]
+        sc = (qj4 & 15u) | ((qjm4 >> 6) << 4);
+        mn = (qj4 >> 4) | ((qj >> 6) << 4);
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Segment decoders: 32 dequantized values, bit-identical to the reference.
+// `blk` points at the block (super-block) start; `j` is the segment in it.
+
+__device__ __forceinline__ void decode_seg_q4k(const uint8_t* blk, int j, float* w) {
+    const uint4 hdr = ld16(blk);
+    const float d = half_to_float(hdr.x & 0xFFFFu), dmin = half_to_float(hdr.x >> 16);
+    uint32_t sc, mn;
+    scale_min_k4(j, hdr.y, hdr.z, hdr.w, sc, mn);
+    const float ds = d * (float)sc, dm = dmin * (float)mn;
+    const int g = j >> 1, sh = (j & 1) * 4;
+    const uint4 a = ld16(blk + 16 + 32 * g), b = ld16(blk + 32 + 32 * g);
+    const uint32_t q[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+    for (int i = 0; i < 32; i++) {
+        const uint32_t v = (q[i >> 2] >> (8 * (i & 3) + sh)) & 15u;
+        w[i] = __builtin_fmaf(ds, (float)v, -dm);
+    }
+}
+
+__device__ __forceinline__ void decode_seg_q5k(const uint8_t* blk, int j, float* w) {
+    const uint4 hdr = ld16(blk);
+    const float d = half_to_float(hdr.x & 0xFFFFu), dmin = half_to_float(hdr.x >> 16);
+    uint32_t sc, mn;
+    scale_min_k4(j, hdr.y, hdr.z, hdr.w, sc, mn);
+    const float ds = d * (float)sc, dm = dmin * (float)mn;
+    const int g = j >> 1, sh = (j & 1) * 4;
+    const uint4 h0 = ld16(blk + 16), h1 = ld16(blk + 32);
+    const uint4 a = ld16(blk + 48 + 32 * g), b = ld16(blk + 64 + 32 * g);
+    const uint32_t q[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+    const uint32_t qh[8] = {h0.x, h0.y, h0.z, h0.w, h1.x, h1.y, h1.z, h1.w};
+#pragma unroll
+    for (int i = 0; i < 32; i++) {
+        uint32_t v = (q[i >> 2] >> (8 * (i & 3) + sh)) & 15u;
+        v |= ((qh[i >> 2] >> (8 * (i & 3) + j)) & 1u) << 4;
+        w[i] = __builtin_fmaf(ds, (float)v, -dm);
+    }
+}
+
+__device__ __forceinline__ void decode_seg_q6k(const uint8_t* blk, int j, float* w) {
+    const int n = j >> 2, u = j & 3;
+    const float d = half_to_float(ld_u16(blk + 208));
+    const Bytes32A2 lo = ld32_a2(blk + 64 * n + 32 * (u & 1));
+    const Bytes32A2 hi = ld32_a2(blk + 128 + 32 * n);
+    const uint16_t scw = ld_u16(blk + 192 + 8 * n + 2 * u);  // scales for l<16 and l>=16
+    const float ds0 = d * (float)(int8_t)(scw & 0xFFu);
+    const float ds1 = d * (float)(int8_t)(scw >> 8);
+    const int shl = (u >> 1) * 4, shh = 2 * u;
+#pragma unroll
+    for (int i = 0; i < 32; i++) {
+        const uint32_t l4 = (lo.w[i >> 2] >> (8 * (i & 3) + shl)) & 15u;
+        const uint32_t h2 = (hi.w[i >> 2] >> (8 * (i & 3) + shh)) & 3u;
+        const int q = (int)(l4 | (h2 << 4)) - 32;
+        w[i] = (i < 16 ? ds0 : ds1) * (float)q;
+    }
+}
+
+__device__ __forceinline__ void decode_seg_q8_0(const uint8_t* blk, float* w) {
+    const float d = half_to_float(ld_u16(blk));
+    const Bytes32A2 q = ld32_a2(blk + 2);
+#pragma unroll
+    for (int i = 0; i < 32; i++) w[i] = d * (float)(int8_t)byte_of(q.w[i >> 2], i & 3);
+}
+
+__device__ __forceinline__ void decode_seg_f32(const uint8_t* blk, float* w) {
+    const float4* p = reinterpret_cast<const float4*>(blk);
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        const float4 v = p[i];
+        w[4 * i] = v.x; w[4 * i + 1] = v.y; w[4 * i + 2] = v.z; w[4 * i + 3] = v.w;
+    }
+}
+
+// Segment s (0-based, 32 values each) of a row.
+template <int T>
+__device__ __forceinline__ void decode_row_seg(const uint8_t* row, int s, float* w) {
+    if constexpr (T == kQ4_K) decode_seg_q4k(row + (size_t)(s >> 3) * 144, s & 7, w);
+    else if constexpr (T == kQ5_K) decode_seg_q5k(row + (size_t)(s >> 3) * 176, s & 7, w);
+    else if constexpr (T == kQ6_K) decode_seg_q6k(row + (size_t)(s >> 3) * 210, s & 7, w);
+    else if constexpr (T == kQ8_0) decode_seg_q8_0(row + (size_t)s * 34, w);
+    else decode_seg_f32(row + (size_t)s * 128, w);
+}
+
+// Wave-wide float sum (wave64); every lane receives the total.
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+    return v;
+}
+
+}  // namespace eahmmf

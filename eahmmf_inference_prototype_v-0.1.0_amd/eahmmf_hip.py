@@ -1,0 +1,115 @@
+"""ctypes binding of libeahmmf_hip.so (the C ABI in include/eahmmf_hip.h).
+
+This is the Python view of the same entry points a C++ host (the reference's
+qwen3moe.cpp) binds with ``extern "C"`` declarations.  It adds nothing to the
+compute path: every call goes straight to the HIP library, and importing this
+module fails loudly when the library has not been built.
+"""
+import ctypes
+import os
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "libeahmmf_hip.so")
+
+GGML_F32, GGML_Q8_0, GGML_Q4_K, GGML_Q5_K, GGML_Q6_K = 0, 8, 12, 13, 14
+BLOCK = {GGML_F32: (32, 128), GGML_Q8_0: (32, 34), GGML_Q4_K: (256, 144), GGML_Q5_K: (256, 176), GGML_Q6_K: (256, 210)}
+MAX_TOPK = 16
+
+# Every symbol declared in include/eahmmf_hip.h.
+EXPORTS = (
+    "eahmmf_hip_matmul", "eahmmf_hip_matmul_pair", "eahmmf_hip_moe_decode", "eahmmf_hip_moe_decode_async",
+    "eahmmf_hip_moe_decode_routed_async", "eahmmf_hip_route_topk", "eahmmf_hip_route_topk_async",
+    "eahmmf_hip_dequantize", "eahmmf_hip_row_bytes", "eahmmf_hip_quantize_rows", "eahmmf_hip_alloc",
+    "eahmmf_hip_free", "eahmmf_hip_h2d", "eahmmf_hip_d2h", "eahmmf_hip_sync", "eahmmf_hip_mem_info",
+    "eahmmf_hip_last_error", "eahmmf_hip_device_count", "eahmmf_hip_shutdown",
+)
+
+
+class Weight(ctypes.Structure):
+    _fields_ = [("dev", ctypes.c_void_p), ("type", ctypes.c_int), ("ne0", ctypes.c_int), ("ne1", ctypes.c_int),
+                ("row_bytes", ctypes.c_size_t)]
+
+
+class Expert(ctypes.Structure):
+    _fields_ = [("gate", Weight), ("up", Weight), ("down", Weight)]
+
+
+class ExpertPtrs(ctypes.Structure):
+    _fields_ = [("gate", ctypes.c_void_p), ("up", ctypes.c_void_p), ("down", ctypes.c_void_p)]
+
+
+class MoeShape(ctypes.Structure):
+    _fields_ = [("gate_type", ctypes.c_int), ("up_type", ctypes.c_int), ("down_type", ctypes.c_int),
+                ("D", ctypes.c_int), ("FF", ctypes.c_int), ("gate_row_bytes", ctypes.c_size_t),
+                ("up_row_bytes", ctypes.c_size_t), ("down_row_bytes", ctypes.c_size_t)]
+
+
+def row_bytes(gtype, ne0):
+    blck, nbytes = BLOCK[gtype]
+    if ne0 % blck:
+        raise ValueError(f"row length {ne0} is not a multiple of {blck}")
+    return ne0 // blck * nbytes
+
+
+def load(path=LIB_PATH):
+    """Load the library and declare its signatures.  Raises if it is missing."""
+    if not os.path.exists(path):
+        raise RuntimeError(f"{path} is not built; run __graft_entry__.build() (make -C the package)")
+    lib = ctypes.CDLL(path)
+    c_bool, c_int, c_sz, c_i64, vp = ctypes.c_bool, ctypes.c_int, ctypes.c_size_t, ctypes.c_int64, ctypes.c_void_p
+    sig = {
+        "eahmmf_hip_matmul": (c_bool, [vp, c_int, c_int, c_int, c_sz, vp, c_int, c_int, vp, c_int]),
+        "eahmmf_hip_matmul_pair": (c_bool, [vp, c_int, c_int, c_int, c_sz, vp, c_int, c_int, c_int, c_sz,
+                                            vp, c_int, c_int, vp, c_int, vp, c_int]),
+        "eahmmf_hip_moe_decode": (c_bool, [ctypes.POINTER(Expert), vp, c_int, vp, vp]),
+        "eahmmf_hip_moe_decode_async": (c_int, [ctypes.POINTER(MoeShape), ctypes.POINTER(ExpertPtrs), vp, c_int,
+                                                vp, vp, vp]),
+        "eahmmf_hip_moe_decode_routed_async": (c_int, [ctypes.POINTER(MoeShape), vp, c_int, vp, vp, c_int, vp, vp,
+                                                       vp]),
+        "eahmmf_hip_route_topk": (c_bool, [vp, c_int, c_int, c_int, vp, vp]),
+        "eahmmf_hip_route_topk_async": (c_int, [vp, c_int, c_int, c_int, vp, vp, vp]),
+        "eahmmf_hip_dequantize": (c_int, [vp, c_int, c_i64, c_i64, c_sz, vp, vp]),
+        "eahmmf_hip_row_bytes": (c_sz, [c_int, c_i64]),
+        "eahmmf_hip_quantize_rows": (c_i64, [c_int, vp, c_i64, c_i64, vp]),
+        "eahmmf_hip_alloc": (c_int, [ctypes.POINTER(vp), c_sz]),
+        "eahmmf_hip_free": (c_int, [vp]),
+        "eahmmf_hip_h2d": (c_int, [vp, vp, c_sz]),
+        "eahmmf_hip_d2h": (c_int, [vp, vp, c_sz]),
+        "eahmmf_hip_sync": (c_int, []),
+        "eahmmf_hip_mem_info": (c_int, [ctypes.POINTER(c_sz), ctypes.POINTER(c_sz)]),
+        "eahmmf_hip_last_error": (ctypes.c_char_p, []),
+        "eahmmf_hip_device_count": (c_int, []),
+        "eahmmf_hip_shutdown": (None, []),
+    }
+    for name, (res, args) in sig.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    return lib
+
+
+_lib = None
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        _lib = load()
+    return _lib
+
+
+def last_error():
+    return lib().eahmmf_hip_last_error().decode()
+
+
+def quantize_rows(gtype, src):
+    """fp32 [nrows][ne0] (numpy) -> uint8 [nrows][row_bytes] via the library's host quantizer."""
+    import numpy as np
+    src = np.ascontiguousarray(src, dtype=np.float32)
+    nrows, ne0 = src.shape
+    rb = row_bytes(gtype, ne0)
+    out = np.empty((nrows, rb), dtype=np.uint8)
+    n = lib().eahmmf_hip_quantize_rows(gtype, src.ctypes.data, nrows, ne0, out.ctypes.data)
+    if n != nrows * rb:
+        raise RuntimeError(f"quantize_rows failed: {last_error()}")
+    return out

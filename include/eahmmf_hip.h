@@ -1,0 +1,145 @@
+/*
+ * eahmmf_hip.h - C ABI of the MI355X (gfx950) expert-FFN library,
+ * libeahmmf_hip.so.
+ *
+ * Plain pointers and sizes only.  "device" pointers are HIP device memory on
+ * the current device (hipSetDevice / the caller's choice), "host" pointers are
+ * ordinary pageable host memory.  Weight pointers address row 0 of one expert
+ * component; rows are contiguous at stride row_bytes (the GGUF layout, bytes
+ * never repacked).  Supported ggml types: 8 (Q8_0), 12 (Q4_K), 13 (Q5_K),
+ * 14 (Q6_K).
+ *
+ * Error convention (same as the reference's CUDA C ABI): the bool entry points
+ * return false on invalid arguments or any HIP error and never abort; queued
+ * work is drained before returning, even after an error.  The int entry points
+ * return 0 on success and a negative code otherwise.  eahmmf_hip_last_error()
+ * describes the most recent failure on the calling thread.
+ *
+ * Threading: like the reference's ABI, one caller thread per device is
+ * assumed; each device has one internal stream and one set of scratch and
+ * pinned staging buffers that grow on demand and are kept until
+ * eahmmf_hip_shutdown().
+ */
+#ifndef EAHMMF_HIP_H
+#define EAHMMF_HIP_H
+#include <stdbool.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- drop-in replacements for the reference's CUDA C ABI -------------- */
+
+/* out[t*ldo + r] = sum_k W[r,k] * x[t*ldx + k], r < ne1, t < nb; host x/out,
+ * synchronous.  Only r < ne1 of each output row is written.
+ * Replaces eahmmf_cuda_matmul (expert_cuda.cu:251-261, declared
+ * qwen3moe.cpp:422-423, called by gpu_matmul qwen3moe.cpp:471-474). */
+bool eahmmf_hip_matmul(const uint8_t* device_weights, int type, int ne0, int ne1, size_t row_bytes,
+                       const float* host_x, int nb, int ldx, float* host_out, int ldo);
+
+/* Gate and up projections of one expert sharing one input transfer and one
+ * synchronisation.  Requires equal (ne0, ne1).  Replaces
+ * eahmmf_cuda_matmul_pair (expert_cuda.cu:344-348, declared qwen3moe.cpp:424,
+ * called by gpu_matmul_pair qwen3moe.cpp:476-491). */
+bool eahmmf_hip_matmul_pair(const uint8_t* gw, int gt, int gne0, int gne1, size_t grb,
+                            const uint8_t* uw, int ut, int une0, int une1, size_t urb,
+                            const float* host_x, int nb, int ldx,
+                            float* host_g, int ldg, float* host_u, int ldu);
+
+/* ---- fused MoE expert block (additions, same conventions) ------------- */
+
+/* One expert component as the kernels see it: the device fields of the
+ * reference's WeightView (eahmmf.h:54-62). */
+typedef struct {
+    const uint8_t* dev;
+    int type;
+    int ne0, ne1;
+    size_t row_bytes;
+} eahmmf_hip_weight;
+
+/* One routed expert: its three leased components (ExpertViews, eahmmf.h:263-267). */
+typedef struct {
+    eahmmf_hip_weight gate, up, down;
+} eahmmf_hip_expert;
+
+/* Device-resident table entry, one per expert id of a layer. */
+typedef struct {
+    const uint8_t* gate;
+    const uint8_t* up;
+    const uint8_t* down;
+} eahmmf_hip_expert_ptrs;
+
+/* Shape of a layer's experts: gate/up are FF x D (ne0 = D), down is D x FF. */
+typedef struct {
+    int gate_type, up_type, down_type;
+    int D, FF;
+    size_t gate_row_bytes, up_row_bytes, down_row_bytes;
+} eahmmf_hip_moe_shape;
+
+/* Maximum routed experts per token in one fused call. */
+#define EAHMMF_HIP_MAX_TOPK 16
+
+/* Single-token expert block, synchronous, host x[D] -> host y[D]:
+ *   y = sum_j w[j] * down_j( silu(gate_j x) * (up_j x) ).
+ * All k experts must share one shape.  The caller holds the k leases across
+ * the call.  Replaces the per-expert loop of qwen3moe.cpp:1024-1067 for one
+ * token (gate/up pair, SiLU, down, weighted sum). */
+bool eahmmf_hip_moe_decode(const eahmmf_hip_expert* experts, const float* w, int k,
+                           const float* host_x, float* host_y);
+
+/* Same on device buffers, asynchronous on `stream` (a hipStream_t, 0 for the
+ * null stream).  experts/w are read on the host during the call. */
+int eahmmf_hip_moe_decode_async(const eahmmf_hip_moe_shape* shape, const eahmmf_hip_expert_ptrs* experts,
+                                const float* w, int k, const float* dev_x, float* dev_y, void* stream);
+
+/* Routed variant: routing results and the expert table live on the device
+ * (dev_table [n_expert], dev_ids/dev_w [k]); no host round trip between
+ * routing and the expert block. */
+int eahmmf_hip_moe_decode_routed_async(const eahmmf_hip_moe_shape* shape, const eahmmf_hip_expert_ptrs* dev_table,
+                                       int n_expert, const int* dev_ids, const float* dev_w, int k,
+                                       const float* dev_x, float* dev_y, void* stream);
+
+/* Softmax -> top-k -> renormalise (qwen3moe.cpp:1011-1023), synchronous on
+ * host buffers: logits[nb][n_expert] -> ids[nb][k], w[nb][k] in rank order
+ * (e = expf(l - max) descending, lower id first on ties). */
+bool eahmmf_hip_route_topk(const float* host_logits, int nb, int n_expert, int k, int* host_ids, float* host_w);
+int eahmmf_hip_route_topk_async(const float* dev_logits, int nb, int n_expert, int k, int* dev_ids, float* dev_w,
+                                void* stream);
+
+/* ---- format utilities ------------------------------------------------- */
+
+/* Dequantize nrows rows of ne0 values into dev_out[r*ne0 + k], bit-identical
+ * to the reference CPU decoder (qwen3moe.cpp:128-202). */
+int eahmmf_hip_dequantize(const uint8_t* dev_w, int type, int64_t ne0, int64_t nrows, size_t row_bytes,
+                          float* dev_out, void* stream);
+
+/* Row bytes of a row of ne0 values, 0 if the type/length is unsupported. */
+size_t eahmmf_hip_row_bytes(int type, int64_t ne0);
+
+/* Host-side quantizer (synthetic weights): src[nrows][ne0] fp32 -> dst rows of
+ * eahmmf_hip_row_bytes(type, ne0) bytes.  Returns bytes written or -1. */
+int64_t eahmmf_hip_quantize_rows(int type, const float* src, int64_t nrows, int64_t ne0, uint8_t* dst);
+
+/* ---- device memory for DeviceBackend implementations ----------------- */
+
+/* Thin wrappers used by the C++ HipDevice (hipMalloc/hipFree/async copies on
+ * the library stream/hipMemGetInfo).  Return 0 on success. */
+int eahmmf_hip_alloc(void** dev_ptr, size_t bytes);
+int eahmmf_hip_free(void* dev_ptr);
+int eahmmf_hip_h2d(void* dev_dst, const void* host_src, size_t n);
+int eahmmf_hip_d2h(void* host_dst, const void* dev_src, size_t n);
+int eahmmf_hip_sync(void);
+int eahmmf_hip_mem_info(size_t* free_bytes, size_t* total_bytes);
+
+/* ---- diagnostics / lifetime ------------------------------------------- */
+const char* eahmmf_hip_last_error(void);
+int eahmmf_hip_device_count(void);
+/* Frees the calling device's scratch, staging buffers and stream. */
+void eahmmf_hip_shutdown(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

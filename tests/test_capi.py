@@ -1,0 +1,68 @@
+"""C ABI checks that need no GPU: exports, argument validation, host helpers."""
+import os
+import re
+
+import numpy as np
+import pytest
+
+import oracle
+from conftest import ROOT
+
+
+def declared_symbols():
+    txt = open(os.path.join(ROOT, "include", "eahmmf_hip.h")).read()
+    txt = re.sub(r"/\*.*?\*/", "", txt, flags=re.S)
+    return sorted(set(re.findall(r"\b(eahmmf_hip_[a-z0-9_]+)\s*\(", txt)))
+
+
+def test_every_declared_symbol_is_exported(binding, hip):
+    syms = declared_symbols()
+    assert len(syms) >= 19
+    for s in syms:
+        assert hasattr(hip, s), s
+    assert set(syms) == set(binding.EXPORTS)
+
+
+def test_invalid_arguments_fail_without_touching_the_device(hip):
+    x = np.zeros(256, dtype=np.float32)
+    out = np.zeros(8, dtype=np.float32)
+    # null weights, unsupported type, bad ldx, row_bytes mismatch: all rejected up front
+    assert not hip.eahmmf_hip_matmul(None, 12, 256, 8, 144, x.ctypes.data, 1, 256, out.ctypes.data, 8)
+    assert "null" in hip.eahmmf_hip_last_error().decode()
+    fake = 4096  # never dereferenced: validation fails first
+    assert not hip.eahmmf_hip_matmul(fake, 2, 256, 8, 144, x.ctypes.data, 1, 256, out.ctypes.data, 8)
+    assert "type" in hip.eahmmf_hip_last_error().decode()
+    assert not hip.eahmmf_hip_matmul(fake, 12, 256, 8, 144, x.ctypes.data, 1, 128, out.ctypes.data, 8)
+    assert not hip.eahmmf_hip_matmul(fake, 12, 256, 8, 140, x.ctypes.data, 1, 256, out.ctypes.data, 8)
+    assert not hip.eahmmf_hip_matmul(fake, 12, 200, 8, 144, x.ctypes.data, 1, 256, out.ctypes.data, 8)
+    assert not hip.eahmmf_hip_matmul_pair(fake, 12, 256, 8, 144, fake, 12, 256, 4, 144, x.ctypes.data, 1, 256,
+                                          out.ctypes.data, 8, out.ctypes.data, 8)
+    assert "mismatch" in hip.eahmmf_hip_last_error().decode()
+    ids = np.zeros(8, dtype=np.int32)
+    assert not hip.eahmmf_hip_route_topk(x.ctypes.data, 1, 128, 17, ids.ctypes.data, out.ctypes.data)
+    assert not hip.eahmmf_hip_route_topk(x.ctypes.data, 1, 1024, 8, ids.ctypes.data, out.ctypes.data)
+
+
+@pytest.mark.parametrize("t,ne0", [(0, 64), (8, 96), (12, 2048), (13, 768), (14, 768), (14, 1536)])
+def test_row_bytes(hip, t, ne0):
+    assert hip.eahmmf_hip_row_bytes(t, ne0) == oracle.row_bytes(t, ne0)
+
+
+def test_row_bytes_rejects(hip):
+    assert hip.eahmmf_hip_row_bytes(12, 300) == 0
+    assert hip.eahmmf_hip_row_bytes(3, 256) == 0
+
+
+@pytest.mark.parametrize("t,bits", [(8, 8), (12, 4), (13, 5), (14, 6)])
+def test_quantizer_round_trip(binding, t, bits):
+    """Quantize N(0, 0.02) rows and decode them with the oracle: the error is
+    bounded by the format's step size (a broken layout gives O(1) errors)."""
+    rng = np.random.default_rng(5)
+    ne0 = 512
+    w = rng.normal(0, 0.02, (16, ne0)).astype(np.float32)
+    q = binding.quantize_rows(t, w)
+    back = oracle.dequant_rows(t, q, ne0)
+    err = np.abs(back - w)
+    amax = np.abs(w).max()
+    assert err.max() < amax * 2.0 ** (2 - bits) * 1.2
+    assert err.mean() < amax * 2.0 ** (-bits)

@@ -1,0 +1,239 @@
+"""HIP path vs the oracle, through the C ABI (MI355X).
+
+Bars (from the north star): dequantized weights and top-k expert ids
+bit-exact; outputs within 1e-3 relative / 1e-4 absolute of the oracle's fp32
+result: |gpu - oracle| <= 1e-4 + 1e-3 * |oracle| elementwise.
+"""
+import ctypes
+import os
+
+import numpy as np
+import pytest
+
+import oracle
+import synth
+from conftest import GOLDEN
+
+pytestmark = pytest.mark.gpu
+
+RTOL, ATOL = 1e-3, 1e-4
+Q8_0, Q4_K, Q5_K, Q6_K = 8, 12, 13, 14
+
+
+def close(got, want):
+    err = np.abs(got.astype(np.float64) - want.astype(np.float64))
+    lim = ATOL + RTOL * np.abs(want.astype(np.float64))
+    bad = err > lim
+    assert not bad.any(), f"{bad.sum()} of {bad.size} outside tolerance; max err {err.max():.3e}"
+
+
+@pytest.fixture(scope="module")
+def torch_dev():
+    import torch
+    assert torch.cuda.is_available()
+    return torch
+
+
+def to_dev(torch, a):
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def ptr(t):
+    return ctypes.c_void_p(t.data_ptr())
+
+
+# ---------------------------------------------------------------------------
+# dequantization: bit-exact
+
+@pytest.mark.parametrize("t", [Q8_0, Q4_K, Q5_K, Q6_K])
+def test_dequant_golden_bit_exact(torch_dev, hip, t):
+    torch = torch_dev
+    g = np.load(os.path.join(GOLDEN, "dequant_golden.npz"))
+    blocks, want = g[f"blocks_{t}"], g[f"values_{t}"]
+    blck = oracle.BLOCK[t][0]
+    dw = to_dev(torch, blocks)
+    out = torch.empty((blocks.shape[0], blck), dtype=torch.float32, device="cuda")
+    assert hip.eahmmf_hip_dequantize(ptr(dw), t, blck, blocks.shape[0], blocks.shape[1], ptr(out), None) == 0
+    torch.cuda.synchronize()
+    got = out.cpu().numpy()
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+@pytest.mark.parametrize("t,rows,ne0", [(Q4_K, 768, 2048), (Q6_K, 2048, 768), (Q5_K, 768, 2048), (Q8_0, 2048, 768),
+                                        (Q8_0, 37, 96), (Q6_K, 9, 1536)])
+def test_dequant_expert_shapes_bit_exact(torch_dev, hip, t, rows, ne0):
+    torch = torch_dev
+    rng = np.random.default_rng(rows + ne0 + t)
+    w = synth.random_rows(t, rows, ne0, rng)
+    dw = to_dev(torch, w)
+    out = torch.empty((rows, ne0), dtype=torch.float32, device="cuda")
+    assert hip.eahmmf_hip_dequantize(ptr(dw), t, ne0, rows, w.shape[1], ptr(out), None) == 0
+    torch.cuda.synchronize()
+    want = oracle.dequant_rows(t, w, ne0)
+    assert np.array_equal(out.cpu().numpy().view(np.uint32), want.view(np.uint32))
+
+
+# ---------------------------------------------------------------------------
+# drop-in matmul / pair (host buffers, synchronous)
+
+MATMUL_CASES = [
+    (Q4_K, 2048, 768, 1), (Q4_K, 2048, 768, 3), (Q6_K, 768, 2048, 1), (Q6_K, 768, 2048, 8), (Q5_K, 2048, 64, 13),
+    (Q8_0, 2048, 96, 5), (Q8_0, 128, 256, 2), (Q8_0, 96, 17, 3), (Q6_K, 1536, 40, 64), (Q4_K, 4096, 33, 9),
+    (Q5_K, 256, 256, 4),
+]
+
+
+@pytest.mark.parametrize("t,ne0,ne1,nb", MATMUL_CASES)
+def test_matmul_vs_oracle(torch_dev, hip, t, ne0, ne1, nb):
+    torch = torch_dev
+    rng = np.random.default_rng(ne0 * 7 + ne1 + nb)
+    w = synth.random_rows(t, ne1, ne0, rng)
+    x = rng.normal(0, 1, (nb, ne0)).astype(np.float32)
+    dw = to_dev(torch, w)
+    ldx, ldo = ne0 + 3, ne1 + 5
+    xh = np.zeros((nb, ldx), dtype=np.float32)
+    xh[:, :ne0] = x
+    out = np.full((nb, ldo), 7.0, dtype=np.float32)
+    ok = hip.eahmmf_hip_matmul(ptr(dw), t, ne0, ne1, w.shape[1], xh.ctypes.data, nb, ldx, out.ctypes.data, ldo)
+    assert ok, hip.eahmmf_hip_last_error()
+    close(out[:, :ne1], oracle.matmul(t, w, ne0, x))
+    assert np.all(out[:, ne1:] == 7.0)  # padding untouched
+
+
+def test_matmul_golden_cases(torch_dev, hip):
+    torch = torch_dev
+    g = np.load(os.path.join(GOLDEN, "matmul_golden.npz"))
+    i = 0
+    while f"case{i}_meta" in g:
+        t, ne0, ne1, nb = (int(v) for v in g[f"case{i}_meta"])
+        w, x, want = g[f"case{i}_w"], g[f"case{i}_x"], g[f"case{i}_y"]
+        dw = to_dev(torch, w)
+        out = np.empty((nb, ne1), dtype=np.float32)
+        assert hip.eahmmf_hip_matmul(ptr(dw), t, ne0, ne1, w.shape[1], x.ctypes.data, nb, ne0, out.ctypes.data, ne1)
+        # golden W carries wide random scales: compare relative to the row scale
+        scale = np.abs(want).max()
+        assert np.abs(out - want).max() <= 1e-5 * scale + 1e-4
+        i += 1
+
+
+@pytest.mark.parametrize("gt_,ut,nb", [(Q4_K, Q4_K, 1), (Q5_K, Q4_K, 4), (Q8_0, Q8_0, 7)])
+def test_matmul_pair_vs_oracle(torch_dev, hip, gt_, ut, nb):
+    torch = torch_dev
+    ne0, ne1 = 512, 96
+    rng = np.random.default_rng(nb)
+    gw = synth.random_rows(gt_, ne1, ne0, rng)
+    uw = synth.random_rows(ut, ne1, ne0, rng)
+    x = rng.normal(0, 1, (nb, ne0)).astype(np.float32)
+    dg, du = to_dev(torch, gw), to_dev(torch, uw)
+    g = np.empty((nb, ne1), dtype=np.float32)
+    u = np.empty((nb, ne1), dtype=np.float32)
+    ok = hip.eahmmf_hip_matmul_pair(ptr(dg), gt_, ne0, ne1, gw.shape[1], ptr(du), ut, ne0, ne1, uw.shape[1],
+                                    x.ctypes.data, nb, ne0, g.ctypes.data, ne1, u.ctypes.data, ne1)
+    assert ok, hip.eahmmf_hip_last_error()
+    close(g, oracle.matmul(gt_, gw, ne0, x))
+    close(u, oracle.matmul(ut, uw, ne0, x))
+
+
+# ---------------------------------------------------------------------------
+# fused single-token expert block
+
+def make_layer(binding, types, D, FF, n_expert, rng, quantized=True):
+    gtp, utp, dtp = types
+    ex = []
+    for _ in range(n_expert):
+        if quantized:
+            g = synth.quantized_rows(binding, gtp, FF, D, rng)
+            u = synth.quantized_rows(binding, utp, FF, D, rng)
+            d = synth.quantized_rows(binding, dtp, D, FF, rng)
+        else:
+            g = synth.random_rows(gtp, FF, D, rng)
+            u = synth.random_rows(utp, FF, D, rng)
+            d = synth.random_rows(dtp, D, FF, rng)
+        ex.append(((gtp, g), (utp, u), (dtp, d)))
+    return ex
+
+
+DECODE_CASES = [
+    ("c1_q8_0", (Q8_0, Q8_0, Q8_0), 256, 128, 8, 2),
+    ("tiny_mix", (Q5_K, Q4_K, Q6_K), 256, 256, 8, 2),
+    ("c2_q4_k_m", (Q4_K, Q4_K, Q6_K), 2048, 768, 16, 8),
+    ("c3_q5_k", (Q5_K, Q5_K, Q5_K), 2048, 768, 8, 8),
+    ("c3_q8_0", (Q8_0, Q8_0, Q8_0), 2048, 768, 8, 8),
+    ("c5_q4_k_m", (Q4_K, Q4_K, Q6_K), 4096, 1536, 8, 8),
+]
+
+
+@pytest.mark.parametrize("name,types,D,FF,E,k", DECODE_CASES, ids=[c[0] for c in DECODE_CASES])
+def test_moe_decode_vs_oracle(torch_dev, binding, hip, name, types, D, FF, E, k):
+    torch = torch_dev
+    rng = np.random.default_rng(D + FF + k)
+    layer = make_layer(binding, types, D, FF, E, rng)
+    x = rng.normal(0, 1, (1, D)).astype(np.float32)
+    logits = rng.normal(0, 1, (1, E)).astype(np.float32)
+    ids, w = oracle.route_topk(logits, k)
+    want = oracle.moe_layer(layer, x, ids, w)[0]
+    dev = [[to_dev(torch, layer[e][c][1]) for c in range(3)] for e in range(E)]
+    experts = (binding.Expert * k)()
+    for j in range(k):
+        e = int(ids[0, j])
+        for c, (nm, ne0, ne1) in enumerate((("gate", D, FF), ("up", D, FF), ("down", FF, D))):
+            t = layer[e][c][0]
+            setattr(experts[j], nm, binding.Weight(dev[e][c].data_ptr(), t, ne0, ne1, binding.row_bytes(t, ne0)))
+    y = np.empty(D, dtype=np.float32)
+    wk = np.ascontiguousarray(w[0])
+    assert hip.eahmmf_hip_moe_decode(experts, wk.ctypes.data, k, x.ctypes.data, y.ctypes.data), \
+        hip.eahmmf_hip_last_error()
+    close(y, want)
+
+
+def test_route_topk_vs_oracle(torch_dev, hip):
+    rng = np.random.default_rng(3)
+    nb, E, k = 257, 128, 8
+    logits = rng.normal(0, 1, (nb, E)).astype(np.float32)
+    logits[0, 5] = logits[0, 9] = 4.0  # exact tie: lower id first
+    logits[1, :] = 0.5
+    ids = np.empty((nb, k), dtype=np.int32)
+    w = np.empty((nb, k), dtype=np.float32)
+    assert hip.eahmmf_hip_route_topk(logits.ctypes.data, nb, E, k, ids.ctypes.data, w.ctypes.data)
+    oids, ow = oracle.route_topk(logits, k)
+    assert np.array_equal(ids, oids)
+    np.testing.assert_allclose(w, ow, rtol=1e-6, atol=0)  # device expf vs glibc expf: a few ulps
+
+
+def test_moe_decode_async_and_routed(torch_dev, binding, hip):
+    """Device-resident activations: direct slots and the routed variant (ids
+    and weights produced on the device by route_topk) give the oracle's answer."""
+    torch = torch_dev
+    D, FF, E, k = 2048, 768, 32, 8
+    rng = np.random.default_rng(99)
+    layer = make_layer(binding, (Q4_K, Q4_K, Q6_K), D, FF, E, rng)
+    x = rng.normal(0, 1, (1, D)).astype(np.float32)
+    logits = rng.normal(0, 1, (1, E)).astype(np.float32)
+    ids, w = oracle.route_topk(logits, k)
+    want = oracle.moe_layer(layer, x, ids, w)[0]
+    dev = [[to_dev(torch, layer[e][c][1]) for c in range(3)] for e in range(E)]
+    shape = binding.MoeShape(Q4_K, Q4_K, Q6_K, D, FF, binding.row_bytes(Q4_K, D), binding.row_bytes(Q4_K, D),
+                             binding.row_bytes(Q6_K, FF))
+    stream = torch.cuda.current_stream().cuda_stream
+    dx = to_dev(torch, x)
+    dy = torch.full((D,), float("nan"), device="cuda")
+    slots = (binding.ExpertPtrs * k)(*[binding.ExpertPtrs(*[dev[int(e)][c].data_ptr() for c in range(3)])
+                                       for e in ids[0]])
+    wk = np.ascontiguousarray(w[0])
+    assert hip.eahmmf_hip_moe_decode_async(ctypes.byref(shape), slots, wk.ctypes.data, k, ptr(dx), ptr(dy),
+                                           ctypes.c_void_p(stream)) == 0
+    torch.cuda.synchronize()
+    close(dy.cpu().numpy(), want)
+    # routed: table + routing on device
+    table = np.array([[dev[e][c].data_ptr() for c in range(3)] for e in range(E)], dtype=np.uint64)
+    dtable = to_dev(torch, table.view(np.int64))
+    dlog = to_dev(torch, logits)
+    dids = torch.empty((1, k), dtype=torch.int32, device="cuda")
+    dwts = torch.empty((1, k), dtype=torch.float32, device="cuda")
+    dy2 = torch.full((D,), float("nan"), device="cuda")
+    assert hip.eahmmf_hip_route_topk_async(ptr(dlog), 1, E, k, ptr(dids), ptr(dwts), ctypes.c_void_p(stream)) == 0
+    assert hip.eahmmf_hip_moe_decode_routed_async(ctypes.byref(shape), ptr(dtable), E, ptr(dids), ptr(dwts), k,
+                                                  ptr(dx), ptr(dy2), ctypes.c_void_p(stream)) == 0
+    torch.cuda.synchronize()
+    assert np.array_equal(dids.cpu().numpy(), ids)
+    close(dy2.cpu().numpy(), want)
