@@ -31,6 +31,11 @@ struct ExpertEntry {
     const uint8_t* down;
 };
 
+// hipGetLastError() reports the last failure of any runtime call on this
+// thread, including ones made by other libraries in the process; launchers
+// clear it first so a launch is judged by its own status only.
+inline void clear_stale_error() { (void)hipGetLastError(); }
+
 hipError_t launch_dequant(int type, const uint8_t* w, int64_t ne0, int64_t nrows, size_t row_bytes, float* out,
                           hipStream_t st);
 hipError_t launch_matmul(int type, const uint8_t* w, int ne0, int ne1, size_t row_bytes, const float* x, int nb,

@@ -68,6 +68,7 @@ hipError_t launch_dequant(int type, const uint8_t* w, int64_t ne0, int64_t nrows
     const int64_t segs = ne0 / 32;
     const int64_t total = segs * nrows;
     if (total <= 0) return hipSuccess;
+    clear_stale_error();
     const dim3 grid((unsigned)((total + 255) / 256)), block(256);
     switch (type) {
         case kQ4_K: dequant_kernel<kQ4_K><<<grid, block, 0, st>>>(w, segs, nrows, row_bytes, out); break;
@@ -83,6 +84,7 @@ hipError_t launch_dequant(int type, const uint8_t* w, int64_t ne0, int64_t nrows
 hipError_t launch_matmul(int type, const uint8_t* w, int ne0, int ne1, size_t row_bytes, const float* x, int nb,
                          int ldx, float* out, int ldo, hipStream_t st) {
     constexpr int TT = 8;
+    clear_stale_error();
     const dim3 grid((unsigned)((ne1 + 3) / 4), (unsigned)((nb + TT - 1) / TT)), block(256);
     switch (type) {
         case kQ4_K: matmul_kernel<kQ4_K, TT><<<grid, block, 0, st>>>(w, ne0, ne1, row_bytes, x, nb, ldx, out, ldo); break;

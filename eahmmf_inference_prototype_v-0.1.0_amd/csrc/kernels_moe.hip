@@ -206,6 +206,7 @@ static hipError_t run_decode(const MoeShape& s, const SlotSource& src, int k, co
     if (!moe_shape_ok(s) || k <= 0 || k > kMaxSlots) return hipErrorInvalidValue;
     if ((size_t)k * s.FF * sizeof(float) > 64 * 1024 || (size_t)s.D * sizeof(float) > 64 * 1024)
         return hipErrorInvalidValue;
+    clear_stale_error();
     hipError_t e;
     switch (s.gate_type) {
         case kQ4_K: e = dispatch_phase_a_up<kQ4_K>(s, src, k, x, h, st); break;
@@ -250,6 +251,7 @@ hipError_t launch_moe_decode_routed(const MoeShape& s, const ExpertEntry* table,
 hipError_t launch_route_topk(const float* logits, int nb, int n_expert, int k, int* ids, float* w, hipStream_t st) {
     if (nb <= 0 || n_expert <= 0 || n_expert > 512 || k <= 0 || k > kMaxSlots || k > n_expert)
         return hipErrorInvalidValue;
+    clear_stale_error();
     const dim3 grid((unsigned)((nb + 3) / 4)), block(256);
     route_topk_kernel<<<grid, block, 0, st>>>(logits, nb, n_expert, k, ids, w);
     return hipGetLastError();

@@ -51,10 +51,24 @@ def row_bytes(gtype, ne0):
     return ne0 // blck * nbytes
 
 
+def _share_torch_runtime():
+    """PyTorch wheels bundle their own HIP/HSA runtime.  A process must hold
+    only one: two runtimes each try to own the device and the second reports
+    no device.  When torch is installed it is imported first, and the
+    library's libamdhip64.so.7 dependency then resolves to the runtime torch
+    already loaded (same soname).  Without torch the system ROCm runtime is
+    used."""
+    try:
+        import torch  # noqa: F401
+    except ImportError:
+        pass
+
+
 def load(path=LIB_PATH):
     """Load the library and declare its signatures.  Raises if it is missing."""
     if not os.path.exists(path):
         raise RuntimeError(f"{path} is not built; run __graft_entry__.build() (make -C the package)")
+    _share_torch_runtime()
     lib = ctypes.CDLL(path)
     c_bool, c_int, c_sz, c_i64, vp = ctypes.c_bool, ctypes.c_int, ctypes.c_size_t, ctypes.c_int64, ctypes.c_void_p
     sig = {

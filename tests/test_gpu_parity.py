@@ -53,7 +53,8 @@ def test_dequant_golden_bit_exact(torch_dev, hip, t):
     blck = oracle.BLOCK[t][0]
     dw = to_dev(torch, blocks)
     out = torch.empty((blocks.shape[0], blck), dtype=torch.float32, device="cuda")
-    assert hip.eahmmf_hip_dequantize(ptr(dw), t, blck, blocks.shape[0], blocks.shape[1], ptr(out), None) == 0
+    rc = hip.eahmmf_hip_dequantize(ptr(dw), t, blck, blocks.shape[0], blocks.shape[1], ptr(out), None)
+    assert rc == 0, hip.eahmmf_hip_last_error()
     torch.cuda.synchronize()
     got = out.cpu().numpy()
     assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
@@ -67,7 +68,8 @@ def test_dequant_expert_shapes_bit_exact(torch_dev, hip, t, rows, ne0):
     w = synth.random_rows(t, rows, ne0, rng)
     dw = to_dev(torch, w)
     out = torch.empty((rows, ne0), dtype=torch.float32, device="cuda")
-    assert hip.eahmmf_hip_dequantize(ptr(dw), t, ne0, rows, w.shape[1], ptr(out), None) == 0
+    rc = hip.eahmmf_hip_dequantize(ptr(dw), t, ne0, rows, w.shape[1], ptr(out), None)
+    assert rc == 0, hip.eahmmf_hip_last_error()
     torch.cuda.synchronize()
     want = oracle.dequant_rows(t, w, ne0)
     assert np.array_equal(out.cpu().numpy().view(np.uint32), want.view(np.uint32))
@@ -109,7 +111,8 @@ def test_matmul_golden_cases(torch_dev, hip):
         w, x, want = g[f"case{i}_w"], g[f"case{i}_x"], g[f"case{i}_y"]
         dw = to_dev(torch, w)
         out = np.empty((nb, ne1), dtype=np.float32)
-        assert hip.eahmmf_hip_matmul(ptr(dw), t, ne0, ne1, w.shape[1], x.ctypes.data, nb, ne0, out.ctypes.data, ne1)
+        assert hip.eahmmf_hip_matmul(ptr(dw), t, ne0, ne1, w.shape[1], x.ctypes.data, nb, ne0, out.ctypes.data, ne1), \
+            hip.eahmmf_hip_last_error()
         # golden W carries wide random scales: compare relative to the row scale
         scale = np.abs(want).max()
         assert np.abs(out - want).max() <= 1e-5 * scale + 1e-4
