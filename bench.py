@@ -150,22 +150,13 @@ def main():
     sp = ctypes.c_void_p(stream.cuda_stream)
     vp = ctypes.c_void_p
 
-    def route(i):
-        s = i % NS
-        rc = hip.eahmmf_hip_route_topk_async(vp(dlog[s].data_ptr()), 1, E, K, vp(dids[s].data_ptr()),
-                                            vp(dw[s].data_ptr()), sp)
-        assert rc == 0, b.last_error()
-
-    def experts(i):
-        s = i % NS
-        rc = hip.eahmmf_hip_moe_decode_routed_async(ctypes.byref(shape), vp(tables[i % R].data_ptr()), E,
-                                                    vp(dids[s].data_ptr()), vp(dw[s].data_ptr()), K,
-                                                    vp(dx[s].data_ptr()), vp(dy[s].data_ptr()), sp)
-        assert rc == 0, b.last_error()
-
     def step(i):
-        route(i)
-        experts(i)
+        s = i % NS
+        rc = hip.eahmmf_hip_moe_layer_decode_async(ctypes.byref(shape), vp(tables[i % R].data_ptr()), E,
+                                                   vp(dlog[s].data_ptr()), K, vp(dx[s].data_ptr()),
+                                                   vp(dy[s].data_ptr()), vp(dids[s].data_ptr()), vp(dw[s].data_ptr()),
+                                                   sp)
+        assert rc == 0, b.last_error()
 
     for i in range(args.warmup):
         step(i)
@@ -175,17 +166,19 @@ def main():
         step(args.warmup + i)
     torch.cuda.synchronize()
     el = time.perf_counter() - t0
+    assert hip.eahmmf_hip_device_flags() == 0, "a fused launch ran out of its bounded wait"
+    kernel_name = ("moe_decode_fused (routing + gate/up + down in one launch)" if hip.eahmmf_hip_set_fused(-1)
+                   else "route_topk + moe_gate_up + moe_down")
     bytes_step = K * (2 * FF * b.row_bytes(Q4_K, D) + D * b.row_bytes(Q6_K, FF))
     value = bytes_step * args.steps / el / 1e9
     ms = el * 1e3 / args.steps
 
-    # expert block alone, HIP events on the launch stream
+    # the layer kernel alone, HIP events on the launch stream
     n_ev = 200
     ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(n_ev)]
     for i in range(n_ev):
-        route(i)
         ev[i][0].record(stream)
-        experts(i)
+        step(i)
         ev[i][1].record(stream)
     torch.cuda.synchronize()
     durs = np.array([a.elapsed_time(z) for a, z in ev]) * 1e3  # us
@@ -203,7 +196,7 @@ def main():
                        R * (gate.nbytes + up.nbytes + down.nbytes))},
         "pct_of_hbm_peak": round(100 * value / HBM_PEAK_GBS, 2),
         "expert_only_decode_tokens_per_s_48_layers": round(1.0 / (48 * ms * 1e-3), 1),
-        "roofline": {"bound": "hbm", "kernel": "expert block (moe_gate_up + moe_down)",
+        "roofline": {"bound": "hbm", "kernel": kernel_name,
                      "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
                      "avg_us": round(kern_us, 3), "p10_us": round(float(np.percentile(durs, 10)), 3),

@@ -8,6 +8,7 @@
 // stream, and always drain the stream before returning, also after an error,
 // so a caller may release its expert leases as soon as the call returns.
 #include <stdarg.h>
+#include <stdlib.h>
 #include <stdio.h>
 #include <string.h>
 
@@ -49,7 +50,19 @@ struct DevCtx {
     hipStream_t stream = nullptr;
     DeviceBuf dx, dy, dy2, dh, dids, dw;  // device scratch
     DeviceBuf px, py, py2;                // pinned host staging
+    unsigned* dsync = nullptr;            // fused-launch counters (zeroed once, reset by the kernel)
 };
+
+// 1: single fused launch where the shape allows it; 0: route + two-kernel path.
+// EAHMMF_HIP_UNFUSED=1 in the environment selects 0 at start-up.
+int g_fused = -1;
+bool fused_enabled() {
+    if (g_fused < 0) {
+        const char* e = getenv("EAHMMF_HIP_UNFUSED");
+        g_fused = (e && *e && *e != '0') ? 0 : 1;
+    }
+    return g_fused == 1;
+}
 
 std::mutex g_mu;
 std::map<int, DevCtx> g_ctx;
@@ -61,6 +74,15 @@ DevCtx* ctx_for_current_device() {
     DevCtx& c = g_ctx[dev];
     if (!c.stream && !hip_ok(hipStreamCreateWithFlags(&c.stream, hipStreamNonBlocking), "hipStreamCreate"))
         return nullptr;
+    if (!c.dsync) {
+        void* p = nullptr;
+        if (!hip_ok(hipMalloc(&p, 256), "hipMalloc(sync)")) return nullptr;
+        if (!hip_ok(hipMemset(p, 0, 256), "hipMemset(sync)")) {
+            (void)hipFree(p);
+            return nullptr;
+        }
+        c.dsync = (unsigned*)p;
+    }
     return &c;
 }
 
@@ -213,8 +235,23 @@ bool eahmmf_hip_moe_decode(const eahmmf_hip_expert* experts, const float* w, int
     const size_t ybytes = (size_t)s.D * sizeof(float);
     bool ok = grow_device(c->dy, ybytes) && grow_pinned(c->py, ybytes) &&
               grow_device(c->dh, (size_t)k * s.FF * sizeof(float)) && stage_x(c, host_x, 1, s.D, s.D);
-    if (ok) ok = hip_ok(launch_moe_decode(s, slots, (const float*)c->dx.p, (float*)c->dh.p, (float*)c->dy.p, c->stream),
-                        "moe decode launch");
+    if (ok) {
+        if (fused_enabled() && fused_supported(s, k, 0)) {
+            FusedArgsHost f;
+            f.shape = s;
+            f.k = k;
+            f.mode = 0;
+            f.direct = slots;
+            f.x = (const float*)c->dx.p;
+            f.y = (float*)c->dy.p;
+            f.h = (float*)c->dh.p;
+            f.sync = c->dsync;
+            ok = hip_ok(launch_moe_fused(f, c->stream), "fused moe decode launch");
+        } else {
+            ok = hip_ok(launch_moe_decode(s, slots, (const float*)c->dx.p, (float*)c->dh.p, (float*)c->dy.p,
+                                          c->stream), "moe decode launch");
+        }
+    }
     if (ok) ok = hip_ok(hipMemcpyAsync(c->py.p, c->dy.p, ybytes, hipMemcpyDeviceToHost, c->stream), "copy y");
     ok = drain(c, ok);
     if (ok) memcpy(host_y, c->py.p, ybytes);
@@ -254,6 +291,18 @@ int eahmmf_hip_moe_decode_async(const eahmmf_hip_moe_shape* shape, const eahmmf_
     DevCtx* c = ctx_for_current_device();
     if (!c) return -2;
     if (!grow_device(c->dh, (size_t)k * s.FF * sizeof(float))) return -2;
+    if (fused_enabled() && fused_supported(s, k, 0)) {
+        FusedArgsHost f;
+        f.shape = s;
+        f.k = k;
+        f.mode = 0;
+        f.direct = slots;
+        f.x = dev_x;
+        f.y = dev_y;
+        f.h = (float*)c->dh.p;
+        f.sync = c->dsync;
+        return hip_ok(launch_moe_fused(f, (hipStream_t)stream), "fused moe decode launch") ? 0 : -3;
+    }
     if (!hip_ok(launch_moe_decode(s, slots, dev_x, (float*)c->dh.p, dev_y, (hipStream_t)stream), "moe decode launch"))
         return -3;
     return 0;
@@ -270,11 +319,88 @@ int eahmmf_hip_moe_decode_routed_async(const eahmmf_hip_moe_shape* shape, const 
     DevCtx* c = ctx_for_current_device();
     if (!c) return -2;
     if (!grow_device(c->dh, (size_t)k * s.FF * sizeof(float))) return -2;
+    if (fused_enabled() && fused_supported(s, k, 0)) {
+        FusedArgsHost f;
+        f.shape = s;
+        f.k = k;
+        f.n_expert = n_expert;
+        f.mode = 2;
+        f.table = (const ExpertEntry*)dev_table;
+        f.ids_in = dev_ids;
+        f.w_in = dev_w;
+        f.x = dev_x;
+        f.y = dev_y;
+        f.h = (float*)c->dh.p;
+        f.sync = c->dsync;
+        return hip_ok(launch_moe_fused(f, (hipStream_t)stream), "fused routed moe decode launch") ? 0 : -3;
+    }
     if (!hip_ok(launch_moe_decode_routed(s, (const ExpertEntry*)dev_table, n_expert, dev_ids, dev_w, k, dev_x,
                                          (float*)c->dh.p, dev_y, (hipStream_t)stream),
                 "routed moe decode launch"))
         return -3;
     return 0;
+}
+
+int eahmmf_hip_moe_layer_decode_async(const eahmmf_hip_moe_shape* shape, const eahmmf_hip_expert_ptrs* dev_table,
+                                      int n_expert, const float* dev_logits, int k, const float* dev_x, float* dev_y,
+                                      int* dev_ids_out, float* dev_w_out, void* stream) {
+    MoeShape s{};
+    if (!shape_from_abi(shape, s)) return -1;
+    if (!dev_table || !dev_logits || !dev_x || !dev_y) return set_error("null argument"), -1;
+    if (n_expert <= 0 || n_expert > 512 || k <= 0 || k > kMaxSlots || k > n_expert)
+        return set_error("bad routing shape n_expert=%d k=%d", n_expert, k), -1;
+    DevCtx* c = ctx_for_current_device();
+    if (!c) return -2;
+    if (!grow_device(c->dh, (size_t)k * s.FF * sizeof(float))) return -2;
+    hipStream_t st = (hipStream_t)stream;
+    if (fused_enabled() && fused_supported(s, k, n_expert)) {
+        FusedArgsHost f;
+        f.shape = s;
+        f.k = k;
+        f.n_expert = n_expert;
+        f.mode = 1;
+        f.table = (const ExpertEntry*)dev_table;
+        f.logits = dev_logits;
+        f.ids_out = dev_ids_out;
+        f.w_out = dev_w_out;
+        f.x = dev_x;
+        f.y = dev_y;
+        f.h = (float*)c->dh.p;
+        f.sync = c->dsync;
+        return hip_ok(launch_moe_fused(f, st), "fused moe layer launch") ? 0 : -3;
+    }
+    // two-step path: routing kernel into scratch (or the caller's buffers), then the expert block
+    int* ids = dev_ids_out;
+    float* w = dev_w_out;
+    if (!ids || !w) {
+        if (!grow_device(c->dids, (size_t)k * sizeof(int)) || !grow_device(c->dw, (size_t)k * sizeof(float))) return -2;
+        ids = (int*)c->dids.p;
+        w = (float*)c->dw.p;
+    }
+    if (!hip_ok(launch_route_topk(dev_logits, 1, n_expert, k, ids, w, st), "route launch")) return -3;
+    if (!hip_ok(launch_moe_decode_routed(s, (const ExpertEntry*)dev_table, n_expert, ids, w, k, dev_x,
+                                         (float*)c->dh.p, dev_y, st),
+                "routed moe decode launch"))
+        return -3;
+    return 0;
+}
+
+int eahmmf_hip_set_fused(int enable) {
+    const int prev = fused_enabled() ? 1 : 0;
+    if (enable >= 0) g_fused = enable ? 1 : 0;
+    return prev;
+}
+
+int eahmmf_hip_device_flags(void) {
+    DevCtx* c = ctx_for_current_device();
+    if (!c) return -2;
+    unsigned v[4] = {0, 0, 0, 0};
+    if (!hip_ok(hipMemcpy(v, c->dsync, sizeof v, hipMemcpyDeviceToHost), "read device flags")) return -2;
+    if (v[2]) {
+        const unsigned zero = 0;
+        (void)hipMemcpy(c->dsync + 2, &zero, sizeof zero, hipMemcpyHostToDevice);
+    }
+    return (int)v[2];
 }
 
 bool eahmmf_hip_route_topk(const float* host_logits, int nb, int n_expert, int k, int* host_ids, float* host_w) {
@@ -365,6 +491,7 @@ void eahmmf_hip_shutdown(void) {
         if (b->p) (void)hipFree(b->p);
     for (DeviceBuf* b : {&c.px, &c.py, &c.py2})
         if (b->p) (void)hipHostFree(b->p);
+    if (c.dsync) (void)hipFree(c.dsync);
     if (c.stream) (void)hipStreamDestroy(c.stream);
     g_ctx.erase(it);
 }

@@ -48,6 +48,26 @@ hipError_t launch_moe_decode(const MoeShape& s, const DecodeSlots& slots, const 
 hipError_t launch_moe_decode_routed(const MoeShape& s, const ExpertEntry* table, int n_expert, const int* ids,
                                     const float* w, int k, const float* x, float* h, float* y, hipStream_t st);
 
+// Host description of one fused expert-block launch (kernels_fused.hip).
+struct FusedArgsHost {
+    MoeShape shape;
+    int k = 0, n_expert = 0;
+    int mode = 0;  // 0: direct slots, 1: logits + table (routing in the kernel), 2: ids/w + table
+    DecodeSlots direct{};
+    const ExpertEntry* table = nullptr;
+    const float* logits = nullptr;
+    const int* ids_in = nullptr;
+    const float* w_in = nullptr;
+    int* ids_out = nullptr;
+    float* w_out = nullptr;
+    const float* x = nullptr;
+    float* y = nullptr;
+    float* h = nullptr;           // k * FF floats
+    unsigned* sync = nullptr;     // 3 counters, zero before the first launch
+};
+bool fused_supported(const MoeShape& s, int k, int n_expert_for_routing);
+hipError_t launch_moe_fused(const FusedArgsHost& h, hipStream_t st);
+
 // softmax -> top-k (e desc, index asc) -> renormalise; logits [nb][n_expert].
 hipError_t launch_route_topk(const float* logits, int nb, int n_expert, int k, int* ids, float* w, hipStream_t st);
 

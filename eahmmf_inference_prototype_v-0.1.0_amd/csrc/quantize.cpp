@@ -51,12 +51,6 @@ float from_half(uint16_t h) {
     return s ? -v : v;
 }
 
-void put_half(uint8_t* p, float v) {
-    const uint16_t h = to_half(v);
-    p[0] = (uint8_t)(h & 0xFF);
-    p[1] = (uint8_t)(h >> 8);
-}
-
 int clampi(int v, int lo, int hi) { return v < lo ? lo : (v > hi ? hi : v); }
 
 void q8_0_block(const float* x, uint8_t* b) {

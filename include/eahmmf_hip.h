@@ -101,6 +101,15 @@ int eahmmf_hip_moe_decode_routed_async(const eahmmf_hip_moe_shape* shape, const 
                                        int n_expert, const int* dev_ids, const float* dev_w, int k,
                                        const float* dev_x, float* dev_y, void* stream);
 
+/* One launch for a whole layer-token: routing from device router logits
+ * (dev_logits [n_expert], n_expert <= 256 for the fused kernel) and the
+ * expert block over the device table.  The chosen ids and weights are also
+ * written to dev_ids_out/dev_w_out [k] when those are non-null.  Replaces the
+ * routing and expert loop of qwen3moe.cpp:1011-1067 for one token. */
+int eahmmf_hip_moe_layer_decode_async(const eahmmf_hip_moe_shape* shape, const eahmmf_hip_expert_ptrs* dev_table,
+                                      int n_expert, const float* dev_logits, int k, const float* dev_x, float* dev_y,
+                                      int* dev_ids_out, float* dev_w_out, void* stream);
+
 /* Softmax -> top-k -> renormalise (qwen3moe.cpp:1011-1023), synchronous on
  * host buffers: logits[nb][n_expert] -> ids[nb][k], w[nb][k] in rank order
  * (e = expf(l - max) descending, lower id first on ties). */
@@ -134,6 +143,14 @@ int eahmmf_hip_sync(void);
 int eahmmf_hip_mem_info(size_t* free_bytes, size_t* total_bytes);
 
 /* ---- diagnostics / lifetime ------------------------------------------- */
+/* Selects the single-launch fused expert block (1, the default) or the
+ * routing + two-kernel path (0); a negative argument only queries.  Returns
+ * the previous setting.  EAHMMF_HIP_UNFUSED=1 selects 0 at start-up (like the
+ * reference's EAHMMF_OLD_KERNEL switch, expert_cuda.cu:307-308). */
+int eahmmf_hip_set_fused(int enable);
+/* Nonzero if a fused launch on the current device hit its bounded wait since
+ * the last call (its output is then not valid); clears the flag. */
+int eahmmf_hip_device_flags(void);
 const char* eahmmf_hip_last_error(void);
 int eahmmf_hip_device_count(void);
 /* Frees the calling device's scratch, staging buffers and stream. */

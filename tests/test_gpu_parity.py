@@ -159,6 +159,8 @@ def make_layer(binding, types, D, FF, n_expert, rng, quantized=True):
 DECODE_CASES = [
     ("c1_q8_0", (Q8_0, Q8_0, Q8_0), 256, 128, 8, 2),
     ("tiny_mix", (Q5_K, Q4_K, Q6_K), 256, 256, 8, 2),
+    ("d768_two_kernel_only", (Q4_K, Q4_K, Q6_K), 768, 256, 8, 4),
+    ("q6_k_gate_up", (Q6_K, Q6_K, Q4_K), 1024, 512, 8, 4),
     ("c2_q4_k_m", (Q4_K, Q4_K, Q6_K), 2048, 768, 16, 8),
     ("c3_q5_k", (Q5_K, Q5_K, Q5_K), 2048, 768, 8, 8),
     ("c3_q8_0", (Q8_0, Q8_0, Q8_0), 2048, 768, 8, 8),
@@ -166,8 +168,16 @@ DECODE_CASES = [
 ]
 
 
+@pytest.fixture(params=[1, 0], ids=["fused", "two_kernel"])
+def path(request, hip):
+    prev = hip.eahmmf_hip_set_fused(request.param)
+    yield request.param
+    hip.eahmmf_hip_set_fused(prev)
+    assert hip.eahmmf_hip_device_flags() == 0  # no fused launch ran out of its bounded wait
+
+
 @pytest.mark.parametrize("name,types,D,FF,E,k", DECODE_CASES, ids=[c[0] for c in DECODE_CASES])
-def test_moe_decode_vs_oracle(torch_dev, binding, hip, name, types, D, FF, E, k):
+def test_moe_decode_vs_oracle(torch_dev, binding, hip, path, name, types, D, FF, E, k):
     torch = torch_dev
     rng = np.random.default_rng(D + FF + k)
     layer = make_layer(binding, types, D, FF, E, rng)
@@ -203,7 +213,7 @@ def test_route_topk_vs_oracle(torch_dev, hip):
     np.testing.assert_allclose(w, ow, rtol=1e-6, atol=0)  # device expf vs glibc expf: a few ulps
 
 
-def test_moe_decode_async_and_routed(torch_dev, binding, hip):
+def test_moe_decode_async_and_routed(torch_dev, binding, hip, path):
     """Device-resident activations: direct slots and the routed variant (ids
     and weights produced on the device by route_topk) give the oracle's answer."""
     torch = torch_dev
@@ -240,3 +250,46 @@ def test_moe_decode_async_and_routed(torch_dev, binding, hip):
     torch.cuda.synchronize()
     assert np.array_equal(dids.cpu().numpy(), ids)
     close(dy2.cpu().numpy(), want)
+
+
+@pytest.mark.parametrize("name,types,D,FF,E,k", [
+    ("c2_q4_k_m", (Q4_K, Q4_K, Q6_K), 2048, 768, 128, 8),
+    ("c1_q8_0", (Q8_0, Q8_0, Q8_0), 256, 128, 8, 2),
+    ("c3_q5_k", (Q5_K, Q5_K, Q5_K), 2048, 768, 32, 8),
+    ("c5_q4_k_m", (Q4_K, Q4_K, Q6_K), 4096, 1536, 16, 8),
+], ids=lambda c: c if isinstance(c, str) else None)
+def test_moe_layer_decode_vs_oracle(torch_dev, binding, hip, path, name, types, D, FF, E, k):
+    """One launch per layer-token (routing from device logits) over a device
+    expert table, repeated for several tokens on one stream: ids bit-exact,
+    weights to a few ulps, y within tolerance, every token."""
+    torch = torch_dev
+    rng = np.random.default_rng(E + D)
+    n_unique = min(E, 24)
+    uniq = make_layer(binding, types, D, FF, n_unique, rng)
+    layer = [uniq[e % n_unique] for e in range(E)]
+    dev_u = [[to_dev(torch, uniq[e][c][1]) for c in range(3)] for e in range(n_unique)]
+    table = np.array([[dev_u[e % n_unique][c].data_ptr() for c in range(3)] for e in range(E)], dtype=np.uint64)
+    dtable = to_dev(torch, table.view(np.int64))
+    gt_, ut, dt_ = types
+    shape = binding.MoeShape(gt_, ut, dt_, D, FF, binding.row_bytes(gt_, D), binding.row_bytes(ut, D),
+                             binding.row_bytes(dt_, FF))
+    T = 6
+    xs = rng.normal(0, 1, (T, D)).astype(np.float32)
+    logits = rng.normal(0, 1, (T, E)).astype(np.float32)
+    dx, dl = to_dev(torch, xs), to_dev(torch, logits)
+    dy = torch.full((T, D), float("nan"), device="cuda")
+    dids = torch.full((T, k), -7, dtype=torch.int32, device="cuda")
+    dw = torch.zeros((T, k), dtype=torch.float32, device="cuda")
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    for t in range(T):
+        rc = hip.eahmmf_hip_moe_layer_decode_async(ctypes.byref(shape), ptr(dtable), E, ptr(dl[t]), k, ptr(dx[t]),
+                                                   ptr(dy[t]), ptr(dids[t]), ptr(dw[t]), stream)
+        assert rc == 0, hip.eahmmf_hip_last_error()
+    torch.cuda.synchronize()
+    ids, w = oracle.route_topk(logits, k)
+    assert np.array_equal(dids.cpu().numpy(), ids)
+    np.testing.assert_allclose(dw.cpu().numpy(), w, rtol=1e-6, atol=0)
+    y = dy.cpu().numpy()
+    for t in range(T):
+        want = oracle.moe_layer(layer, xs[t:t + 1], ids[t:t + 1], w[t:t + 1])[0]
+        close(y[t], want)
