@@ -48,9 +48,10 @@ struct DeviceBuf {
 
 struct DevCtx {
     hipStream_t stream = nullptr;
-    DeviceBuf dx, dy, dy2, dh, dids, dw;  // device scratch
+    DeviceBuf dx, dy, dy2, dh, dids, dw, dyp;  // device scratch
     DeviceBuf px, py, py2;                // pinned host staging
-    unsigned* dsync = nullptr;            // fused-launch counters (zeroed once, reset by the kernel)
+    unsigned* dsync = nullptr;            // fused-launch counters and flags (zeroed once)
+    unsigned epoch = 0;                   // fused launches issued on dsync
 };
 
 // 1: single fused launch where the shape allows it; 0: route + two-kernel path.
@@ -76,8 +77,8 @@ DevCtx* ctx_for_current_device() {
         return nullptr;
     if (!c.dsync) {
         void* p = nullptr;
-        if (!hip_ok(hipMalloc(&p, 256), "hipMalloc(sync)")) return nullptr;
-        if (!hip_ok(hipMemset(p, 0, 256), "hipMemset(sync)")) {
+        if (!hip_ok(hipMalloc(&p, kSyncWords * sizeof(unsigned)), "hipMalloc(sync)")) return nullptr;
+        if (!hip_ok(hipMemset(p, 0, kSyncWords * sizeof(unsigned)), "hipMemset(sync)")) {
             (void)hipFree(p);
             return nullptr;
         }
@@ -141,6 +142,9 @@ bool stage_x(DevCtx* c, const float* host_x, int nb, int ne0, int ldx) {
 void unstage_rows(const float* dense, int nb, int n, float* host, int ld) {
     for (int t = 0; t < nb; t++) memcpy(host + (size_t)t * ld, dense + (size_t)t * n, sizeof(float) * n);
 }
+
+// the fused launch's per-partition partial outputs (8 partitions x D floats)
+bool grow_fused(DevCtx* c, const MoeShape& s) { return grow_device(c->dyp, (size_t)8 * s.D * sizeof(float)); }
 
 bool weight_ok(const eahmmf_hip_weight& w) { return w.dev && type_supported(w.type) && w.ne0 > 0 && w.ne1 > 0; }
 
@@ -236,7 +240,7 @@ bool eahmmf_hip_moe_decode(const eahmmf_hip_expert* experts, const float* w, int
     bool ok = grow_device(c->dy, ybytes) && grow_pinned(c->py, ybytes) &&
               grow_device(c->dh, (size_t)k * s.FF * sizeof(float)) && stage_x(c, host_x, 1, s.D, s.D);
     if (ok) {
-        if (fused_enabled() && fused_supported(s, k, 0)) {
+        if (fused_enabled() && fused_supported(s, k, 0) && grow_fused(c, s)) {
             FusedArgsHost f;
             f.shape = s;
             f.k = k;
@@ -246,6 +250,8 @@ bool eahmmf_hip_moe_decode(const eahmmf_hip_expert* experts, const float* w, int
             f.y = (float*)c->dy.p;
             f.h = (float*)c->dh.p;
             f.sync = c->dsync;
+        f.ypart = (float*)c->dyp.p;
+        f.epoch = ++c->epoch;
             ok = hip_ok(launch_moe_fused(f, c->stream), "fused moe decode launch");
         } else {
             ok = hip_ok(launch_moe_decode(s, slots, (const float*)c->dx.p, (float*)c->dh.p, (float*)c->dy.p,
@@ -291,7 +297,7 @@ int eahmmf_hip_moe_decode_async(const eahmmf_hip_moe_shape* shape, const eahmmf_
     DevCtx* c = ctx_for_current_device();
     if (!c) return -2;
     if (!grow_device(c->dh, (size_t)k * s.FF * sizeof(float))) return -2;
-    if (fused_enabled() && fused_supported(s, k, 0)) {
+    if (fused_enabled() && fused_supported(s, k, 0) && grow_fused(c, s)) {
         FusedArgsHost f;
         f.shape = s;
         f.k = k;
@@ -301,6 +307,8 @@ int eahmmf_hip_moe_decode_async(const eahmmf_hip_moe_shape* shape, const eahmmf_
         f.y = dev_y;
         f.h = (float*)c->dh.p;
         f.sync = c->dsync;
+        f.ypart = (float*)c->dyp.p;
+        f.epoch = ++c->epoch;
         return hip_ok(launch_moe_fused(f, (hipStream_t)stream), "fused moe decode launch") ? 0 : -3;
     }
     if (!hip_ok(launch_moe_decode(s, slots, dev_x, (float*)c->dh.p, dev_y, (hipStream_t)stream), "moe decode launch"))
@@ -319,7 +327,7 @@ int eahmmf_hip_moe_decode_routed_async(const eahmmf_hip_moe_shape* shape, const 
     DevCtx* c = ctx_for_current_device();
     if (!c) return -2;
     if (!grow_device(c->dh, (size_t)k * s.FF * sizeof(float))) return -2;
-    if (fused_enabled() && fused_supported(s, k, 0)) {
+    if (fused_enabled() && fused_supported(s, k, 0) && grow_fused(c, s)) {
         FusedArgsHost f;
         f.shape = s;
         f.k = k;
@@ -332,6 +340,8 @@ int eahmmf_hip_moe_decode_routed_async(const eahmmf_hip_moe_shape* shape, const 
         f.y = dev_y;
         f.h = (float*)c->dh.p;
         f.sync = c->dsync;
+        f.ypart = (float*)c->dyp.p;
+        f.epoch = ++c->epoch;
         return hip_ok(launch_moe_fused(f, (hipStream_t)stream), "fused routed moe decode launch") ? 0 : -3;
     }
     if (!hip_ok(launch_moe_decode_routed(s, (const ExpertEntry*)dev_table, n_expert, dev_ids, dev_w, k, dev_x,
@@ -353,7 +363,7 @@ int eahmmf_hip_moe_layer_decode_async(const eahmmf_hip_moe_shape* shape, const e
     if (!c) return -2;
     if (!grow_device(c->dh, (size_t)k * s.FF * sizeof(float))) return -2;
     hipStream_t st = (hipStream_t)stream;
-    if (fused_enabled() && fused_supported(s, k, n_expert)) {
+    if (fused_enabled() && fused_supported(s, k, n_expert) && grow_fused(c, s)) {
         FusedArgsHost f;
         f.shape = s;
         f.k = k;
@@ -367,6 +377,8 @@ int eahmmf_hip_moe_layer_decode_async(const eahmmf_hip_moe_shape* shape, const e
         f.y = dev_y;
         f.h = (float*)c->dh.p;
         f.sync = c->dsync;
+        f.ypart = (float*)c->dyp.p;
+        f.epoch = ++c->epoch;
         return hip_ok(launch_moe_fused(f, st), "fused moe layer launch") ? 0 : -3;
     }
     // two-step path: routing kernel into scratch (or the caller's buffers), then the expert block
@@ -394,13 +406,16 @@ int eahmmf_hip_set_fused(int enable) {
 int eahmmf_hip_device_flags(void) {
     DevCtx* c = ctx_for_current_device();
     if (!c) return -2;
-    unsigned v[4] = {0, 0, 0, 0};
-    if (!hip_ok(hipMemcpy(v, c->dsync, sizeof v, hipMemcpyDeviceToHost), "read device flags")) return -2;
-    if (v[2]) {
+    if (!hip_ok(hipStreamSynchronize(c->stream), "sync")) return -2;
+    if (!hip_ok(hipDeviceSynchronize(), "device sync")) return -2;
+    unsigned v = 0;
+    if (!hip_ok(hipMemcpy(&v, c->dsync + kSyncFlagWord, sizeof v, hipMemcpyDeviceToHost), "read device flags"))
+        return -2;
+    if (v) {
         const unsigned zero = 0;
-        (void)hipMemcpy(c->dsync + 2, &zero, sizeof zero, hipMemcpyHostToDevice);
+        (void)hipMemcpy(c->dsync + kSyncFlagWord, &zero, sizeof zero, hipMemcpyHostToDevice);
     }
-    return (int)v[2];
+    return (int)v;
 }
 
 bool eahmmf_hip_route_topk(const float* host_logits, int nb, int n_expert, int k, int* host_ids, float* host_w) {
@@ -487,7 +502,7 @@ void eahmmf_hip_shutdown(void) {
     if (it == g_ctx.end()) return;
     DevCtx& c = it->second;
     if (c.stream) (void)hipStreamSynchronize(c.stream);
-    for (DeviceBuf* b : {&c.dx, &c.dy, &c.dy2, &c.dh, &c.dids, &c.dw})
+    for (DeviceBuf* b : {&c.dx, &c.dy, &c.dy2, &c.dh, &c.dids, &c.dw, &c.dyp})
         if (b->p) (void)hipFree(b->p);
     for (DeviceBuf* b : {&c.px, &c.py, &c.py2})
         if (b->p) (void)hipHostFree(b->p);

@@ -63,8 +63,12 @@ struct FusedArgsHost {
     const float* x = nullptr;
     float* y = nullptr;
     float* h = nullptr;           // k * FF floats
-    unsigned* sync = nullptr;     // 3 counters, zero before the first launch
+    float* ypart = nullptr;       // 8 * D floats: per-partition partial outputs
+    unsigned* sync = nullptr;     // kSyncWords counters, zero before the first launch
+    unsigned epoch = 0;           // launch number on this sync buffer, starting at 1
 };
+constexpr int kSyncWords = 4096;
+constexpr int kSyncFlagWord = 1020;  // error flag word inside the sync buffer
 bool fused_supported(const MoeShape& s, int k, int n_expert_for_routing);
 hipError_t launch_moe_fused(const FusedArgsHost& h, hipStream_t st);
 

@@ -1,33 +1,42 @@
-// kernels_fused.hip - one persistent launch per token for the whole MoE
-// expert block: routing -> gate/up + SiLU -> down + router-weighted sum.
+// kernels_fused.hip - one launch per token for the whole MoE expert block:
+// routing -> gate/up + SiLU -> down -> router-weighted sum.
 //
 // This replaces, for one decode token, the reference's host loop
-// (qwen3moe.cpp:1011-1067): softmax/top-k/renormalise, per expert a
-// gate/up pair and a down matmul on the GPU with SiLU and the weighted
-// scatter-add on the CPU, 16 synchronous round trips per layer.
+// (qwen3moe.cpp:1011-1067): softmax/top-k/renormalise, per expert a gate/up
+// pair and a down matmul on the GPU, SiLU and the weighted scatter-add on the
+// CPU, 16 synchronous round trips per layer.
 //
-// The grid is sized to what the device holds at once (occupancy x CUs), so
-// every workgroup is resident and they may wait on each other:
-//   1. wave 0 routes (expf(l - max), top-k with the lower id winning ties,
-//      renormalise in rank order); waves 1-2 quantize x into 3 int8 levels
-//      per 64-value segment (in LDS);
-//   2. phase A: lane groups of min(64, D/64) lanes own one 64-value segment
-//      of x each and walk (expert, row) tasks; each task loads the gate and
-//      up row segments straight from HBM, takes exact int8 dots (v_dot4)
-//      against the activation levels, reduces across the group and stores
-//      h = silu(g) * u;
-//   3. the down-projection row segments each thread will need are issued as
-//      loads before waiting, so they stream from HBM during phase A;
-//   4. h is written with device-coherent stores; a counter incremented once
-//      per workgroup (after its stores completed) releases everyone when the
-//      last workgroup finishes phase A;
-//   5. phase B: threads own (expert, 64-value segment of FF) units, hold that
-//      slice of h in registers (fp32), and produce w_j * down_j[r].h_j per
-//      row; partials are summed in LDS in a fixed order (deterministic) and
-//      y[r] is written once;
-//   6. the last workgroup to finish resets the counters for the next launch.
-// The wait is bounded: if it ever runs out, an error flag is raised and the
-// kernel still exits.
+// Layout of the work.  The routed experts are split into NP partitions (one
+// expert each for k <= 8, k/8 each for k = 16); workgroup b belongs to
+// partition b % NP and is rank q = b / NP inside it.  With NP = 8,
+// consecutive workgroups land on the eight XCDs in turn (checked once per
+// device, and by every workgroup), so a partition lives on one XCD and its
+// slice of h is exchanged through that XCD's L2.  Otherwise h travels with
+// device-coherent stores and loads.
+// Per workgroup (256 threads):
+//   1. wave 0 routes: logits and the expert table are read once, e_i =
+//      expf(l_i - max), top-k by DPP max/min reductions (the lower id wins
+//      ties), renormalised in rank order.  Waves 1-3 turn x into three int8
+//      levels per 64-value segment in LDS.
+//   2. wave 3 copies the down-projection rows this workgroup will need
+//      straight from HBM into LDS (global_load_lds, asynchronous), so they
+//      stream during phase A.
+//   3. phase A on waves 0-2: lane groups of D/64 lanes each own one 64-value
+//      segment of x and walk this workgroup's (expert, row) pairs; gate and up
+//      row segments are loaded straight from HBM into registers, dotted
+//      exactly in int32 (v_dot4) against the activation levels, reduced in
+//      the group, and h = silu(g) * u is stored.
+//   4. partition barrier: one counter per partition, one increment per
+//      workgroup after its stores completed; bounded polling by atomic reads.
+//   5. phase B: the partition's h is read into LDS; threads own (expert,
+//      64-value segment of FF) units, compute w_j * down_j[r].h_j for the
+//      staged rows in fp32, and sum the units of each row in a fixed order
+//      into this partition's partial ypart[p][r].
+//   6. per row chunk, the last of the NP partitions to arrive adds the NP
+//      partials in partition order (deterministic) and writes y.
+// Counters are reset by the last workgroup through each stage, so every
+// launch starts from zero.  Every wait is bounded; if a bound is ever hit an
+// error flag is raised and the kernel still exits.
 #include <mutex>
 
 #include "internal.h"
@@ -35,15 +44,31 @@
 
 namespace eahmmf {
 
-constexpr int kFusedThreads = 192;
+constexpr int kThreads = 256;
+constexpr int kAThreads = 192;  // waves 0-2 run phase A
 constexpr int kMaxD = 4096;
-constexpr int kMaxRowsB = 16;
-constexpr int kPrefetchB = 2;
+constexpr int kMaxE = 256;
+constexpr int kStageB = 32 * 1024;  // LDS bytes for staged down rows
+constexpr int kMaxHP = 4096;        // floats of h held per partition
+constexpr int kMaxPart = 1024;      // (row, unit) partials per round
 constexpr unsigned kSpinLimit = 1u << 22;
+
+// sync buffer layout (unsigned words, kSyncWords in all).  Atomic counters
+// serve the device-coherent protocol; epoch flags serve the XCD-local one.
+constexpr int kSyncArrive = 0, kSyncPass = 8, kSyncChunk = 16, kSyncErr = kSyncFlagWord;
+constexpr int kMaxChunks = 512;
+constexpr int kMaxM = 128;                             // workgroups per partition (epoch flags)
+constexpr int kFlagArrive = 1024, kFlagChunk = 2048;  // [8][kMaxM] each
+static_assert(kSyncChunk + kMaxChunks <= kSyncErr && kFlagChunk + 8 * kMaxM <= kSyncWords, "sync layout");
 
 struct FusedArgs {
     MoeShape s;
     int k, n_expert, mode;  // mode 0: direct slots, 1: logits + table, 2: ids/w + table
+    int np, m;              // partitions and workgroups per partition
+    int rows_b;             // output rows per workgroup (chunk)
+    int round_b;            // rows staged per phase-B round
+    int local_l2;           // 1: partition p runs on XCD p, so h is exchanged through that XCD's L2
+    unsigned epoch;         // launch number (>= 1): the value this launch's flags carry
     DecodeSlots direct;
     const ExpertEntry* table;
     const float* logits;
@@ -53,8 +78,9 @@ struct FusedArgs {
     float* w_out;
     const float* x;
     float* y;
-    float* h;
-    unsigned* sync;  // [0] phase-A done, [1] finished, [2] error flag
+    float* h;      // k * FF
+    float* ypart;  // np * D
+    unsigned* sync;
 };
 
 template <int CTRL, int ROWS>
@@ -93,18 +119,48 @@ __device__ __forceinline__ int dpp_min_int(int v) {
     return __builtin_amdgcn_readlane(v, 63);
 }
 
-// Device-coherent (sc1) store: written through past the XCD's L2, so no
-// whole-cache writeback is needed before other XCDs may read it.
+// Device-coherent (sc1) accesses: visible across the XCDs' separate L2s
+// without whole-cache writeback or invalidate.
 __device__ __forceinline__ void store_coherent(float* p, float v) {
     __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
-// s_waitcnt vmcnt(0): this wave's stores have completed (gfx9 encoding:
-// vmcnt 0, expcnt 7, lgkmcnt 15).  Compiler fences keep the stores before it.
-__device__ __forceinline__ void wait_stores() {
+__device__ __forceinline__ float load_coherent(const float* p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ unsigned load_counter(const unsigned* p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ unsigned bump_counter(unsigned* p) {
+    return __hip_atomic_fetch_add(p, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void reset_counter(unsigned* p) {
+    __hip_atomic_store(p, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// s_waitcnt vmcnt(0): this wave's memory operations have completed (gfx9
+// encoding: vmcnt 0, expcnt 7, lgkmcnt 15).  Compiler fences keep the
+// stores before it.
+__device__ __forceinline__ void wait_vm() {
     __atomic_signal_fence(__ATOMIC_SEQ_CST);
     __builtin_amdgcn_s_waitcnt(0x0F70);
     __atomic_signal_fence(__ATOMIC_SEQ_CST);
 }
+
+// Current value of a counter read with an atomic read-modify-write: it is
+// served where the increments are performed, never from a stale cached copy.
+__device__ __forceinline__ unsigned poll_counter(unsigned* p) {
+    return __hip_atomic_fetch_add(p, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Load that bypasses the CU's L1 (sc0) and is served by the XCD's L2: sees
+// every store another CU of the same XCD has completed.
+__device__ __forceinline__ unsigned load_l2(const unsigned* p) {
+    const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(const_cast<unsigned*>(p), 0, 4, 0x00020000);
+    return __builtin_amdgcn_raw_buffer_load_b32(r, 0, 0, 1);
+}
+
+// XCD (XCC) the calling wave runs on: hardware register HW_REG_XCC_ID (20),
+// bits [3:0].
+__device__ __forceinline__ int xcc_id() { return (int)(__builtin_amdgcn_s_getreg(20 | (0 << 6) | (3 << 11)) & 0xF); }
 
 template <int W>
 __device__ __forceinline__ float group_sum(float v) {
@@ -113,24 +169,27 @@ __device__ __forceinline__ float group_sum(float v) {
     return v;
 }
 
-constexpr int kMaxH = 16384;  // k * FF floats held in LDS during phase B
-
 struct alignas(16) FusedLds {
+    uint8_t bstage[kStageB];  // first member: 16-byte aligned
     union {
-        struct {  // phase A: activation levels
+        struct {  // steps 1-3: activation levels
             int8_t xq[kLevels][kMaxD];
             float xsc[kLevels][kMaxD / 64];
             float xs32[kMaxD / 32];
         } a;
-        struct {  // phase B: h and the row partials
-            float h[kMaxH];
-            float part[kFusedThreads * kMaxRowsB];
+        struct {  // step 5: the partition's h as int8 levels, and (row, unit) partials
+            int8_t hq[kLevels][kMaxHP];
+            float hsc[kLevels][kMaxHP / 64];
+            float hs32[kMaxHP / 32];
+            float part[kMaxPart];
         } b;
     };
+    ExpertEntry table[kMaxE];
     const uint8_t* gate[kMaxSlots];
     const uint8_t* up[kMaxSlots];
     const uint8_t* down[kMaxSlots];
     float w[kMaxSlots];
+    int flag;
 };
 
 // Route one token with wave 0 (n_expert <= 256).  Results into LDS.
@@ -142,6 +201,7 @@ __device__ void route_wave(const FusedArgs& a, FusedLds& L) {
     for (int i = 0; i < 4; i++) {
         const int id = lane + 64 * i;
         e[i] = id < a.n_expert ? a.logits[id] : -INFINITY;
+        if (id < a.n_expert) L.table[id] = a.table[id];
         mx = fmaxf(mx, e[i]);
     }
     mx = dpp_max(mx);
@@ -150,8 +210,8 @@ __device__ void route_wave(const FusedArgs& a, FusedLds& L) {
         const int id = lane + 64 * i;
         e[i] = id < a.n_expert ? expf(e[i] - mx) : -1.0f;
     }
-    float tot = 0.f;
-    float mine = 0.f;  // lane r keeps the r-th chosen e
+    float tot = 0.f, mine = 0.f;  // lane r keeps the r-th chosen e and id
+    int myid = -1;
     for (int r = 0; r < a.k; r++) {
         float be = -2.0f;
         int bi = 0x7fffffff;
@@ -163,42 +223,53 @@ __device__ void route_wave(const FusedArgs& a, FusedLds& L) {
 #pragma unroll
         for (int i = 0; i < 4; i++)
             if (lane + 64 * i == id) e[i] = -1.0f;
-        if (lane == r) mine = m;
-        tot += m;  // rank order, as the reference sums
-        if (lane == 0) {
-            // NaN logits can leave no candidate: that slot then contributes nothing
-            const bool valid = id >= 0 && id < a.n_expert;
-            const ExpertEntry ent = valid ? a.table[id] : ExpertEntry{nullptr, nullptr, nullptr};
-            L.gate[r] = ent.gate;
-            L.up[r] = ent.up;
-            L.down[r] = ent.down;
-            if (a.ids_out && blockIdx.x == 0) a.ids_out[r] = valid ? id : -1;
+        if (lane == r) {
+            mine = m;
+            myid = id;
         }
+        tot += m;  // rank order, as the reference sums
     }
     if (lane < a.k) {
-        const float wr = mine / tot;
+        // NaN logits can leave a slot without a candidate: it then contributes nothing
+        const bool valid = myid >= 0 && myid < a.n_expert;
+        const ExpertEntry ent = valid ? L.table[myid] : ExpertEntry{nullptr, nullptr, nullptr};
+        L.gate[lane] = ent.gate;
+        L.up[lane] = ent.up;
+        L.down[lane] = ent.down;
+        const float wr = valid ? mine / tot : 0.f;
         L.w[lane] = wr;
-        if (a.w_out && blockIdx.x == 0) a.w_out[lane] = wr;
+        if (blockIdx.x == 0) {
+            if (a.ids_out) a.ids_out[lane] = valid ? myid : -1;
+            if (a.w_out) a.w_out[lane] = wr;
+        }
     }
 }
 
-// x (fp32, D) -> 3 int8 levels per 64-value segment + 32-value sums, into LDS.
-// Eight threads per segment, eight values each; threads [t0, t0+nthr).
-__device__ void quantize_x(const FusedArgs& a, FusedLds& L, int t, int nthr) {
-    const int D = a.s.D;
-    const int nseg = D / 64;
+// n fp32 values (n % 64 == 0) -> 3 int8 levels per 64-value segment and
+// 32-value sums, into LDS: level lv of value i at q + lv*qstride + i, scale
+// of segment g at sc + lv*scstride + g, sum of values [32c, 32c+32) at s32[c].
+// Eight threads per segment, eight values each; threads t in [0, nthr).
+template <bool COHERENT>
+__device__ void quantize_levels(const float* src, int n, int8_t* q, int qstride, float* sc, int scstride, float* s32,
+                                int t, int nthr) {
+    const int nseg = n / 64;
     const int per_pass = nthr / 8;
     for (int base = 0; base < nseg; base += per_pass) {
         const int seg = base + t / 8;
         const int part = t % 8;
-        const bool active = seg < nseg && t < per_pass * 8;
+        const bool active = seg < nseg;
         float v[8];
         float amax = 0.f, sum = 0.f;
         if (active) {
-            const float4* p = reinterpret_cast<const float4*>(a.x + seg * 64 + part * 8);
-            const float4 v0 = p[0], v1 = p[1];
-            v[0] = v0.x; v[1] = v0.y; v[2] = v0.z; v[3] = v0.w;
-            v[4] = v1.x; v[5] = v1.y; v[6] = v1.z; v[7] = v1.w;
+            const float* sp = src + seg * 64 + part * 8;
+            if (COHERENT) {
+#pragma unroll
+                for (int i = 0; i < 8; i++) v[i] = __hip_atomic_load(sp + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            } else {
+                const float4 v0 = reinterpret_cast<const float4*>(sp)[0], v1 = reinterpret_cast<const float4*>(sp)[1];
+                v[0] = v0.x; v[1] = v0.y; v[2] = v0.z; v[3] = v0.w;
+                v[4] = v1.x; v[5] = v1.y; v[6] = v1.z; v[7] = v1.w;
+            }
 #pragma unroll
             for (int i = 0; i < 8; i++) {
                 amax = fmaxf(amax, fabsf(v[i]));
@@ -217,220 +288,313 @@ __device__ void quantize_x(const FusedArgs& a, FusedLds& L, int t, int nthr) {
         if (active) {
             const float s1 = amax / 127.0f;
             const float s2 = s1 / 254.0f, s3 = s2 / 254.0f;
-            const float sc[kLevels] = {s1, s2, s3};
+            const float lsc[kLevels] = {s1, s2, s3};
             float r[8];
 #pragma unroll
             for (int i = 0; i < 8; i++) r[i] = v[i];
 #pragma unroll
             for (int lv = 0; lv < kLevels; lv++) {
-                const float inv = sc[lv] > 0.f ? 1.0f / sc[lv] : 0.f;
+                const float inv = lsc[lv] > 0.f ? 1.0f / lsc[lv] : 0.f;
                 uint32_t packed[2] = {0u, 0u};
 #pragma unroll
                 for (int i = 0; i < 8; i++) {
                     float qf = __builtin_rintf(r[i] * inv);
                     qf = fminf(127.f, fmaxf(-127.f, qf));
-                    r[i] = __builtin_fmaf(-qf, sc[lv], r[i]);
+                    r[i] = __builtin_fmaf(-qf, lsc[lv], r[i]);
                     packed[i >> 2] |= ((uint32_t)(int)qf & 0xFFu) << (8 * (i & 3));
                 }
-                *reinterpret_cast<uint2*>(&L.a.xq[lv][seg * 64 + part * 8]) = make_uint2(packed[0], packed[1]);
-                if (part == 0) L.a.xsc[lv][seg] = sc[lv];
+                *reinterpret_cast<uint2*>(q + lv * qstride + seg * 64 + part * 8) = make_uint2(packed[0], packed[1]);
+                if (part == 0) sc[lv * scstride + seg] = lsc[lv];
             }
-            if ((part & 3) == 0) L.a.xs32[seg * 2 + part / 4] = sum;
+            if ((part & 3) == 0) s32[seg * 2 + part / 4] = sum;
         }
     }
 }
+
+// The activation levels of segment g (64 values) held by one lane.
+__device__ __forceinline__ void load_xseg(XSeg& xs, const int8_t* q, int qstride, const float* sc, int scstride,
+                                          const float* s32, int g) {
+#pragma unroll
+    for (int lv = 0; lv < kLevels; lv++) {
+        const uint4* xp = reinterpret_cast<const uint4*>(q + lv * qstride + g * 64);
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+            const uint4 v = xp[c];
+            xs.q[lv][4 * c] = (int)v.x; xs.q[lv][4 * c + 1] = (int)v.y;
+            xs.q[lv][4 * c + 2] = (int)v.z; xs.q[lv][4 * c + 3] = (int)v.w;
+        }
+        xs.s[lv] = sc[lv * scstride + g];
+    }
+    xs.sum32[0] = s32[2 * g];
+    xs.sum32[1] = s32[2 * g + 1];
+}
+
+// Copy global bytes [src, src_end) into LDS at dst, one wave, 16 bytes per
+// lane per instruction.  The copy covers src rounded down to 16 bytes up to
+// src_end rounded up, so every access is an aligned 16-byte block inside the
+// pages that hold the range.  src's offset inside the copy is src & 15.
+__device__ __forceinline__ void stage_range(const uint8_t* src, const uint8_t* src_end, uint8_t* dst, int lane) {
+    const uintptr_t a = (uintptr_t)src & ~(uintptr_t)15;
+    const uintptr_t z = ((uintptr_t)src_end + 15) & ~(uintptr_t)15;
+    const int n16 = (int)((z - a) / 16);
+    for (int base = 0; base < n16; base += 64) {
+        // the LDS slot of lane i is dst + base*16 + 16*i; lanes past the end stay idle
+        if (base + lane < n16)
+            __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(a + (uintptr_t)(base + lane) * 16),
+                                             (__attribute__((address_space(3))) void*)(dst + base * 16), 16, 0, 0);
+    }
+}
+
+// LDS bytes reserved per expert for one staged round of rows (16-byte
+// rounding slack at both ends).
+__host__ __device__ inline int stage_stride(int rows, int row_bytes) { return ((rows * row_bytes + 15) / 16 + 1) * 16; }
 
 template <int LA, int GT, int UT, int DT>
 __device__ void fused_body(const FusedArgs& a, FusedLds& L) {
     const int tid = threadIdx.x;
+    const int wave = tid / 64, lane = tid % 64;
     const MoeShape& s = a.s;
     const int D = s.D, FF = s.FF, k = a.k;
-    const int nwg = gridDim.x;
+    const int np = a.np, m = a.m;
+    const int p = blockIdx.x % np, q = blockIdx.x / np;
+    const int ep = k / np;  // experts per partition
+    const int segB = FF / 64;
+    const int UP = ep * segB;  // units of the partition
+    const int drb = (int)s.down_rb;
 
-    // ---- 1. routing / slots and activation levels
-    if (a.mode == 1) {
-        if (tid < 64) route_wave(a, L);
-        else quantize_x(a, L, tid - 64, kFusedThreads - 64);
-    } else {
-        if (tid < k) {
+    // ---- 1. routing / slots (wave 0) and activation levels (waves 1-3)
+    if (wave == 0) {
+        if (a.mode == 1) {
+            route_wave(a, L);
+        } else if (lane < k) {
             if (a.mode == 0) {
-                L.gate[tid] = a.direct.gate[tid];
-                L.up[tid] = a.direct.up[tid];
-                L.down[tid] = a.direct.down[tid];
-                L.w[tid] = a.direct.w[tid];
+                L.gate[lane] = a.direct.gate[lane];
+                L.up[lane] = a.direct.up[lane];
+                L.down[lane] = a.direct.down[lane];
+                L.w[lane] = a.direct.w[lane];
             } else {
-                const int id = a.ids_in[tid];
+                const int id = a.ids_in[lane];
                 const bool ok = id >= 0 && id < a.n_expert;
                 const ExpertEntry ent = ok ? a.table[id] : ExpertEntry{nullptr, nullptr, nullptr};
-                L.gate[tid] = ent.gate;
-                L.up[tid] = ent.up;
-                L.down[tid] = ent.down;
-                L.w[tid] = ok ? a.w_in[tid] : 0.f;
+                L.gate[lane] = ent.gate;
+                L.up[lane] = ent.up;
+                L.down[lane] = ent.down;
+                L.w[lane] = ok ? a.w_in[lane] : 0.f;
             }
         }
-        quantize_x(a, L, tid, kFusedThreads);
+    } else {
+        quantize_levels<false>(a.x, D, &L.a.xq[0][0], kMaxD, &L.a.xsc[0][0], kMaxD / 64, L.a.xs32, tid - 64,
+                               kThreads - 64);
     }
     __syncthreads();
 
-    // ---- phase-B assignment and prefetch of the down rows (independent of h)
-    const int segB = FF / 64;
-    const int U = k * segB;
-    const int S = kFusedThreads / U;  // row slots per workgroup
-    const bool b_active = tid < S * U;
-    const int slot = tid / U, unit = tid % U;
-    const int bj = unit / segB, bseg = unit % segB;
-    const int NS = nwg * S;
-    const int gslot = blockIdx.x * S + slot;
-    const int RB = (D + NS - 1) / NS;
-    const uint8_t* bdown = b_active ? L.down[bj] : nullptr;
-    RawSeg<DT> pre[kPrefetchB];
-#pragma unroll
-    for (int i = 0; i < kPrefetchB; i++) {
-        const int r = gslot + i * NS;
-        if (b_active && bdown && i < RB && r < D) pre[i].load(bdown + (size_t)r * s.down_rb, bseg);
-    }
+    // output rows of this workgroup's chunk, staged in rounds of round_b rows
+    const int r_begin = q * a.rows_b;
+    const int r_end = min(D, r_begin + a.rows_b);
+    const int round_rows = a.round_b;
+    const int stride_e = stage_stride(round_rows, drb);
+    auto issue_stage = [&](int r0) {  // wave 3 only
+        const int r1 = min(r_end, r0 + round_rows);
+        for (int e = 0; e < ep; e++) {
+            const uint8_t* dw = L.down[p * ep + e];
+            if (dw && r1 > r0)
+                stage_range(dw + (size_t)r0 * drb, dw + (size_t)r1 * drb, L.bstage + e * stride_e, lane);
+        }
+    };
 
-    // ---- 2. phase A
-    constexpr int GA = kFusedThreads / LA;
-    const int grp = tid / LA, li = tid % LA;
-    XSeg xs;
-#pragma unroll
-    for (int lv = 0; lv < kLevels; lv++) {
-        const uint4* p = reinterpret_cast<const uint4*>(&L.a.xq[lv][li * 64]);
-#pragma unroll
-        for (int q = 0; q < 4; q++) {
-            const uint4 v = p[q];
-            xs.q[lv][4 * q] = (int)v.x; xs.q[lv][4 * q + 1] = (int)v.y;
-            xs.q[lv][4 * q + 2] = (int)v.z; xs.q[lv][4 * q + 3] = (int)v.w;
-        }
-        xs.s[lv] = L.a.xsc[lv][li];
-    }
-    xs.sum32[0] = L.a.xs32[2 * li];
-    xs.sum32[1] = L.a.xs32[2 * li + 1];
-    const int P = k * FF;
-    const int NG = nwg * GA;
-    for (int t0 = blockIdx.x * GA + grp; t0 < P; t0 += 2 * NG) {
-        const int t1 = t0 + NG;
-        const bool has1 = t1 < P;
-        RawSeg<GT> g0, g1;
-        RawSeg<UT> u0, u1;
-        const int j0 = t0 / FF, f0 = t0 % FF;
-        const int j1 = has1 ? t1 / FF : j0, f1 = has1 ? t1 % FF : f0;
-        const bool ok0 = L.gate[j0] && L.up[j0];
-        const bool ok1 = has1 && L.gate[j1] && L.up[j1];
-        if (ok0) {
-            g0.load(L.gate[j0] + (size_t)f0 * s.gate_rb, li);
-            u0.load(L.up[j0] + (size_t)f0 * s.up_rb, li);
-        }
-        if (ok1) {
-            g1.load(L.gate[j1] + (size_t)f1 * s.gate_rb, li);
-            u1.load(L.up[j1] + (size_t)f1 * s.up_rb, li);
-        }
-        float dg0 = ok0 ? g0.dot_q8(li, xs) : 0.f;
-        float du0 = ok0 ? u0.dot_q8(li, xs) : 0.f;
-        float dg1 = ok1 ? g1.dot_q8(li, xs) : 0.f;
-        float du1 = ok1 ? u1.dot_q8(li, xs) : 0.f;
-        dg0 = group_sum<LA>(dg0);
-        du0 = group_sum<LA>(du0);
-        dg1 = group_sum<LA>(dg1);
-        du1 = group_sum<LA>(du1);
-        if (li == 0) {
-            store_coherent(&a.h[t0], dg0 / (1.0f + expf(-dg0)) * du0);
-            if (has1) store_coherent(&a.h[t1], dg1 / (1.0f + expf(-dg1)) * du1);
+    // ---- 2. wave 3 stages the first round of down rows into LDS
+    if (wave == 3) issue_stage(r_begin);
+
+    // ---- 3. phase A on waves 0-2
+    if (wave < 3) {
+        constexpr int GA = kAThreads / LA;
+        const int grp = tid / LA, li = tid % LA;
+        XSeg xs;
+        load_xseg(xs, &L.a.xq[0][0], kMaxD, &L.a.xsc[0][0], kMaxD / 64, L.a.xs32, li);
+        // this workgroup's rows of the partition: [ra0, ra1) over ep * FF
+        const int rows_a = ep * FF;
+        const int per_wg = (rows_a + m - 1) / m;
+        const int ra0 = q * per_wg, ra1 = min(rows_a, ra0 + per_wg);
+        for (int t0 = ra0 + grp; t0 < ra1; t0 += 2 * GA) {
+            const int t1 = t0 + GA;
+            const bool has1 = t1 < ra1;
+            const int j0 = p * ep + t0 / FF, f0 = t0 % FF;
+            const int j1 = has1 ? p * ep + t1 / FF : j0, f1 = has1 ? t1 % FF : f0;
+            const bool ok0 = L.gate[j0] && L.up[j0];
+            const bool ok1 = has1 && L.gate[j1] && L.up[j1];
+            RawSeg<GT> g0, g1;
+            RawSeg<UT> u0, u1;
+            if (ok0) {
+                g0.load(L.gate[j0] + (size_t)f0 * s.gate_rb, li);
+                u0.load(L.up[j0] + (size_t)f0 * s.up_rb, li);
+            }
+            if (ok1) {
+                g1.load(L.gate[j1] + (size_t)f1 * s.gate_rb, li);
+                u1.load(L.up[j1] + (size_t)f1 * s.up_rb, li);
+            }
+            float dg0 = ok0 ? g0.dot_q8(li, xs) : 0.f;
+            float du0 = ok0 ? u0.dot_q8(li, xs) : 0.f;
+            float dg1 = ok1 ? g1.dot_q8(li, xs) : 0.f;
+            float du1 = ok1 ? u1.dot_q8(li, xs) : 0.f;
+            dg0 = group_sum<LA>(dg0);
+            du0 = group_sum<LA>(du0);
+            dg1 = group_sum<LA>(dg1);
+            du1 = group_sum<LA>(du1);
+            if (li == 0) {
+                const float h0 = dg0 / (1.0f + expf(-dg0)) * du0;
+                const float h1 = dg1 / (1.0f + expf(-dg1)) * du1;
+                if (a.local_l2) {  // the partition's readers share this XCD's L2
+                    a.h[j0 * FF + f0] = h0;
+                    if (has1) a.h[j1 * FF + f1] = h1;
+                } else {
+                    store_coherent(&a.h[j0 * FF + f0], h0);
+                    if (has1) store_coherent(&a.h[j1 * FF + f1], h1);
+                }
+            }
         }
     }
 
-    // ---- 4. grid-wide hand-off from phase A to phase B.  h went out with
-    // device-coherent stores; each wave waits for its stores to complete,
-    // then one counter increment per workgroup; polling uses device-coherent
-    // loads (no cache maintenance inside the loop).
-    wait_stores();
+    // ---- 4. partition barrier (h complete for partition p)
+    wait_vm();  // h stores of waves 0-2 and the staging copies of wave 3 have completed
     __syncthreads();
-    if (tid == 0) {
-        __hip_atomic_fetch_add(&a.sync[0], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (a.local_l2) {
+        // every workgroup of the partition publishes the launch epoch in its own
+        // flag word (a plain store into this XCD's L2); wave 0 watches all m flags
+        if (tid == 0) {
+            if (xcc_id() != p)  // the partition-to-XCD mapping this exchange relies on
+                __hip_atomic_store(&a.sync[kSyncErr], 2u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            a.sync[kFlagArrive + p * kMaxM + q] = a.epoch;
+        }
+        if (wave == 0) {
+            unsigned spins = 0;
+            for (;;) {
+                const bool mine = lane >= m || load_l2(&a.sync[kFlagArrive + p * kMaxM + lane]) == a.epoch;
+                if (__all(mine)) break;
+                __builtin_amdgcn_s_sleep(1);
+                if (++spins == kSpinLimit) {
+                    if (lane == 0) __hip_atomic_store(&a.sync[kSyncErr], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    break;
+                }
+            }
+        }
+    } else if (tid == 0) {
+        bump_counter(&a.sync[kSyncArrive + p]);
         unsigned spins = 0;
-        while (__hip_atomic_load(&a.sync[0], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < (unsigned)nwg) {
-            __builtin_amdgcn_s_sleep(4);
+        while (poll_counter(&a.sync[kSyncArrive + p]) < (unsigned)m) {
+            __builtin_amdgcn_s_sleep(2);
             if (++spins == kSpinLimit) {
-                __hip_atomic_store(&a.sync[2], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                __hip_atomic_store(&a.sync[kSyncErr], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                 break;
             }
         }
+        if (bump_counter(&a.sync[kSyncPass + p]) == (unsigned)m - 1) {  // everyone has passed: reset
+            reset_counter(&a.sync[kSyncArrive + p]);
+            reset_counter(&a.sync[kSyncPass + p]);
+        }
     }
-    // one L2/L1 invalidate per workgroup, then h is read with ordinary cached
-    // loads: the first workgroup of each XCD brings it into that XCD's L2
-    if (tid == 0) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-    __syncthreads();
-    {
-        const int nh4 = k * FF / 4;
-        const float4* src = reinterpret_cast<const float4*>(a.h);
-        float4* dst = reinterpret_cast<float4*>(L.b.h);
-        for (int i = tid; i < nh4; i += kFusedThreads) dst[i] = src[i];
-    }
-    __syncthreads();
+    __syncthreads();  // the activation levels are dead from here: the LDS union switches to phase B
 
-    // ---- 5. phase B
+    // ---- 5. phase B: the partition's h as int8 levels (read from L2 when the
+    // partition shares an XCD, with device-coherent loads otherwise)
+    const int hn = ep * FF;
+    if (a.local_l2)
+        quantize_levels<false>(a.h + p * ep * FF, hn, &L.b.hq[0][0], kMaxHP, &L.b.hsc[0][0], kMaxHP / 64, L.b.hs32,
+                               tid, kThreads);
+    else
+        quantize_levels<true>(a.h + p * ep * FF, hn, &L.b.hq[0][0], kMaxHP, &L.b.hsc[0][0], kMaxHP / 64, L.b.hs32,
+                              tid, kThreads);
+    __syncthreads();
+    const int slots = kThreads / UP;
+    const bool b_active = tid < slots * UP;
+    const int slot = tid / UP, unit = tid % UP;
+    const int be = unit / segB, bseg = unit % segB;  // expert within the partition, segment
+    XSeg hs;
+    float wj = 0.f;
+    const uint8_t* dexp = nullptr;
     if (b_active) {
-        float hv[64];
-        const float4* hp = reinterpret_cast<const float4*>(&L.b.h[bj * FF + bseg * 64]);
-#pragma unroll
-        for (int q = 0; q < 16; q++) {
-            const float4 v = hp[q];
-            hv[4 * q] = v.x; hv[4 * q + 1] = v.y; hv[4 * q + 2] = v.z; hv[4 * q + 3] = v.w;
-        }
-        constexpr int NSUM = SumSpan<DT>::n > 0 ? SumSpan<DT>::n : 1;
-        float hsum[NSUM];
-#pragma unroll
-        for (int g = 0; g < NSUM; g++) {
-            float acc = 0.f;
-            if (SumSpan<DT>::n > 0) {
-#pragma unroll
-                for (int i = 0; i < SumSpan<DT>::width; i++) acc += hv[g * SumSpan<DT>::width + i];
-            }
-            hsum[g] = acc;
-        }
-        const float wj = L.w[bj];
-        for (int i = 0; i < RB && i < kMaxRowsB; i++) {
-            const int r = gslot + i * NS;
-            float part = 0.f;
-            if (r < D && bdown) {
-                RawSeg<DT> raw;
-                if (i < kPrefetchB) raw = pre[i];
-                else raw.load(bdown + (size_t)r * s.down_rb, bseg);
-                part = wj * raw.dot_f32(bseg, hv, hsum);
-            }
-            L.b.part[(slot * kMaxRowsB + i) * U + unit] = part;
-        }
+        load_xseg(hs, &L.b.hq[0][0], kMaxHP, &L.b.hsc[0][0], kMaxHP / 64, L.b.hs32, be * segB + bseg);
+        wj = L.w[p * ep + be];
+        dexp = L.down[p * ep + be];
     }
-    __syncthreads();
-    // reduce partials: wave w takes (slot, row) pairs w, w+3, ...
-    {
-        const int wave = tid / 64, lane = tid % 64;
-        const int pairs = S * min(RB, kMaxRowsB);
-        for (int pi = wave; pi < pairs; pi += kFusedThreads / 64) {
-            const int sl = pi / min(RB, kMaxRowsB), i = pi % min(RB, kMaxRowsB);
-            const int r = blockIdx.x * S + sl + i * NS;
-            const float* pp = &L.b.part[(sl * kMaxRowsB + i) * U];
+    for (int r0 = r_begin; r0 < r_end; r0 += round_rows) {
+        const int rr = min(round_rows, r_end - r0);
+        if (r0 != r_begin) {  // later rounds: stage now into the single buffer
+            __syncthreads();
+            if (wave == 3) issue_stage(r0);
+            wait_vm();
+            __syncthreads();
+        }
+        if (b_active && dexp) {
+            // row r0 of this expert starts (src & 15) bytes into its staged copy
+            const uint8_t* rows = L.bstage + be * stride_e + (int)((uintptr_t)(dexp + (size_t)r0 * drb) & 15);
+            for (int i = slot; i < rr; i += slots) {
+                RawSeg<DT> raw;
+                raw.load(rows + i * drb, bseg);
+                L.b.part[i * UP + unit] = wj * raw.dot_q8(bseg, hs);
+            }
+        } else if (b_active) {
+            for (int i = slot; i < rr; i += slots) L.b.part[i * UP + unit] = 0.f;
+        }
+        __syncthreads();
+        // fixed-order sum over the partition's units, one thread per row
+        for (int i = tid; i < rr; i += kThreads) {
             float v = 0.f;
-            for (int u = lane; u < U; u += 64) v += pp[u];
-            v = group_sum<64>(v);
-            if (lane == 0 && r < D) a.y[r] = v;
+            for (int u = 0; u < UP; u++) v += L.b.part[i * UP + u];
+            store_coherent(&a.ypart[p * D + r0 + i], v);
         }
     }
 
-    // ---- 6. the last workgroup out resets the counters for the next launch
+    // ---- 6. combine the partitions' partials of this row chunk into y
+    wait_vm();
     __syncthreads();
-    if (tid == 0) {
-        const unsigned done = __hip_atomic_fetch_add(&a.sync[1], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        if (done == (unsigned)nwg - 1) {
-            __hip_atomic_store(&a.sync[0], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            __hip_atomic_store(&a.sync[1], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (a.local_l2) {
+        // partition q % 8 reduces chunk q once all eight partials carry this epoch
+        if (tid == 0)
+            __hip_atomic_store(&a.sync[kFlagChunk + p * kMaxM + q], a.epoch, __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
+        if (p == q % np) {
+            if (wave == 0) {
+                unsigned spins = 0;
+                for (;;) {
+                    const bool mine =
+                        lane >= np || __hip_atomic_load(&a.sync[kFlagChunk + lane * kMaxM + q], __ATOMIC_RELAXED,
+                                                        __HIP_MEMORY_SCOPE_AGENT) == a.epoch;
+                    if (__all(mine)) break;
+                    __builtin_amdgcn_s_sleep(1);
+                    if (++spins == kSpinLimit) {
+                        if (lane == 0)
+                            __hip_atomic_store(&a.sync[kSyncErr], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                        break;
+                    }
+                }
+            }
+            __syncthreads();
+            for (int r = r_begin + tid; r < r_end; r += kThreads) {
+                float v = 0.f;
+                for (int pp = 0; pp < np; pp++) v += load_coherent(&a.ypart[pp * D + r]);
+                a.y[r] = v;
+            }
+        }
+    } else {
+        // the last partition to finish this row chunk writes y
+        if (tid == 0) {
+            const unsigned done = bump_counter(&a.sync[kSyncChunk + q]);  // returns the coherent count
+            L.flag = done == (unsigned)np - 1;
+            if (L.flag) reset_counter(&a.sync[kSyncChunk + q]);
+        }
+        __syncthreads();
+        if (L.flag) {
+            for (int r = r_begin + tid; r < r_end; r += kThreads) {
+                float v = 0.f;
+                for (int pp = 0; pp < np; pp++) v += load_coherent(&a.ypart[pp * D + r]);
+                a.y[r] = v;
+            }
         }
     }
 }
 
 template <int LA, int GT, int UT, int DT>
-__global__ __launch_bounds__(kFusedThreads) void moe_decode_fused(FusedArgs a) {
+__global__ __launch_bounds__(kThreads) void moe_decode_fused(FusedArgs a) {
     __shared__ FusedLds L;
     fused_body<LA, GT, UT, DT>(a, L);
 }
@@ -479,34 +643,75 @@ static FusedFn pick_fused(const MoeShape& s) {
     }
 }
 
+static int partitions_for(int k) { return k <= 8 ? k : (k % 8 == 0 ? 8 : 0); }
+
 bool fused_supported(const MoeShape& s, int k, int n_expert_for_routing) {
     if (!moe_shape_ok(s) || k <= 0 || k > kMaxSlots) return false;
     if (s.D % 64 || s.FF % 64 || s.D > kMaxD) return false;
     if (!pick_fused(s)) return false;
-    const int U = k * (s.FF / 64);
-    if (U > kFusedThreads || k * s.FF > kMaxH) return false;
-    if (n_expert_for_routing > 256) return false;
+    const int np = partitions_for(k);
+    if (!np) return false;
+    const int ep = k / np;
+    const int UP = ep * (s.FF / 64);
+    if (UP > kThreads || ep * s.FF > kMaxHP || UP > kMaxPart) return false;
+    if (n_expert_for_routing > kMaxE) return false;
+    if (ep * stage_stride(1, (int)s.down_rb) > kStageB) return false;  // one staged row per expert must fit
     return true;
 }
 
-// Grid size: every workgroup must be resident at once.  The
-// occupancy answer is cached per kernel and device.
-static int fused_grid(FusedFn fn, int device) {
-    struct Entry { FusedFn fn; int device, grid; };
-    static Entry cache[64];
+struct GridInfo {
+    int cus = 0, per_cu = 0;
+};
+
+// Workgroups resident at once on the device (occupancy x CUs), cached per
+// kernel and device.
+static GridInfo fused_capacity(FusedFn fn, int device) {
+    struct Entry {
+        FusedFn fn;
+        int device;
+        GridInfo g;
+    };
+    static Entry cache[128];
     static int n = 0;
     static std::mutex mu;
-    std::lock_guard<std::mutex> g(mu);
+    std::lock_guard<std::mutex> lk(mu);
     for (int i = 0; i < n; i++)
-        if (cache[i].fn == fn && cache[i].device == device) return cache[i].grid;
-    int cus = 0, occ = 0;
-    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess) return 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, reinterpret_cast<const void*>(fn), kFusedThreads, 0) !=
+        if (cache[i].fn == fn && cache[i].device == device) return cache[i].g;
+    GridInfo g;
+    int occ = 0;
+    if (hipDeviceGetAttribute(&g.cus, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess) return GridInfo{};
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, reinterpret_cast<const void*>(fn), kThreads, 0) !=
         hipSuccess)
-        return 0;
-    const int grid = (occ < 2 ? occ : 2) * cus;
-    if (n < 64) cache[n++] = Entry{fn, device, grid};
-    return grid;
+        return GridInfo{};
+    g.per_cu = occ < 2 ? occ : 2;
+    if (n < 128) cache[n++] = Entry{fn, device, g};
+    return g;
+}
+
+__global__ void xcc_probe_kernel(int* out) {
+    if (threadIdx.x == 0) out[blockIdx.x] = xcc_id();
+}
+
+// One-time check per device that workgroup b of a plain launch runs on XCD
+// b % 8 (the round-robin dispatch the XCD-local exchange relies on).
+static bool xcd_round_robin(int device) {
+    static int state[64];  // 0 unknown, 1 yes, 2 no
+    static std::mutex mu;
+    std::lock_guard<std::mutex> lk(mu);
+    if (device < 0 || device >= 64) return false;
+    if (state[device]) return state[device] == 1;
+    state[device] = 2;
+    constexpr int kProbe = 1024;
+    int* d = nullptr;
+    if (hipMalloc(&d, kProbe * sizeof(int)) != hipSuccess) return false;
+    hipLaunchKernelGGL(xcc_probe_kernel, dim3(kProbe), dim3(64), 0, nullptr, d);
+    int hbuf[kProbe];
+    bool ok = hipGetLastError() == hipSuccess &&
+              hipMemcpy(hbuf, d, sizeof hbuf, hipMemcpyDeviceToHost) == hipSuccess;
+    (void)hipFree(d);
+    for (int b = 0; ok && b < kProbe; b++) ok = hbuf[b] == b % 8;
+    if (ok) state[device] = 1;
+    return ok;
 }
 
 hipError_t launch_moe_fused(const FusedArgsHost& h, hipStream_t st) {
@@ -525,21 +730,37 @@ hipError_t launch_moe_fused(const FusedArgsHost& h, hipStream_t st) {
     a.x = h.x;
     a.y = h.y;
     a.h = h.h;
+    a.ypart = h.ypart;
     a.sync = h.sync;
-    if (!fused_supported(a.s, a.k, a.mode == 1 ? a.n_expert : 0)) return hipErrorInvalidValue;
+    if (!fused_supported(a.s, a.k, a.mode == 1 ? a.n_expert : 0) || !a.ypart || !a.h || !a.sync)
+        return hipErrorInvalidValue;
     FusedFn fn = pick_fused(a.s);
     int dev = 0;
     hipError_t e = hipGetDevice(&dev);
     if (e != hipSuccess) return e;
-    const int grid = fused_grid(fn, dev);
-    if (grid <= 0) return hipErrorInvalidConfiguration;
-    // the phase-B partial buffer holds kMaxRowsB rows per slot
-    const int S = kFusedThreads / (a.k * (a.s.FF / 64));
-    if ((a.s.D + grid * S - 1) / (grid * S) > kMaxRowsB) return hipErrorInvalidValue;
+    const GridInfo g = fused_capacity(fn, dev);
+    if (g.per_cu <= 0) return hipErrorInvalidConfiguration;
+    a.np = partitions_for(a.k);
+    a.local_l2 = (a.np == 8 && xcd_round_robin(dev)) ? 1 : 0;
+    a.epoch = h.epoch;
+    const int m0 = g.per_cu * g.cus / a.np;  // every workgroup resident at once
+    if (m0 <= 0) return hipErrorInvalidConfiguration;
+    a.rows_b = (a.s.D + m0 - 1) / m0;
+    a.m = (a.s.D + a.rows_b - 1) / a.rows_b;  // no workgroup without output rows
+    if (a.m > kMaxChunks || (a.local_l2 && a.m > kMaxM) || a.epoch == 0) return hipErrorInvalidConfiguration;
+    const int ep = a.k / a.np;
+    const int UP = ep * (a.s.FF / 64);
+    const int slots = kThreads / UP;
+    int rr = a.rows_b;
+    while (rr > 1 && ep * stage_stride(rr, (int)a.s.down_rb) > kStageB) rr--;
+    if (rr * UP > kMaxPart) rr = kMaxPart / UP;
+    if (rr > slots && rr < a.rows_b) rr -= rr % slots;  // whole passes over the row slots
+    if (rr <= 0) return hipErrorInvalidConfiguration;
+    a.round_b = rr;
     clear_stale_error();
     // A plain launch: the grid never exceeds what is resident at once, and the
     // stream runs nothing else concurrently, so every workgroup is live.
-    hipLaunchKernelGGL(fn, dim3(grid), dim3(kFusedThreads), 0, st, a);
+    hipLaunchKernelGGL(fn, dim3(a.np * a.m), dim3(kThreads), 0, st, a);
     return hipGetLastError();
 }
 
