@@ -403,6 +403,12 @@ int eahmmf_hip_set_fused(int enable) {
     return prev;
 }
 
+int eahmmf_hip_fused_exchange(void) {
+    int dev = 0;
+    if (!hip_ok(hipGetDevice(&dev), "get device")) return -1;
+    return fused_exchange_mode(dev);
+}
+
 int eahmmf_hip_device_flags(void) {
     DevCtx* c = ctx_for_current_device();
     if (!c) return -2;

@@ -70,6 +70,10 @@ struct FusedArgsHost {
 constexpr int kSyncWords = 4096;
 constexpr int kSyncFlagWord = 1020;  // error flag word inside the sync buffer
 bool fused_supported(const MoeShape& s, int k, int n_expert_for_routing);
+// 1 if the fused kernel's partitions exchange h through their own XCD's L2 on
+// this device (workgroup b runs on XCD b % 8), 0 if it uses the
+// device-coherent protocol.
+int fused_exchange_mode(int device);
 hipError_t launch_moe_fused(const FusedArgsHost& h, hipStream_t st);
 
 // softmax -> top-k (e desc, index asc) -> renormalise; logits [nb][n_expert].

@@ -7,12 +7,14 @@
 // CPU, 16 synchronous round trips per layer.
 //
 // Layout of the work.  The routed experts are split into NP partitions (one
-// expert each for k <= 8, k/8 each for k = 16); workgroup b belongs to
-// partition b % NP and is rank q = b / NP inside it.  With NP = 8,
-// consecutive workgroups land on the eight XCDs in turn (checked once per
-// device, and by every workgroup), so a partition lives on one XCD and its
-// slice of h is exchanged through that XCD's L2.  Otherwise h travels with
-// device-coherent stores and loads.
+// expert each for k <= 8, k/8 each for k = 16); workgroup b is rank q = b / NP
+// inside its partition.  With NP = 8 the partition is the XCD the workgroup
+// runs on (hardware XCC id): the dispatcher hands consecutive workgroups to
+// the eight XCDs in turn, starting wherever the previous launch stopped, so
+// workgroups b, b+8, b+16, ... share one XCD (checked once per device) and a
+// partition's slice of h is exchanged through that XCD's L2.  Otherwise
+// workgroup b belongs to partition b % NP and h travels with device-coherent
+// stores and loads.
 // Per workgroup (256 threads):
 //   1. wave 0 routes: logits and the expert table are read once, e_i =
 //      expf(l_i - max), top-k by DPP max/min reductions (the lower id wins
@@ -26,16 +28,19 @@
 //      row segments are loaded straight from HBM into registers, dotted
 //      exactly in int32 (v_dot4) against the activation levels, reduced in
 //      the group, and h = silu(g) * u is stored.
-//   4. partition barrier: one counter per partition, one increment per
-//      workgroup after its stores completed; bounded polling by atomic reads.
+//   4. partition barrier.  XCD-local: each workgroup stores the launch epoch
+//      in its own flag word and wave 0 polls the partition's m flags with
+//      agent-scope loads (which miss the CU's L1).  Otherwise one atomic
+//      counter per partition.
 //   5. phase B: the partition's h is read into LDS; threads own (expert,
 //      64-value segment of FF) units, compute w_j * down_j[r].h_j for the
 //      staged rows in fp32, and sum the units of each row in a fixed order
 //      into this partition's partial ypart[p][r].
-//   6. per row chunk, the last of the NP partitions to arrive adds the NP
-//      partials in partition order (deterministic) and writes y.
+//   6. per row chunk, one workgroup adds the NP partials in partition order
+//      (deterministic) and writes y: partition q % NP once all NP epoch flags
+//      of the chunk are set (XCD-local), else the last partition to arrive.
 // Counters are reset by the last workgroup through each stage, so every
-// launch starts from zero.  Every wait is bounded; if a bound is ever hit an
+// launch starts from zero; epoch flags need no reset.  Every wait is bounded; if a bound is ever hit an
 // error flag is raised and the kernel still exits.
 #include <mutex>
 
@@ -57,7 +62,7 @@ constexpr unsigned kSpinLimit = 1u << 22;
 // serve the device-coherent protocol; epoch flags serve the XCD-local one.
 constexpr int kSyncArrive = 0, kSyncPass = 8, kSyncChunk = 16, kSyncErr = kSyncFlagWord;
 constexpr int kMaxChunks = 512;
-constexpr int kMaxM = 128;                             // workgroups per partition (epoch flags)
+constexpr int kMaxM = 128;                             // workgroups per partition (epoch flags, 2 per lane)
 constexpr int kFlagArrive = 1024, kFlagChunk = 2048;  // [8][kMaxM] each
 static_assert(kSyncChunk + kMaxChunks <= kSyncErr && kFlagChunk + 8 * kMaxM <= kSyncWords, "sync layout");
 
@@ -151,11 +156,13 @@ __device__ __forceinline__ unsigned poll_counter(unsigned* p) {
     return __hip_atomic_fetch_add(p, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// Load that bypasses the CU's L1 (sc0) and is served by the XCD's L2: sees
-// every store another CU of the same XCD has completed.
-__device__ __forceinline__ unsigned load_l2(const unsigned* p) {
-    const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(const_cast<unsigned*>(p), 0, 4, 0x00020000);
-    return __builtin_amdgcn_raw_buffer_load_b32(r, 0, 0, 1);
+// Poll of a flag another CU of the same XCD stores with a plain store.  The
+// load must miss the CU's L1: an sc0 (workgroup-scope) load, even after
+// "buffer_inv sc0", is served by a stale L1 line until that line is evicted
+// (measured: never within 20 ms on an idle CU), while an agent-scope (sc1)
+// load sees the completed store within ~0.2 us.
+__device__ __forceinline__ unsigned load_flag(const unsigned* p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // XCD (XCC) the calling wave runs on: hardware register HW_REG_XCC_ID (20),
@@ -356,7 +363,9 @@ __device__ void fused_body(const FusedArgs& a, FusedLds& L) {
     const MoeShape& s = a.s;
     const int D = s.D, FF = s.FF, k = a.k;
     const int np = a.np, m = a.m;
-    const int p = blockIdx.x % np, q = blockIdx.x / np;
+    const int xcc = a.local_l2 ? xcc_id() : 0;
+    const bool xcc_bad = xcc >= np;  // never on a device that passed the host's placement check
+    const int p = a.local_l2 ? (xcc_bad ? 0 : xcc) : (int)blockIdx.x % np, q = blockIdx.x / np;
     const int ep = k / np;  // experts per partition
     const int segB = FF / 64;
     const int UP = ep * segB;  // units of the partition
@@ -461,14 +470,16 @@ __device__ void fused_body(const FusedArgs& a, FusedLds& L) {
         // every workgroup of the partition publishes the launch epoch in its own
         // flag word (a plain store into this XCD's L2); wave 0 watches all m flags
         if (tid == 0) {
-            if (xcc_id() != p)  // the partition-to-XCD mapping this exchange relies on
+            if (xcc_bad)  // the XCD-to-partition mapping this exchange relies on does not hold
                 __hip_atomic_store(&a.sync[kSyncErr], 2u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             a.sync[kFlagArrive + p * kMaxM + q] = a.epoch;
         }
         if (wave == 0) {
             unsigned spins = 0;
             for (;;) {
-                const bool mine = lane >= m || load_l2(&a.sync[kFlagArrive + p * kMaxM + lane]) == a.epoch;
+                const unsigned* fl = &a.sync[kFlagArrive + p * kMaxM];
+                const bool mine = (lane >= m || load_flag(fl + lane) == a.epoch) &&
+                                  (lane + 64 >= m || load_flag(fl + lane + 64) == a.epoch);
                 if (__all(mine)) break;
                 __builtin_amdgcn_s_sleep(1);
                 if (++spins == kSpinLimit) {
@@ -692,8 +703,9 @@ __global__ void xcc_probe_kernel(int* out) {
     if (threadIdx.x == 0) out[blockIdx.x] = xcc_id();
 }
 
-// One-time check per device that workgroup b of a plain launch runs on XCD
-// b % 8 (the round-robin dispatch the XCD-local exchange relies on).
+// One-time check per device that a plain launch places workgroup b on XCD
+// (b + s) % 8 for one start s (the round-robin dispatch the XCD-local exchange
+// relies on; s depends on the launches before).
 static bool xcd_round_robin(int device) {
     static int state[64];  // 0 unknown, 1 yes, 2 no
     static std::mutex mu;
@@ -703,16 +715,21 @@ static bool xcd_round_robin(int device) {
     state[device] = 2;
     constexpr int kProbe = 1024;
     int* d = nullptr;
+    clear_stale_error();  // an earlier, unrelated failure must not read as the probe's
     if (hipMalloc(&d, kProbe * sizeof(int)) != hipSuccess) return false;
     hipLaunchKernelGGL(xcc_probe_kernel, dim3(kProbe), dim3(64), 0, nullptr, d);
     int hbuf[kProbe];
     bool ok = hipGetLastError() == hipSuccess &&
               hipMemcpy(hbuf, d, sizeof hbuf, hipMemcpyDeviceToHost) == hipSuccess;
     (void)hipFree(d);
-    for (int b = 0; ok && b < kProbe; b++) ok = hbuf[b] == b % 8;
+    const int s = ok ? hbuf[0] : -1;
+    ok = ok && s >= 0 && s < 8;
+    for (int b = 0; ok && b < kProbe; b++) ok = hbuf[b] == (b + s) % 8;
     if (ok) state[device] = 1;
     return ok;
 }
+
+int fused_exchange_mode(int device) { return xcd_round_robin(device) ? 1 : 0; }
 
 hipError_t launch_moe_fused(const FusedArgsHost& h, hipStream_t st) {
     FusedArgs a{};

@@ -148,6 +148,11 @@ int eahmmf_hip_mem_info(size_t* free_bytes, size_t* total_bytes);
  * the previous setting.  EAHMMF_HIP_UNFUSED=1 selects 0 at start-up (like the
  * reference's EAHMMF_OLD_KERNEL switch, expert_cuda.cu:307-308). */
 int eahmmf_hip_set_fused(int enable);
+/* How the fused kernel's partitions exchange their gate/up results on the
+ * current device: 1 through each XCD's own L2 (the dispatch places workgroup b
+ * on XCD b % 8, checked once per device), 0 through device-coherent memory,
+ * -1 on error. */
+int eahmmf_hip_fused_exchange(void);
 /* Nonzero if a fused launch on the current device hit its bounded wait since
  * the last call (its output is then not valid); clears the flag. */
 int eahmmf_hip_device_flags(void);
