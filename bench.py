@@ -29,6 +29,7 @@ PKG_DIR = os.path.join(ROOT, "eahmmf_inference_prototype_v-0.1.0_amd")
 HBM_PEAK_GBS = 8000.0
 D, FF, E, K = 2048, 768, 128, 8
 Q4_K, Q6_K = 12, 14
+COPY_BYTES = 256 << 20
 
 
 def load_binding():
@@ -99,6 +100,38 @@ def cpu_baseline(gate, up, down, xs, logits, budget_s):
                       f"OpenMP threads={threads}"}
 
 
+def measured_traffic(fused):
+    """HBM bytes per launch of the fused kernel at this workload, from the
+    committed rocprofv3 FETCH_SIZE/WRITE_SIZE passes (scaled by a plain copy's
+    counters); None when the two-kernel path runs or no measurement exists."""
+    path = os.path.join(ROOT, "profiles", "moe_decode_fused_c2_hbm_traffic.json")
+    if not fused or not os.path.exists(path):
+        return None
+    with open(path) as f:
+        return int(json.load(f)["traffic_bytes"])
+
+
+def calibrate_copy(torch, steps):
+    """A plain device-to-device copy of COPY_BYTES, timed with HIP events.  Under
+    rocprofv3 --pmc its FETCH_SIZE / WRITE_SIZE per dispatch should read
+    COPY_BYTES each; the ratio scales the same counters of the expert kernel."""
+    n = COPY_BYTES // 4
+    src = torch.randn(n, device="cuda")
+    dst = torch.empty_like(src)
+    st = torch.cuda.current_stream()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    e0.record(st)
+    for _ in range(steps):
+        dst.copy_(src)
+    e1.record(st)
+    torch.cuda.synchronize()
+    us = e0.elapsed_time(e1) * 1e3 / steps
+    print(json.dumps({"copy_bytes": COPY_BYTES, "dispatches": steps + 1, "avg_us": round(us, 3),
+                      "read_plus_write_GBs": round(2 * COPY_BYTES / (us * 1e-6) / 1e9, 1)}), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -107,6 +140,8 @@ def main():
     ap.add_argument("--replicas", type=int, default=16)
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="only run a plain 256 MiB device copy (the reference kernel for scaling HBM counters)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only (asked for --gpus {args.gpus}); the expert path shards by expert "
@@ -114,6 +149,9 @@ def main():
         sys.exit(2)
 
     import torch
+    if args.calibrate_copy:
+        calibrate_copy(torch, args.steps)
+        return
     b = load_binding()
     hip = b.lib()
     torch.cuda.set_device(0)
@@ -167,7 +205,8 @@ def main():
     torch.cuda.synchronize()
     el = time.perf_counter() - t0
     assert hip.eahmmf_hip_device_flags() == 0, "a fused launch ran out of its bounded wait"
-    kernel_name = ("moe_decode_fused (routing + gate/up + down in one launch)" if hip.eahmmf_hip_set_fused(-1)
+    fused = bool(hip.eahmmf_hip_set_fused(-1))
+    kernel_name = ("moe_decode_fused (routing + gate/up + down in one launch)" if fused
                    else "route_topk + moe_gate_up + moe_down")
     bytes_step = K * (2 * FF * b.row_bytes(Q4_K, D) + D * b.row_bytes(Q6_K, FF))
     value = bytes_step * args.steps / el / 1e9
@@ -198,9 +237,10 @@ def main():
         "expert_only_decode_tokens_per_s_48_layers": round(1.0 / (48 * ms * 1e-3), 1),
         "roofline": {"bound": "hbm", "kernel": kernel_name,
                      "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": measured_traffic(fused),
                      "avg_us": round(kern_us, 3), "p10_us": round(float(np.percentile(durs, 10)), 3),
-                     "p90_us": round(float(np.percentile(durs, 90)), 3)},
+                     "p90_us": round(float(np.percentile(durs, 90)), 3),
+                     "xcd_local_exchange": int(hip.eahmmf_hip_fused_exchange())},
     }
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline(gate, up, down, xs, logits, args.cpu_seconds)
