@@ -250,8 +250,8 @@ bool eahmmf_hip_moe_decode(const eahmmf_hip_expert* experts, const float* w, int
             f.y = (float*)c->dy.p;
             f.h = (float*)c->dh.p;
             f.sync = c->dsync;
-        f.ypart = (float*)c->dyp.p;
-        f.epoch = ++c->epoch;
+            f.ypart = (float*)c->dyp.p;
+            f.epoch = ++c->epoch;
             ok = hip_ok(launch_moe_fused(f, c->stream), "fused moe decode launch");
         } else {
             ok = hip_ok(launch_moe_decode(s, slots, (const float*)c->dx.p, (float*)c->dh.p, (float*)c->dy.p,

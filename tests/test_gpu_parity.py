@@ -257,6 +257,9 @@ def test_moe_decode_async_and_routed(torch_dev, binding, hip, path):
     ("c1_q8_0", (Q8_0, Q8_0, Q8_0), 256, 128, 8, 2),
     ("c3_q5_k", (Q5_K, Q5_K, Q5_K), 2048, 768, 32, 8),
     ("c5_q4_k_m", (Q4_K, Q4_K, Q6_K), 4096, 1536, 16, 8),
+    ("top16_two_experts_per_partition", (Q4_K, Q4_K, Q6_K), 2048, 768, 64, 16),
+    ("top6_coherent_exchange", (Q8_0, Q8_0, Q6_K), 1024, 512, 32, 6),
+    ("top1", (Q6_K, Q6_K, Q5_K), 512, 256, 16, 1),
 ], ids=lambda c: c if isinstance(c, str) else None)
 def test_moe_layer_decode_vs_oracle(torch_dev, binding, hip, path, name, types, D, FF, E, k):
     """One launch per layer-token (routing from device logits) over a device
