@@ -252,69 +252,84 @@ __device__ void route_wave(const FusedArgs& a, FusedLds& L) {
     }
 }
 
-// n fp32 values (n % 64 == 0) -> 3 int8 levels per 64-value segment and
-// 32-value sums, into LDS: level lv of value i at q + lv*qstride + i, scale
-// of segment g at sc + lv*scstride + g, sum of values [32c, 32c+32) at s32[c].
-// Eight threads per segment, eight values each; threads t in [0, nthr).
+// Activation levels.  n fp32 values (n % 64 == 0) become 3 int8 levels per
+// 64-value segment plus 32-value sums, in LDS: level lv of value i at
+// q + lv*qstride + i, scale of segment g at sc + lv*scstride + g, sum of
+// values [32c, 32c+32) at s32[c].  Eight adjacent threads share a segment,
+// eight values each.
+
+// This thread's eight values of segment seg (zeros when inactive).
+template <bool COHERENT>
+__device__ __forceinline__ void load8(const float* src, int seg, int part, bool active, float (&v)[8]) {
+    if (active) {
+        const float* sp = src + seg * 64 + part * 8;
+        if (COHERENT) {
+#pragma unroll
+            for (int i = 0; i < 8; i++) v[i] = __hip_atomic_load(sp + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        } else {
+            const float4 v0 = reinterpret_cast<const float4*>(sp)[0], v1 = reinterpret_cast<const float4*>(sp)[1];
+            v[0] = v0.x; v[1] = v0.y; v[2] = v0.z; v[3] = v0.w;
+            v[4] = v1.x; v[5] = v1.y; v[6] = v1.z; v[7] = v1.w;
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < 8; i++) v[i] = 0.f;
+    }
+}
+
+// Levels of the eight values v of segment seg; every lane of the wave calls it
+// (the segment's amax and sums are exchanged by shuffles).
+__device__ __forceinline__ void quantize8(const float (&v)[8], int seg, int part, bool active, int8_t* q, int qstride,
+                                          float* sc, int scstride, float* s32) {
+    float amax = 0.f, sum = 0.f;
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        amax = fmaxf(amax, fabsf(v[i]));
+        sum += v[i];
+    }
+    amax = fmaxf(amax, __shfl_xor(amax, 1, 64));
+    amax = fmaxf(amax, __shfl_xor(amax, 2, 64));
+    amax = fmaxf(amax, __shfl_xor(amax, 4, 64));
+    sum += __shfl_xor(sum, 1, 64);
+    sum += __shfl_xor(sum, 2, 64);  // four threads = 32 values
+    if (!active) return;
+    // Scales need only be consistent, not exact quotients: each level's
+    // residual r - q*s is formed exactly (fma), and an inverse within an ulp
+    // (v_rcp) keeps |residual| <= s/2 (1 + 2^-22), inside the next level's
+    // +-127 * s/254 range up to its clamp.
+    const float s1 = amax * (1.0f / 127.0f);
+    const float s2 = s1 * (1.0f / 254.0f), s3 = s2 * (1.0f / 254.0f);
+    const float lsc[kLevels] = {s1, s2, s3};
+    float r[8];
+#pragma unroll
+    for (int i = 0; i < 8; i++) r[i] = v[i];
+#pragma unroll
+    for (int lv = 0; lv < kLevels; lv++) {
+        const float inv = lsc[lv] > 0.f ? __builtin_amdgcn_rcpf(lsc[lv]) : 0.f;
+        uint32_t packed[2] = {0u, 0u};
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            float qf = __builtin_rintf(r[i] * inv);
+            qf = fminf(127.f, fmaxf(-127.f, qf));
+            r[i] = __builtin_fmaf(-qf, lsc[lv], r[i]);
+            packed[i >> 2] |= ((uint32_t)(int)qf & 0xFFu) << (8 * (i & 3));
+        }
+        *reinterpret_cast<uint2*>(q + lv * qstride + seg * 64 + part * 8) = make_uint2(packed[0], packed[1]);
+        if (part == 0) sc[lv * scstride + seg] = lsc[lv];
+    }
+    if ((part & 3) == 0) s32[seg * 2 + part / 4] = sum;
+}
+
+// All n values by threads t in [0, nthr) (nthr a multiple of 64).
 template <bool COHERENT>
 __device__ void quantize_levels(const float* src, int n, int8_t* q, int qstride, float* sc, int scstride, float* s32,
                                 int t, int nthr) {
     const int nseg = n / 64;
-    const int per_pass = nthr / 8;
-    for (int base = 0; base < nseg; base += per_pass) {
-        const int seg = base + t / 8;
-        const int part = t % 8;
-        const bool active = seg < nseg;
+    for (int base = 0; base < nseg; base += nthr / 8) {
+        const int seg = base + t / 8, part = t % 8;
         float v[8];
-        float amax = 0.f, sum = 0.f;
-        if (active) {
-            const float* sp = src + seg * 64 + part * 8;
-            if (COHERENT) {
-#pragma unroll
-                for (int i = 0; i < 8; i++) v[i] = __hip_atomic_load(sp + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            } else {
-                const float4 v0 = reinterpret_cast<const float4*>(sp)[0], v1 = reinterpret_cast<const float4*>(sp)[1];
-                v[0] = v0.x; v[1] = v0.y; v[2] = v0.z; v[3] = v0.w;
-                v[4] = v1.x; v[5] = v1.y; v[6] = v1.z; v[7] = v1.w;
-            }
-#pragma unroll
-            for (int i = 0; i < 8; i++) {
-                amax = fmaxf(amax, fabsf(v[i]));
-                sum += v[i];
-            }
-        } else {
-#pragma unroll
-            for (int i = 0; i < 8; i++) v[i] = 0.f;
-        }
-        // the 8 threads of a segment are adjacent lanes
-        amax = fmaxf(amax, __shfl_xor(amax, 1, 64));
-        amax = fmaxf(amax, __shfl_xor(amax, 2, 64));
-        amax = fmaxf(amax, __shfl_xor(amax, 4, 64));
-        sum += __shfl_xor(sum, 1, 64);
-        sum += __shfl_xor(sum, 2, 64);  // four threads = 32 values
-        if (active) {
-            const float s1 = amax / 127.0f;
-            const float s2 = s1 / 254.0f, s3 = s2 / 254.0f;
-            const float lsc[kLevels] = {s1, s2, s3};
-            float r[8];
-#pragma unroll
-            for (int i = 0; i < 8; i++) r[i] = v[i];
-#pragma unroll
-            for (int lv = 0; lv < kLevels; lv++) {
-                const float inv = lsc[lv] > 0.f ? 1.0f / lsc[lv] : 0.f;
-                uint32_t packed[2] = {0u, 0u};
-#pragma unroll
-                for (int i = 0; i < 8; i++) {
-                    float qf = __builtin_rintf(r[i] * inv);
-                    qf = fminf(127.f, fmaxf(-127.f, qf));
-                    r[i] = __builtin_fmaf(-qf, lsc[lv], r[i]);
-                    packed[i >> 2] |= ((uint32_t)(int)qf & 0xFFu) << (8 * (i & 3));
-                }
-                *reinterpret_cast<uint2*>(q + lv * qstride + seg * 64 + part * 8) = make_uint2(packed[0], packed[1]);
-                if (part == 0) sc[lv * scstride + seg] = lsc[lv];
-            }
-            if ((part & 3) == 0) s32[seg * 2 + part / 4] = sum;
-        }
+        load8<COHERENT>(src, seg, part, seg < nseg, v);
+        quantize8(v, seg, part, seg < nseg, q, qstride, sc, scstride, s32);
     }
 }
 

@@ -296,3 +296,38 @@ def test_moe_layer_decode_vs_oracle(torch_dev, binding, hip, path, name, types, 
     for t in range(T):
         want = oracle.moe_layer(layer, xs[t:t + 1], ids[t:t + 1], w[t:t + 1])[0]
         close(y[t], want)
+
+
+@pytest.mark.parametrize("n_expert,k,levels", [(128, 8, 3), (256, 16, 2), (64, 8, 1), (100, 6, 4)])
+def test_layer_routing_ties(torch_dev, binding, hip, path, n_expert, k, levels):
+    """Logits drawn from a few levels (many exact ties): the chosen ids follow
+    (e desc, id asc) exactly, the weights the rank-order renormalisation."""
+    torch = torch_dev
+    rng = np.random.default_rng(n_expert * 31 + k)
+    D, FF = 256, 128
+    uniq = make_layer(binding, (Q8_0, Q8_0, Q8_0), D, FF, 4, rng)
+    dev_u = [[to_dev(torch, uniq[e][c][1]) for c in range(3)] for e in range(4)]
+    table = np.array([[dev_u[e % 4][c].data_ptr() for c in range(3)] for e in range(n_expert)], dtype=np.uint64)
+    dtable = to_dev(torch, table.view(np.int64))
+    rb = binding.row_bytes(Q8_0, D)
+    shape = binding.MoeShape(Q8_0, Q8_0, Q8_0, D, FF, rb, rb, binding.row_bytes(Q8_0, FF))
+    T = 8
+    logits = rng.integers(0, levels, (T, n_expert)).astype(np.float32) * 0.5
+    xs = rng.normal(0, 1, (T, D)).astype(np.float32)
+    dx, dl = to_dev(torch, xs), to_dev(torch, logits)
+    dy = torch.empty((T, D), device="cuda")
+    dids = torch.full((T, k), -7, dtype=torch.int32, device="cuda")
+    dw = torch.zeros((T, k), dtype=torch.float32, device="cuda")
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    for t in range(T):
+        rc = hip.eahmmf_hip_moe_layer_decode_async(ctypes.byref(shape), ptr(dtable), n_expert, ptr(dl[t]), k,
+                                                   ptr(dx[t]), ptr(dy[t]), ptr(dids[t]), ptr(dw[t]), stream)
+        assert rc == 0, hip.eahmmf_hip_last_error()
+    torch.cuda.synchronize()
+    ids, w = oracle.route_topk(logits, k)
+    assert np.array_equal(dids.cpu().numpy(), ids)
+    np.testing.assert_allclose(dw.cpu().numpy(), w, rtol=1e-6, atol=0)
+    layer = [uniq[e % 4] for e in range(n_expert)]
+    y = dy.cpu().numpy()
+    for t in range(T):
+        close(y[t], oracle.moe_layer(layer, xs[t:t + 1], ids[t:t + 1], w[t:t + 1])[0])
