@@ -15,6 +15,8 @@
 #include <map>
 #include <mutex>
 #include <string>
+#include <vector>
+#include <algorithm>
 
 #include "../../include/eahmmf_hip.h"
 #include "internal.h"
@@ -48,7 +50,7 @@ struct DeviceBuf {
 
 struct DevCtx {
     hipStream_t stream = nullptr;
-    DeviceBuf dx, dy, dy2, dh, dids, dw, dyp;  // device scratch
+    DeviceBuf dx, dy, dy2, dh, dids, dw, dyp, dgs, dtab;  // device scratch
     DeviceBuf px, py, py2;                // pinned host staging
     unsigned* dsync = nullptr;            // fused-launch counters and flags (zeroed once)
     unsigned epoch = 0;                   // fused launches issued on dsync
@@ -397,6 +399,94 @@ int eahmmf_hip_moe_layer_decode_async(const eahmmf_hip_moe_shape* shape, const e
     return 0;
 }
 
+int eahmmf_hip_moe_grouped_async(const eahmmf_hip_moe_shape* shape, const eahmmf_hip_expert_ptrs* dev_table,
+                                 int n_expert, const int* dev_ids, const float* dev_w, int nb, int k,
+                                 const float* dev_x, float* dev_y, void* stream) {
+    MoeShape s{};
+    if (!shape_from_abi(shape, s)) return -1;
+    if (!dev_table || !dev_ids || !dev_w || !dev_x || !dev_y) return set_error("null argument"), -1;
+    if (!grouped_supported(s, nb, k, n_expert))
+        return set_error("unsupported grouped shape: nb=%d k=%d n_expert=%d D=%d FF=%d", nb, k, n_expert, s.D, s.FF),
+               -1;
+    DevCtx* c = ctx_for_current_device();
+    if (!c) return -2;
+    if (!grow_device(c->dgs, grouped_scratch_bytes(s, nb, k, n_expert))) return -2;
+    return hip_ok(launch_moe_grouped(s, (const ExpertEntry*)dev_table, n_expert, dev_ids, dev_w, nb, k, dev_x, s.D,
+                                     dev_y, s.D, c->dgs.p, (hipStream_t)stream),
+                  "grouped moe launch")
+               ? 0
+               : -3;
+}
+
+bool eahmmf_hip_moe_grouped(const eahmmf_hip_expert* experts, int n_groups, const int* group_offsets,
+                            const int* tokens, const float* weights, int nb, const float* host_x, float* host_y) {
+    if (!experts || !group_offsets || !tokens || !weights || !host_x || !host_y)
+        return set_error("null argument"), false;
+    if (n_groups <= 0 || nb <= 0) return set_error("n_groups=%d nb=%d", n_groups, nb), false;
+    const eahmmf_hip_expert& e0 = experts[0];
+    if (!weight_ok(e0.gate) || !weight_ok(e0.up) || !weight_ok(e0.down))
+        return set_error("group 0: missing device pointer or unsupported type"), false;
+    MoeShape s{e0.gate.type, e0.up.type, e0.down.type, e0.gate.ne0, e0.gate.ne1,
+               e0.gate.row_bytes, e0.up.row_bytes, e0.down.row_bytes};
+    std::vector<ExpertEntry> table((size_t)n_groups);
+    for (int g = 0; g < n_groups; g++) {
+        const eahmmf_hip_expert& e = experts[g];
+        if (!weight_ok(e.gate) || !weight_ok(e.up) || !weight_ok(e.down))
+            return set_error("group %d: missing device pointer or unsupported type", g), false;
+        if (e.gate.type != s.gate_type || e.up.type != s.up_type || e.down.type != s.down_type ||
+            e.gate.ne0 != s.D || e.gate.ne1 != s.FF || e.up.ne0 != s.D || e.up.ne1 != s.FF || e.down.ne0 != s.FF ||
+            e.down.ne1 != s.D || e.gate.row_bytes != s.gate_rb || e.up.row_bytes != s.up_rb ||
+            e.down.row_bytes != s.down_rb)
+            return set_error("group %d: shape/type differs from group 0", g), false;
+        table[g] = ExpertEntry{e.gate.dev, e.up.dev, e.down.dev};
+        if (group_offsets[g + 1] < group_offsets[g]) return set_error("group_offsets not ascending"), false;
+    }
+    if (group_offsets[0] != 0) return set_error("group_offsets[0] must be 0"), false;
+    // per token: its groups in ascending order (the lists are per group, in token order)
+    std::vector<int> per_tok((size_t)nb, 0);
+    for (int g = 0; g < n_groups; g++)
+        for (int i = group_offsets[g]; i < group_offsets[g + 1]; i++) {
+            const int t = tokens[i];
+            if (t < 0 || t >= nb) return set_error("token %d of group %d outside 0..%d", t, g, nb - 1), false;
+            per_tok[t]++;
+        }
+    int k = 0;
+    for (int t = 0; t < nb; t++) k = per_tok[t] > k ? per_tok[t] : k;
+    if (k <= 0 || k > kMaxSlots) return set_error("a token appears in %d groups (1..%d supported)", k, kMaxSlots), false;
+    if (!grouped_supported(s, nb, k, n_groups))
+        return set_error("unsupported grouped shape: nb=%d k=%d groups=%d", nb, k, n_groups), false;
+    std::vector<int> ids((size_t)nb * k, -1);
+    std::vector<float> w((size_t)nb * k, 0.f);
+    std::fill(per_tok.begin(), per_tok.end(), 0);
+    for (int g = 0; g < n_groups; g++)
+        for (int i = group_offsets[g]; i < group_offsets[g + 1]; i++) {
+            const int t = tokens[i];
+            const int j = per_tok[t]++;
+            ids[(size_t)t * k + j] = g;
+            w[(size_t)t * k + j] = weights[i];
+        }
+    DevCtx* c = ctx_for_current_device();
+    if (!c) return false;
+    const size_t xb = (size_t)nb * s.D * sizeof(float), tb = table.size() * sizeof(ExpertEntry);
+    const size_t ib = ids.size() * sizeof(int), wb = w.size() * sizeof(float);
+    bool ok = grow_device(c->dtab, tb + ib + wb) && grow_device(c->dgs, grouped_scratch_bytes(s, nb, k, n_groups)) &&
+              grow_device(c->dy, xb) && grow_pinned(c->py, xb) && stage_x(c, host_x, nb, s.D, s.D);
+    if (ok) {
+        uint8_t* d = (uint8_t*)c->dtab.p;
+        ok = hip_ok(hipMemcpyAsync(d, table.data(), tb, hipMemcpyHostToDevice, c->stream), "h2d table") &&
+             hip_ok(hipMemcpyAsync(d + tb, ids.data(), ib, hipMemcpyHostToDevice, c->stream), "h2d ids") &&
+             hip_ok(hipMemcpyAsync(d + tb + ib, w.data(), wb, hipMemcpyHostToDevice, c->stream), "h2d w") &&
+             hip_ok(launch_moe_grouped(s, (const ExpertEntry*)d, n_groups, (const int*)(d + tb),
+                                       (const float*)(d + tb + ib), nb, k, (const float*)c->dx.p, s.D,
+                                       (float*)c->dy.p, s.D, c->dgs.p, c->stream),
+                    "grouped moe launch") &&
+             hip_ok(hipMemcpyAsync(c->py.p, c->dy.p, xb, hipMemcpyDeviceToHost, c->stream), "d2h y");
+    }
+    if (!drain(c, ok)) return false;
+    memcpy(host_y, c->py.p, xb);
+    return true;
+}
+
 int eahmmf_hip_set_fused(int enable) {
     const int prev = fused_enabled() ? 1 : 0;
     if (enable >= 0) g_fused = enable ? 1 : 0;
@@ -508,7 +598,7 @@ void eahmmf_hip_shutdown(void) {
     if (it == g_ctx.end()) return;
     DevCtx& c = it->second;
     if (c.stream) (void)hipStreamSynchronize(c.stream);
-    for (DeviceBuf* b : {&c.dx, &c.dy, &c.dy2, &c.dh, &c.dids, &c.dw, &c.dyp})
+    for (DeviceBuf* b : {&c.dx, &c.dy, &c.dy2, &c.dh, &c.dids, &c.dw, &c.dyp, &c.dgs, &c.dtab})
         if (b->p) (void)hipFree(b->p);
     for (DeviceBuf* b : {&c.px, &c.py, &c.py2})
         if (b->p) (void)hipHostFree(b->p);

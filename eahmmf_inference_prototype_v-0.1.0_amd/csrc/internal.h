@@ -76,6 +76,15 @@ bool fused_supported(const MoeShape& s, int k, int n_expert_for_routing);
 int fused_exchange_mode(int device);
 hipError_t launch_moe_fused(const FusedArgsHost& h, hipStream_t st);
 
+// Ragged grouped expert block (kernels_grouped.hip): nb tokens routed by
+// ids/w [nb][k] over table [n_expert]; x [nb][ldx] -> y [nb][ldy].  scratch
+// holds grouped_scratch_bytes() bytes of device memory.
+bool grouped_supported(const MoeShape& s, int nb, int k, int n_expert);
+size_t grouped_scratch_bytes(const MoeShape& s, int nb, int k, int n_expert);
+hipError_t launch_moe_grouped(const MoeShape& s, const ExpertEntry* table, int n_expert, const int* ids,
+                              const float* w, int nb, int k, const float* x, int ldx, float* y, int ldy,
+                              void* scratch, hipStream_t st);
+
 // softmax -> top-k (e desc, index asc) -> renormalise; logits [nb][n_expert].
 hipError_t launch_route_topk(const float* logits, int nb, int n_expert, int k, int* ids, float* w, hipStream_t st);
 

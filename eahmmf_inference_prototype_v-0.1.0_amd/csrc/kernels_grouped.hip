@@ -1,0 +1,341 @@
+// kernels_grouped.hip - the ragged multi-token expert block (prefill and
+// batched decode): nb tokens, each routed to k experts, grouped by expert.
+//
+// This replaces the reference's host loop for a batch (qwen3moe.cpp:1009-1067):
+// by_exp[e] collects the (token, w) pairs of expert e in token order, the
+// experts are visited in ascending id, each runs gate/up, SiLU and down over its
+// gathered tokens as one batched matmul, and every token adds w * y of its
+// experts in ascending expert order.
+//
+// Device steps, all on one stream:
+//   1. group_pairs_kernel (one workgroup): a stable counting sort of the
+//      (token, slot) pairs by expert id.  Tokens are taken in chunks of 64
+//      (one wave each); a chunk's pairs of expert e are the set bits of a
+//      64-bit LDS mask, so a pair's rank among the chunk's pairs of e is a
+//      popcount and the order is fixed by construction.  Chunk counts are
+//      scanned per expert, expert totals across experts, giving
+//        offs[e]      first position of expert e's group
+//        tok[p], pw[p] token and router weight at position p
+//        pos[t*k+j]   position of (token t, slot j), -1 for an invalid id
+//   2. grouped gate/up: one wave per (expert, FF row), tokens of the group in
+//      tiles of 8: h[p][r] = silu(gate_r . x_tok[p]) * (up_r . x_tok[p]).
+//   3. grouped down: one wave per (expert, D row): yp[p][r] = down_r . h[p].
+//   4. combine: y[t] = sum over the token's pairs in ascending expert id of
+//      w * yp[pos] (fma), the reference's accumulation order.
+// Expert weights are read once per (expert, row) however many tokens the
+// group holds.
+#include "internal.h"
+#include "kquant.h"
+
+namespace eahmmf {
+
+constexpr int kGroupThreads = 1024;
+constexpr int kGroupWaves = kGroupThreads / 64;
+constexpr int kGroupMaxE = 256;  // group masks: 16 waves x E x 8 B of LDS
+constexpr int kTT = 8;  // tokens per tile in the grouped matmuls
+
+__device__ __forceinline__ void lds_order() { __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
+
+// ids/w [nb][k]; cnt scratch [nchunks][E]; outputs offs [E+1], tok/pw [nb*k],
+// pos [nb*k].  Dynamic LDS: kGroupWaves * E uint64 masks + E ints.
+__global__ __launch_bounds__(kGroupThreads) void group_pairs_kernel(const int* __restrict__ ids,
+                                                                    const float* __restrict__ w, int nb, int k, int E,
+                                                                    int* __restrict__ cnt, int* __restrict__ offs,
+                                                                    int* __restrict__ tok, float* __restrict__ pw,
+                                                                    int* __restrict__ pos) {
+    extern __shared__ unsigned long long g_lds[];
+    const int tid = threadIdx.x, wave = tid / 64, lane = tid % 64;
+    unsigned long long* mask = g_lds + (size_t)wave * E;
+    int* tot = reinterpret_cast<int*>(g_lds + (size_t)kGroupWaves * E);
+    const int nchunks = (nb + 63) / 64;
+    auto build_mask = [&](int c) {
+        for (int e = lane; e < E; e += 64) mask[e] = 0ull;
+        lds_order();
+        const int t = c * 64 + lane;
+        if (t < nb)
+            for (int j = 0; j < k; j++) {
+                const int e = ids[(size_t)t * k + j];
+                if (e >= 0 && e < E) __hip_atomic_fetch_or(&mask[e], 1ull << lane, __ATOMIC_RELAXED,
+                                                           __HIP_MEMORY_SCOPE_WORKGROUP);
+            }
+        lds_order();
+    };
+    // 1. per-chunk counts
+    for (int c = wave; c < nchunks; c += kGroupWaves) {
+        build_mask(c);
+        for (int e = lane; e < E; e += 64) cnt[(size_t)c * E + e] = __popcll(mask[e]);
+    }
+    __syncthreads();
+    // 2. per expert: chunk bases (exclusive, in place) and the total
+    for (int e = tid; e < E; e += kGroupThreads) {
+        int run = 0;
+        for (int c = 0; c < nchunks; c++) {
+            const int v = cnt[(size_t)c * E + e];
+            cnt[(size_t)c * E + e] = run;
+            run += v;
+        }
+        tot[e] = run;
+    }
+    __syncthreads();
+    // exclusive scan of the totals by wave 0: lane i owns experts [i*per, (i+1)*per)
+    if (wave == 0) {
+        const int per = (E + 63) / 64;
+        int local = 0;
+        for (int i = 0; i < per; i++) {
+            const int e = lane * per + i;
+            if (e < E) local += tot[e];
+        }
+        int incl = local;
+#pragma unroll
+        for (int off = 1; off < 64; off <<= 1) {
+            const int v = __shfl_up(incl, off, 64);
+            if (lane >= off) incl += v;
+        }
+        int run = incl - local;
+        for (int i = 0; i < per; i++) {
+            const int e = lane * per + i;
+            if (e < E) {
+                offs[e] = run;
+                run += tot[e];
+            }
+        }
+        if (lane == 63) offs[E] = incl;
+    }
+    __syncthreads();
+    // 3. scatter every pair to its place
+    for (int c = wave; c < nchunks; c += kGroupWaves) {
+        build_mask(c);
+        const int t = c * 64 + lane;
+        if (t < nb) {
+            const unsigned long long below = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+            for (int j = 0; j < k; j++) {
+                const int e = ids[(size_t)t * k + j];
+                int p = -1;
+                if (e >= 0 && e < E) {
+                    p = offs[e] + cnt[(size_t)c * E + e] + __popcll(mask[e] & below);
+                    tok[p] = t;
+                    pw[p] = w[(size_t)t * k + j];
+                }
+                pos[(size_t)t * k + j] = p;
+            }
+        }
+    }
+}
+
+// Expert e of the table, rows [blockIdx.x*4 + wave]; the group's tokens in
+// tiles of kTT.  x [nb][ldx] fp32.  h [P][FF].
+template <int GT, int UT>
+__global__ __launch_bounds__(256) void grouped_gate_up_kernel(MoeShape s, const ExpertEntry* __restrict__ table,
+                                                              const int* __restrict__ offs,
+                                                              const int* __restrict__ tok,
+                                                              const float* __restrict__ x, int ldx,
+                                                              float* __restrict__ h) {
+    const int e = blockIdx.y;
+    const int p0 = offs[e], p1 = offs[e + 1];
+    if (p1 <= p0) return;
+    const int lane = threadIdx.x & 63;
+    const int r = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (r >= s.FF) return;  // whole wave
+    const ExpertEntry ent = table[e];
+    const uint8_t* gr = ent.gate + (size_t)r * s.gate_rb;
+    const uint8_t* ur = ent.up + (size_t)r * s.up_rb;
+    const int nseg = s.D / 32;
+    for (int t0 = p0; t0 < p1; t0 += kTT) {
+        const int nt = min(kTT, p1 - t0);
+        const float* xr[kTT];
+#pragma unroll
+        for (int t = 0; t < kTT; t++) xr[t] = x + (size_t)tok[t < nt ? t0 + t : t0] * ldx;
+        float ag[kTT], au[kTT];
+#pragma unroll
+        for (int t = 0; t < kTT; t++) ag[t] = au[t] = 0.f;
+        for (int sg = lane; sg < nseg; sg += 64) {
+            float wg[32], wu[32];
+            decode_row_seg<GT>(gr, sg, wg);
+            decode_row_seg<UT>(ur, sg, wu);
+#pragma unroll
+            for (int t = 0; t < kTT; t++) {
+                if (t < nt) {
+                    const float4* xp = reinterpret_cast<const float4*>(xr[t] + (size_t)sg * 32);
+                    float pg = 0.f, pu = 0.f;
+#pragma unroll
+                    for (int i = 0; i < 8; i++) {
+                        const float4 v = xp[i];
+                        pg = __builtin_fmaf(wg[4 * i], v.x, pg);
+                        pg = __builtin_fmaf(wg[4 * i + 1], v.y, pg);
+                        pg = __builtin_fmaf(wg[4 * i + 2], v.z, pg);
+                        pg = __builtin_fmaf(wg[4 * i + 3], v.w, pg);
+                        pu = __builtin_fmaf(wu[4 * i], v.x, pu);
+                        pu = __builtin_fmaf(wu[4 * i + 1], v.y, pu);
+                        pu = __builtin_fmaf(wu[4 * i + 2], v.z, pu);
+                        pu = __builtin_fmaf(wu[4 * i + 3], v.w, pu);
+                    }
+                    ag[t] += pg;
+                    au[t] += pu;
+                }
+            }
+        }
+#pragma unroll
+        for (int t = 0; t < kTT; t++) {
+            if (t < nt) {
+                const float g = wave_sum(ag[t]), u = wave_sum(au[t]);
+                if (lane == 0) h[(size_t)(t0 + t) * s.FF + r] = g / (1.0f + expf(-g)) * u;
+            }
+        }
+    }
+}
+
+// yp [P][D] = down_e . h [P][FF] for the positions of expert e's group.
+template <int DT>
+__global__ __launch_bounds__(256) void grouped_down_kernel(MoeShape s, const ExpertEntry* __restrict__ table,
+                                                           const int* __restrict__ offs, const float* __restrict__ h,
+                                                           float* __restrict__ yp) {
+    const int e = blockIdx.y;
+    const int p0 = offs[e], p1 = offs[e + 1];
+    if (p1 <= p0) return;
+    const int lane = threadIdx.x & 63;
+    const int r = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (r >= s.D) return;
+    const uint8_t* dr = table[e].down + (size_t)r * s.down_rb;
+    const int nseg = s.FF / 32;
+    for (int t0 = p0; t0 < p1; t0 += kTT) {
+        const int nt = min(kTT, p1 - t0);
+        float acc[kTT];
+#pragma unroll
+        for (int t = 0; t < kTT; t++) acc[t] = 0.f;
+        for (int sg = lane; sg < nseg; sg += 64) {
+            float wv[32];
+            decode_row_seg<DT>(dr, sg, wv);
+#pragma unroll
+            for (int t = 0; t < kTT; t++) {
+                if (t < nt) {
+                    const float4* hp = reinterpret_cast<const float4*>(h + (size_t)(t0 + t) * s.FF + (size_t)sg * 32);
+                    float p = 0.f;
+#pragma unroll
+                    for (int i = 0; i < 8; i++) {
+                        const float4 v = hp[i];
+                        p = __builtin_fmaf(wv[4 * i], v.x, p);
+                        p = __builtin_fmaf(wv[4 * i + 1], v.y, p);
+                        p = __builtin_fmaf(wv[4 * i + 2], v.z, p);
+                        p = __builtin_fmaf(wv[4 * i + 3], v.w, p);
+                    }
+                    acc[t] += p;
+                }
+            }
+        }
+#pragma unroll
+        for (int t = 0; t < kTT; t++) {
+            if (t < nt) {
+                const float v = wave_sum(acc[t]);
+                if (lane == 0) yp[(size_t)(t0 + t) * s.D + r] = v;
+            }
+        }
+    }
+}
+
+// y[t][d] = sum over the token's valid pairs, ascending expert id, of
+// w * yp[pos][d].  One thread per (token, 4 consecutive d).
+__global__ __launch_bounds__(256) void grouped_combine_kernel(const int* __restrict__ ids, const int* __restrict__ pos,
+                                                              const float* __restrict__ pw, int nb, int k, int D,
+                                                              const float* __restrict__ yp, float* __restrict__ y,
+                                                              int ldy) {
+    const int q = blockIdx.x * blockDim.x + threadIdx.x;
+    const int per_tok = D / 4;
+    if (q >= nb * per_tok) return;
+    const int t = q / per_tok, d = (q % per_tok) * 4;
+    // the token's slots in ascending expert id (k <= kMaxSlots; ids are distinct per token)
+    int order[kMaxSlots];
+    int n = 0;
+    for (int j = 0; j < k; j++) {
+        const int pj = pos[(size_t)t * k + j];
+        if (pj < 0) continue;
+        const int ej = ids[(size_t)t * k + j];
+        int i = n++;
+        while (i > 0 && ids[(size_t)t * k + order[i - 1]] > ej) {
+            order[i] = order[i - 1];
+            i--;
+        }
+        order[i] = j;
+    }
+    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int i = 0; i < n; i++) {
+        const int p = pos[(size_t)t * k + order[i]];
+        const float wv = pw[p];
+        const float4 v = *reinterpret_cast<const float4*>(yp + (size_t)p * D + d);
+        acc.x = __builtin_fmaf(wv, v.x, acc.x);
+        acc.y = __builtin_fmaf(wv, v.y, acc.y);
+        acc.z = __builtin_fmaf(wv, v.z, acc.z);
+        acc.w = __builtin_fmaf(wv, v.w, acc.w);
+    }
+    *reinterpret_cast<float4*>(y + (size_t)t * ldy + d) = acc;
+}
+
+template <int GT>
+static hipError_t gate_up_for(int ut, const MoeShape& s, dim3 g, const ExpertEntry* table, const int* offs,
+                              const int* tok, const float* x, int ldx, float* h, hipStream_t st) {
+    switch (ut) {
+        case kQ4_K: grouped_gate_up_kernel<GT, kQ4_K><<<g, 256, 0, st>>>(s, table, offs, tok, x, ldx, h); break;
+        case kQ5_K: grouped_gate_up_kernel<GT, kQ5_K><<<g, 256, 0, st>>>(s, table, offs, tok, x, ldx, h); break;
+        case kQ6_K: grouped_gate_up_kernel<GT, kQ6_K><<<g, 256, 0, st>>>(s, table, offs, tok, x, ldx, h); break;
+        case kQ8_0: grouped_gate_up_kernel<GT, kQ8_0><<<g, 256, 0, st>>>(s, table, offs, tok, x, ldx, h); break;
+        default: return hipErrorInvalidValue;
+    }
+    return hipSuccess;
+}
+
+size_t grouped_scratch_bytes(const MoeShape& s, int nb, int k, int n_expert) {
+    const size_t P = (size_t)nb * k, nchunks = ((size_t)nb + 63) / 64;
+    auto al = [](size_t b) { return (b + 255) & ~(size_t)255; };
+    return al(nchunks * n_expert * 4) + al(((size_t)n_expert + 1) * 4) + 3 * al(P * 4) + al(P * s.FF * 4) +
+           al(P * s.D * 4);
+}
+
+bool grouped_supported(const MoeShape& s, int nb, int k, int n_expert) {
+    return moe_shape_ok(s) && nb > 0 && k > 0 && k <= kMaxSlots && n_expert > 0 && n_expert <= kGroupMaxE &&
+           s.D % 32 == 0 && s.FF % 32 == 0 && s.D % 4 == 0;
+}
+
+hipError_t launch_moe_grouped(const MoeShape& s, const ExpertEntry* table, int n_expert, const int* ids,
+                              const float* w, int nb, int k, const float* x, int ldx, float* y, int ldy,
+                              void* scratch, hipStream_t st) {
+    if (!grouped_supported(s, nb, k, n_expert) || ldx < s.D || ldy < s.D || ldx % 4 || ldy % 4 || !scratch)
+        return hipErrorInvalidValue;
+    const size_t P = (size_t)nb * k, nchunks = ((size_t)nb + 63) / 64;
+    auto al = [](size_t b) { return (b + 255) & ~(size_t)255; };
+    uint8_t* b = static_cast<uint8_t*>(scratch);
+    int* cnt = reinterpret_cast<int*>(b); b += al(nchunks * n_expert * 4);
+    int* offs = reinterpret_cast<int*>(b); b += al(((size_t)n_expert + 1) * 4);
+    int* tok = reinterpret_cast<int*>(b); b += al(P * 4);
+    float* pw = reinterpret_cast<float*>(b); b += al(P * 4);
+    int* pos = reinterpret_cast<int*>(b); b += al(P * 4);
+    float* h = reinterpret_cast<float*>(b); b += al(P * s.FF * 4);
+    float* yp = reinterpret_cast<float*>(b);
+    clear_stale_error();
+    const size_t lds = (size_t)kGroupWaves * n_expert * 8 + (size_t)n_expert * 4;
+    group_pairs_kernel<<<1, kGroupThreads, lds, st>>>(ids, w, nb, k, n_expert, cnt, offs, tok, pw, pos);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    const dim3 ga((unsigned)((s.FF + 3) / 4), (unsigned)n_expert);
+    switch (s.gate_type) {
+        case kQ4_K: e = gate_up_for<kQ4_K>(s.up_type, s, ga, table, offs, tok, x, ldx, h, st); break;
+        case kQ5_K: e = gate_up_for<kQ5_K>(s.up_type, s, ga, table, offs, tok, x, ldx, h, st); break;
+        case kQ6_K: e = gate_up_for<kQ6_K>(s.up_type, s, ga, table, offs, tok, x, ldx, h, st); break;
+        case kQ8_0: e = gate_up_for<kQ8_0>(s.up_type, s, ga, table, offs, tok, x, ldx, h, st); break;
+        default: e = hipErrorInvalidValue;
+    }
+    if (e != hipSuccess) return e;
+    if ((e = hipGetLastError()) != hipSuccess) return e;
+    const dim3 gd((unsigned)((s.D + 3) / 4), (unsigned)n_expert);
+    switch (s.down_type) {
+        case kQ4_K: grouped_down_kernel<kQ4_K><<<gd, 256, 0, st>>>(s, table, offs, h, yp); break;
+        case kQ5_K: grouped_down_kernel<kQ5_K><<<gd, 256, 0, st>>>(s, table, offs, h, yp); break;
+        case kQ6_K: grouped_down_kernel<kQ6_K><<<gd, 256, 0, st>>>(s, table, offs, h, yp); break;
+        case kQ8_0: grouped_down_kernel<kQ8_0><<<gd, 256, 0, st>>>(s, table, offs, h, yp); break;
+        default: return hipErrorInvalidValue;
+    }
+    if ((e = hipGetLastError()) != hipSuccess) return e;
+    const size_t nthr = (size_t)nb * (s.D / 4);
+    grouped_combine_kernel<<<(unsigned)((nthr + 255) / 256), 256, 0, st>>>(ids, pos, pw, nb, k, s.D, yp, y, ldy);
+    return hipGetLastError();
+}
+
+}  // namespace eahmmf

@@ -110,6 +110,28 @@ int eahmmf_hip_moe_layer_decode_async(const eahmmf_hip_moe_shape* shape, const e
                                       int n_expert, const float* dev_logits, int k, const float* dev_x, float* dev_y,
                                       int* dev_ids_out, float* dev_w_out, void* stream);
 
+/* Ragged grouped expert block for a batch of nb tokens (prefill, batched
+ * decode), in the reference's by_exp form: group g (ascending expert id) is
+ * experts[g] applied to tokens[group_offsets[g] .. group_offsets[g+1]) with
+ * router weights weights[same range]; host x[nb][D] -> host y[nb][D],
+ *   y[t] = sum over the groups holding t, ascending, of w * down(silu(gate x_t) * up x_t).
+ * A token may appear in at most EAHMMF_HIP_MAX_TOPK groups; all groups share
+ * one shape.  Synchronous.  Replaces the per-expert loop of
+ * qwen3moe.cpp:1024-1067 for a batch (gather, batched matmuls, SiLU,
+ * weighted scatter-add). */
+bool eahmmf_hip_moe_grouped(const eahmmf_hip_expert* experts, int n_groups, const int* group_offsets,
+                            const int* tokens, const float* weights, int nb, const float* host_x, float* host_y);
+
+/* Same with the routing on the device: dev_ids/dev_w [nb][k] (e.g. from
+ * eahmmf_hip_route_topk_async; ids outside 0..n_expert-1 are skipped) over
+ * the device table [n_expert <= 256]; dev_x/dev_y [nb][D], asynchronous on
+ * `stream`.  The (token, expert) pairs are grouped on the device (stable, in
+ * token order) and each token's results are added in ascending expert id,
+ * as qwen3moe.cpp:1009-1067 does. */
+int eahmmf_hip_moe_grouped_async(const eahmmf_hip_moe_shape* shape, const eahmmf_hip_expert_ptrs* dev_table,
+                                 int n_expert, const int* dev_ids, const float* dev_w, int nb, int k,
+                                 const float* dev_x, float* dev_y, void* stream);
+
 /* Softmax -> top-k -> renormalise (qwen3moe.cpp:1011-1023), synchronous on
  * host buffers: logits[nb][n_expert] -> ids[nb][k], w[nb][k] in rank order
  * (e = expf(l - max) descending, lower id first on ties). */

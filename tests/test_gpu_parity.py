@@ -331,3 +331,90 @@ def test_layer_routing_ties(torch_dev, binding, hip, path, n_expert, k, levels):
     y = dy.cpu().numpy()
     for t in range(T):
         close(y[t], oracle.moe_layer(layer, xs[t:t + 1], ids[t:t + 1], w[t:t + 1])[0])
+
+
+# ---------------------------------------------------------------------------
+# ragged grouped multi-token block
+
+def by_expert_lists(ids, w):
+    """The reference's by_exp grouping (qwen3moe.cpp:1009, 1020): per expert,
+    in ascending id, its (token, w) pairs in token order."""
+    groups = {}
+    for t in range(ids.shape[0]):
+        for j in range(ids.shape[1]):
+            groups.setdefault(int(ids[t, j]), []).append((t, float(w[t, j])))
+    return sorted(groups.items())
+
+
+GROUPED_CASES = [
+    ("c1_q8_0", (Q8_0, Q8_0, Q8_0), 256, 128, 8, 2, 16),
+    ("mixed_types", (Q5_K, Q4_K, Q6_K), 512, 256, 12, 3, 70),
+    ("c2_shape_q4_k_m", (Q4_K, Q4_K, Q6_K), 2048, 768, 16, 8, 40),
+    ("c3_q5_k", (Q5_K, Q5_K, Q5_K), 2048, 768, 8, 4, 9),
+    ("q8_0_down_ne0_96", (Q8_0, Q8_0, Q8_0), 128, 96, 6, 2, 130),
+]
+
+
+@pytest.mark.parametrize("name,types,D,FF,E,k,nb", GROUPED_CASES, ids=[c[0] for c in GROUPED_CASES])
+def test_grouped_vs_oracle(torch_dev, binding, hip, name, types, D, FF, E, k, nb):
+    """Host by_exp lists in, host y out: every token's y within tolerance of
+    the oracle's MoE block over the same routing."""
+    torch = torch_dev
+    rng = np.random.default_rng(D * 3 + FF + k + nb)
+    layer = make_layer(binding, types, D, FF, E, rng)
+    x = rng.normal(0, 1, (nb, D)).astype(np.float32)
+    logits = rng.normal(0, 1, (nb, E)).astype(np.float32)
+    ids, w = oracle.route_topk(logits, k)
+    want = oracle.moe_layer(layer, x, ids, w)
+    dev = [[to_dev(torch, layer[e][c][1]) for c in range(3)] for e in range(E)]
+    groups = by_expert_lists(ids, w)
+    experts = (binding.Expert * len(groups))()
+    offs, toks, wts = [0], [], []
+    for g, (e, lst) in enumerate(groups):
+        for c, (nm, ne0, ne1) in enumerate((("gate", D, FF), ("up", D, FF), ("down", FF, D))):
+            t = layer[e][c][0]
+            setattr(experts[g], nm, binding.Weight(dev[e][c].data_ptr(), t, ne0, ne1, binding.row_bytes(t, ne0)))
+        toks += [t for t, _ in lst]
+        wts += [wv for _, wv in lst]
+        offs.append(len(toks))
+    offs = np.array(offs, np.int32)
+    toks = np.array(toks, np.int32)
+    wts = np.array(wts, np.float32)
+    y = np.full((nb, D), np.nan, np.float32)
+    assert hip.eahmmf_hip_moe_grouped(experts, len(groups), offs.ctypes.data, toks.ctypes.data, wts.ctypes.data, nb,
+                                      x.ctypes.data, y.ctypes.data), hip.eahmmf_hip_last_error()
+    close(y, want)
+
+
+@pytest.mark.parametrize("nb,E,k,skew", [(64, 32, 8, 0.0), (200, 128, 8, 1.1), (1, 16, 4, 0.0), (129, 64, 6, 2.0)])
+def test_grouped_async_device_routing(torch_dev, binding, hip, nb, E, k, skew):
+    """Routing on the device (route_topk), grouping on the device, Zipf-skewed
+    expert popularity: y of every token matches the oracle on the same ids."""
+    torch = torch_dev
+    D, FF = 512, 256
+    types = (Q4_K, Q4_K, Q6_K)
+    rng = np.random.default_rng(nb * 7 + E + k)
+    n_unique = min(E, 12)
+    uniq = make_layer(binding, types, D, FF, n_unique, rng)
+    layer = [uniq[e % n_unique] for e in range(E)]
+    dev_u = [[to_dev(torch, uniq[e][c][1]) for c in range(3)] for e in range(n_unique)]
+    table = np.array([[dev_u[e % n_unique][c].data_ptr() for c in range(3)] for e in range(E)], dtype=np.uint64)
+    dtable = to_dev(torch, table.view(np.int64))
+    shape = binding.MoeShape(Q4_K, Q4_K, Q6_K, D, FF, binding.row_bytes(Q4_K, D), binding.row_bytes(Q4_K, D),
+                             binding.row_bytes(Q6_K, FF))
+    # Gumbel-top-k over a Zipf prior on a seeded permutation of the ids
+    prior = np.log(np.arange(1, E + 1, dtype=np.float64) ** -skew)[rng.permutation(E)]
+    logits = (prior + rng.gumbel(size=(nb, E))).astype(np.float32)
+    x = rng.normal(0, 1, (nb, D)).astype(np.float32)
+    dl, dx = to_dev(torch, logits), to_dev(torch, x)
+    dids = torch.empty((nb, k), dtype=torch.int32, device="cuda")
+    dw = torch.empty((nb, k), dtype=torch.float32, device="cuda")
+    dy = torch.full((nb, D), float("nan"), device="cuda")
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    assert hip.eahmmf_hip_route_topk_async(ptr(dl), nb, E, k, ptr(dids), ptr(dw), stream) == 0
+    assert hip.eahmmf_hip_moe_grouped_async(ctypes.byref(shape), ptr(dtable), E, ptr(dids), ptr(dw), nb, k, ptr(dx),
+                                            ptr(dy), stream) == 0, hip.eahmmf_hip_last_error()
+    torch.cuda.synchronize()
+    ids, w = oracle.route_topk(logits, k)
+    assert np.array_equal(dids.cpu().numpy(), ids)
+    close(dy.cpu().numpy(), oracle.moe_layer(layer, x, ids, w))
