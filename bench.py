@@ -52,6 +52,151 @@ def build_layer(b, rng):
     return gate, up, down
 
 
+def build_layer_replicated(b, rng, D, FF, E, n_unique, gt=Q4_K, dt=Q6_K):
+    """E experts from n_unique distinct quantized ones (bytes of each expert
+    still live at their own HBM addresses; only the values repeat)."""
+    grb, drb = b.row_bytes(gt, D), b.row_bytes(dt, FF)
+    uniq = []
+    for _ in range(n_unique):
+        uniq.append((b.quantize_rows(gt, rng.normal(0, .02, (FF, D)).astype(np.float32)).reshape(-1),
+                     b.quantize_rows(gt, rng.normal(0, .02, (FF, D)).astype(np.float32)).reshape(-1),
+                     b.quantize_rows(dt, rng.normal(0, .02, (D, FF)).astype(np.float32)).reshape(-1)))
+    return uniq, grb, drb
+
+
+def upload_layers(torch, uniq, E, R):
+    """R replicas of an E-expert layer in HBM; returns the per-replica device tables."""
+    n_unique = len(uniq)
+    comps = []
+    for c in range(3):
+        host = torch.from_numpy(np.stack([uniq[e % n_unique][c] for e in range(E)])).pin_memory()
+        dev = torch.empty((R,) + tuple(host.shape), dtype=torch.uint8, device="cuda")
+        for r in range(R):
+            dev[r].copy_(host)
+        comps.append(dev)
+    torch.cuda.synchronize()
+    tables = []
+    for r in range(R):
+        t = np.array([[comps[c][r, e].data_ptr() for c in range(3)] for e in range(E)], dtype=np.uint64)
+        tables.append(torch.from_numpy(t.view(np.int64)).cuda())
+    return comps, tables
+
+
+def zipf_routing(rng, nb, E, k, s=1.1):
+    """Gumbel-top-k over log p_zipf (p ~ rank^-s on a seeded permutation of the
+    ids): logits whose softmax/top-k routing is Zipf-skewed."""
+    prior = np.log(np.arange(1, E + 1, dtype=np.float64) ** -s)[rng.permutation(E)]
+    return (prior + rng.gumbel(size=(nb, E))).astype(np.float32)
+
+
+def bench_c4(args, torch, b, hip):
+    """Ragged grouped prefill: 512 tokens x top-8 over 128 Zipf-skewed experts
+    at the Qwen3-30B-A3B expert shape, routing given (device ids/w), one step =
+    grouping + gate/up + down + combine."""
+    D_, FF_, E_, K_, NB = 2048, 768, 128, 8, 512
+    rng = np.random.default_rng(4)
+    uniq, grb, drb = build_layer_replicated(b, rng, D_, FF_, E_, 16)
+    R = args.replicas if args.replicas else 4
+    comps, tables = upload_layers(torch, uniq, E_, R)
+    shape = b.MoeShape(Q4_K, Q4_K, Q6_K, D_, FF_, grb, grb, drb)
+    NS = 4
+    logits = zipf_routing(rng, NS * NB, E_, K_).reshape(NS, NB, E_)
+    xs = rng.normal(0, 1, (NS, NB, D_)).astype(np.float32)
+    dl, dx = torch.from_numpy(logits).cuda(), torch.from_numpy(xs).cuda()
+    dids = torch.empty((NS, NB, K_), dtype=torch.int32, device="cuda")
+    dw = torch.empty((NS, NB, K_), dtype=torch.float32, device="cuda")
+    dy = torch.empty((NS, NB, D_), dtype=torch.float32, device="cuda")
+    stream = torch.cuda.current_stream()
+    sp, vp = ctypes.c_void_p(stream.cuda_stream), ctypes.c_void_p
+    for i in range(NS):
+        assert hip.eahmmf_hip_route_topk_async(vp(dl[i].data_ptr()), NB, E_, K_, vp(dids[i].data_ptr()),
+                                               vp(dw[i].data_ptr()), sp) == 0
+    torch.cuda.synchronize()
+    ids = dids.cpu().numpy()
+    exp_bytes = 2 * FF_ * grb + D_ * drb
+    step_bytes = [len(np.unique(ids[i])) * exp_bytes + 2 * NB * D_ * 4 for i in range(NS)]
+
+    def step(i):
+        s_ = i % NS
+        rc = hip.eahmmf_hip_moe_grouped_async(ctypes.byref(shape), vp(tables[i % R].data_ptr()), E_,
+                                              vp(dids[s_].data_ptr()), vp(dw[s_].data_ptr()), NB, K_,
+                                              vp(dx[s_].data_ptr()), vp(dy[s_].data_ptr()), sp)
+        assert rc == 0, b.last_error()
+
+    steps = args.steps if args.steps else 50
+    for i in range(args.warmup if args.warmup else 5):
+        step(i)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for i in range(steps):
+        step(i)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    el = e0.elapsed_time(e1) * 1e-3
+    total = sum(step_bytes[i % NS] for i in range(steps))
+    flop = NB * K_ * 2 * (3 * D_ * FF_)
+    gbs = total / el / 1e9
+    print(json.dumps({
+        "metric": "grouped prefill expert-FFN HBM GB/s (% of peak)", "value": round(gbs, 2), "unit": "GB/s",
+        "n_gpus": 1, "steps": steps, "ms_per_step": round(el * 1e3 / steps, 4), "higher_is_better": True,
+        "dtype": "f32", "data": "synthetic",
+        "config": {"workload": "ragged grouped prefill: 512 tokens x top-8 over 128 Zipf(1.1) experts, "
+                               "D=2048 FF=768, Q4_K gate/up + Q6_K down", "layer_replicas": R,
+                   "distinct_experts_per_step": [len(np.unique(ids[i])) for i in range(NS)],
+                   "bytes_per_step_avg": int(np.mean(step_bytes))},
+        "pct_of_hbm_peak": round(100 * gbs / HBM_PEAK_GBS, 2),
+        "tflops": round(flop * steps / el / 1e12, 3)}), flush=True)
+
+
+def bench_c5(args, torch, b, hip):
+    """Single decode token through one MoE layer at the Qwen3-235B-A22B expert
+    shape (D=4096, FF=1536, 128 experts, top-8, Q4_K/Q6_K), routing on device."""
+    D_, FF_, E_, K_ = 4096, 1536, 128, 8
+    rng = np.random.default_rng(5)
+    uniq, grb, drb = build_layer_replicated(b, rng, D_, FF_, E_, 16)
+    R = args.replicas if args.replicas else 4
+    comps, tables = upload_layers(torch, uniq, E_, R)
+    shape = b.MoeShape(Q4_K, Q4_K, Q6_K, D_, FF_, grb, grb, drb)
+    NS = 64
+    xs = torch.from_numpy(rng.normal(0, 1, (NS, D_)).astype(np.float32)).cuda()
+    dl = torch.from_numpy(rng.normal(0, 1, (NS, E_)).astype(np.float32)).cuda()
+    dy = torch.empty((NS, D_), dtype=torch.float32, device="cuda")
+    stream = torch.cuda.current_stream()
+    sp, vp = ctypes.c_void_p(stream.cuda_stream), ctypes.c_void_p
+
+    def step(i):
+        s_ = i % NS
+        rc = hip.eahmmf_hip_moe_layer_decode_async(ctypes.byref(shape), vp(tables[i % R].data_ptr()), E_,
+                                                   vp(dl[s_].data_ptr()), K_, vp(xs[s_].data_ptr()),
+                                                   vp(dy[s_].data_ptr()), None, None, sp)
+        assert rc == 0, b.last_error()
+
+    steps = args.steps if args.steps else 1000
+    for i in range(args.warmup if args.warmup else 50):
+        step(i)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for i in range(steps):
+        step(i)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    assert hip.eahmmf_hip_device_flags() == 0
+    el = e0.elapsed_time(e1) * 1e-3
+    bytes_step = K_ * (2 * FF_ * grb + D_ * drb)
+    gbs = bytes_step * steps / el / 1e9
+    print(json.dumps({
+        "metric": "expert-FFN HBM GB/s (% of peak) + decode tokens/s, Qwen3-235B-A22B shape", "value": round(gbs, 2),
+        "unit": "GB/s", "n_gpus": 1, "steps": steps, "ms_per_step": round(el * 1e3 / steps, 5),
+        "higher_is_better": True, "dtype": "f32", "data": "synthetic",
+        "config": {"workload": "single MoE layer, one decode token, D=4096 FF=1536 128 experts top-8, "
+                               "Q4_K gate/up + Q6_K down, routing on device", "bytes_per_step": bytes_step,
+                   "layer_replicas": R},
+        "pct_of_hbm_peak": round(100 * gbs / HBM_PEAK_GBS, 2),
+        "expert_only_decode_tokens_per_s_94_layers": round(1.0 / (94 * el / steps), 1)}), flush=True)
+
+
 def cpu_baseline(gate, up, down, xs, logits, budget_s):
     """Times the reference CPU expert path on a bounded sample of layer-tokens:
     the compiled reference's own matmul (oracle/_ref) when present, else the
@@ -135,14 +280,21 @@ def calibrate_copy(torch, steps):
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=2000)
-    ap.add_argument("--warmup", type=int, default=100)
-    ap.add_argument("--replicas", type=int, default=16)
+    ap.add_argument("--steps", type=int, default=None, help="timed steps (c2 2000, c4 50, c5 1000)")
+    ap.add_argument("--warmup", type=int, default=None, help="untimed steps (c2 100, c4 5, c5 50)")
+    ap.add_argument("--replicas", type=int, default=None, help="layer copies in HBM (c2 16, c4 4, c5 4)")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--workload", choices=("c2", "c4", "c5"), default="c2",
+                    help="c2 (default): the headline single-token layer; c4: ragged grouped prefill; "
+                         "c5: single-token layer at the 235B shape")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a plain 256 MiB device copy (the reference kernel for scaling HBM counters)")
     args = ap.parse_args()
+    if args.workload == "c2":
+        args.steps = 2000 if args.steps is None else args.steps
+        args.warmup = 100 if args.warmup is None else args.warmup
+        args.replicas = 16 if args.replicas is None else args.replicas
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only (asked for --gpus {args.gpus}); the expert path shards by expert "
               "across GPUs, which this build does not run", file=sys.stderr)
@@ -150,9 +302,14 @@ def main():
 
     import torch
     if args.calibrate_copy:
-        calibrate_copy(torch, args.steps)
+        calibrate_copy(torch, args.steps or 20)
         return
     b = load_binding()
+    if args.workload != "c2":
+        hip_ = b.lib()
+        torch.cuda.set_device(0)
+        (bench_c4 if args.workload == "c4" else bench_c5)(args, torch, b, hip_)
+        return
     hip = b.lib()
     torch.cuda.set_device(0)
     rng = np.random.default_rng(0)

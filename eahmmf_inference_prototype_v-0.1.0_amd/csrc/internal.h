@@ -85,6 +85,20 @@ hipError_t launch_moe_grouped(const MoeShape& s, const ExpertEntry* table, int n
                               const float* w, int nb, int k, const float* x, int ldx, float* y, int ldy,
                               void* scratch, hipStream_t st);
 
+// Matrix-core matmuls of the grouped block (kernels_grouped_mfma.hip).
+bool grouped_mfma_gate_up_ok(const MoeShape& s);
+bool grouped_mfma_down_ok(const MoeShape& s);
+hipError_t launch_prep_rows(const int* offs, int E, const int* tok, const float* src, int ld, int n, int P,
+                            _Float16* vh, _Float16* vl, _Float16* sh, _Float16* sl, float* vscale, hipStream_t st);
+hipError_t launch_gate_up_mfma(const MoeShape& s, const ExpertEntry* table, int E, const int* offs, int nb,
+                               const _Float16* xh, const _Float16* xl, const _Float16* xsh, const _Float16* xsl,
+                               const float* xscale, float* h, hipStream_t st);
+hipError_t launch_down_mfma(const MoeShape& s, const ExpertEntry* table, int E, const int* offs, int nb,
+                            const _Float16* hh, const _Float16* hl, const float* hscale, float* yp, hipStream_t st);
+// 1 (default): the grouped block uses the matrix-core matmuls where the formats
+// allow; 0: the vector-ALU kernels only.  A negative argument only queries.
+int set_grouped_mfma(int enable);
+
 // softmax -> top-k (e desc, index asc) -> renormalise; logits [nb][n_expert].
 hipError_t launch_route_topk(const float* logits, int nb, int n_expert, int k, int* ids, float* w, hipStream_t st);
 

@@ -17,9 +17,11 @@
 //        offs[e]      first position of expert e's group
 //        tok[p], pw[p] token and router weight at position p
 //        pos[t*k+j]   position of (token t, slot j), -1 for an invalid id
-//   2. grouped gate/up: one wave per (expert, FF row), tokens of the group in
-//      tiles of 8: h[p][r] = silu(gate_r . x_tok[p]) * (up_r . x_tok[p]).
-//   3. grouped down: one wave per (expert, D row): yp[p][r] = down_r . h[p].
+//   2. grouped gate/up: h[p][r] = silu(gate_r . x_tok[p]) * (up_r . x_tok[p]);
+//      on the matrix cores for Q4_K/Q5_K (kernels_grouped_mfma.hip), else one
+//      wave per (expert, FF row) with the group's tokens in tiles of 8.
+//   3. grouped down: yp[p][r] = down_r . h[p]; matrix cores for Q6_K, else one
+//      wave per (expert, D row).
 //   4. combine: y[t] = sum over the token's pairs in ascending expert id of
 //      w * yp[pos] (fma), the reference's accumulation order.
 // Expert weights are read once per (expert, row) however many tokens the
@@ -282,11 +284,22 @@ static hipError_t gate_up_for(int ut, const MoeShape& s, dim3 g, const ExpertEnt
     return hipSuccess;
 }
 
+int g_grouped_mfma = 1;  // matrix-core matmuls where the formats allow (see kernels_grouped_mfma.hip)
+
+int set_grouped_mfma(int enable) {
+    const int prev = g_grouped_mfma;
+    if (enable >= 0) g_grouped_mfma = enable ? 1 : 0;
+    return prev;
+}
+
 size_t grouped_scratch_bytes(const MoeShape& s, int nb, int k, int n_expert) {
     const size_t P = (size_t)nb * k, nchunks = ((size_t)nb + 63) / 64;
     auto al = [](size_t b) { return (b + 255) & ~(size_t)255; };
-    return al(nchunks * n_expert * 4) + al(((size_t)n_expert + 1) * 4) + 3 * al(P * 4) + al(P * s.FF * 4) +
-           al(P * s.D * 4);
+    const size_t base = al(nchunks * n_expert * 4) + al(((size_t)n_expert + 1) * 4) + 3 * al(P * 4) +
+                        al(P * s.FF * 4) + al(P * s.D * 4);
+    // fp16 hi/lo activations and sub-block sums for the matrix-core path
+    const size_t mf = 2 * al(P * s.D * 2) + 2 * al(P * (s.D / 32) * 2) + al(P * 4) + 2 * al(P * s.FF * 2) + al(P * 4);
+    return base + mf;
 }
 
 bool grouped_supported(const MoeShape& s, int nb, int k, int n_expert) {
@@ -308,31 +321,55 @@ hipError_t launch_moe_grouped(const MoeShape& s, const ExpertEntry* table, int n
     float* pw = reinterpret_cast<float*>(b); b += al(P * 4);
     int* pos = reinterpret_cast<int*>(b); b += al(P * 4);
     float* h = reinterpret_cast<float*>(b); b += al(P * s.FF * 4);
-    float* yp = reinterpret_cast<float*>(b);
+    float* yp = reinterpret_cast<float*>(b); b += al(P * s.D * 4);
+    _Float16* xh = reinterpret_cast<_Float16*>(b); b += al(P * s.D * 2);
+    _Float16* xl = reinterpret_cast<_Float16*>(b); b += al(P * s.D * 2);
+    _Float16* xsh = reinterpret_cast<_Float16*>(b); b += al(P * (s.D / 32) * 2);
+    _Float16* xsl = reinterpret_cast<_Float16*>(b); b += al(P * (s.D / 32) * 2);
+    float* xsc = reinterpret_cast<float*>(b); b += al(P * 4);
+    _Float16* hh = reinterpret_cast<_Float16*>(b); b += al(P * s.FF * 2);
+    _Float16* hl = reinterpret_cast<_Float16*>(b); b += al(P * s.FF * 2);
+    float* hsc = reinterpret_cast<float*>(b);
+    const bool mf_gu = g_grouped_mfma && grouped_mfma_gate_up_ok(s);
+    const bool mf_dn = g_grouped_mfma && grouped_mfma_down_ok(s);
     clear_stale_error();
     const size_t lds = (size_t)kGroupWaves * n_expert * 8 + (size_t)n_expert * 4;
     group_pairs_kernel<<<1, kGroupThreads, lds, st>>>(ids, w, nb, k, n_expert, cnt, offs, tok, pw, pos);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    const dim3 ga((unsigned)((s.FF + 3) / 4), (unsigned)n_expert);
-    switch (s.gate_type) {
-        case kQ4_K: e = gate_up_for<kQ4_K>(s.up_type, s, ga, table, offs, tok, x, ldx, h, st); break;
-        case kQ5_K: e = gate_up_for<kQ5_K>(s.up_type, s, ga, table, offs, tok, x, ldx, h, st); break;
-        case kQ6_K: e = gate_up_for<kQ6_K>(s.up_type, s, ga, table, offs, tok, x, ldx, h, st); break;
-        case kQ8_0: e = gate_up_for<kQ8_0>(s.up_type, s, ga, table, offs, tok, x, ldx, h, st); break;
-        default: e = hipErrorInvalidValue;
+    if (mf_gu) {
+        if ((e = launch_prep_rows(offs, n_expert, tok, x, ldx, s.D, (int)P, xh, xl, xsh, xsl, xsc, st)) != hipSuccess)
+            return e;
+        if ((e = launch_gate_up_mfma(s, table, n_expert, offs, nb, xh, xl, xsh, xsl, xsc, h, st)) != hipSuccess)
+            return e;
+    } else {
+        const dim3 ga((unsigned)((s.FF + 3) / 4), (unsigned)n_expert);
+        switch (s.gate_type) {
+            case kQ4_K: e = gate_up_for<kQ4_K>(s.up_type, s, ga, table, offs, tok, x, ldx, h, st); break;
+            case kQ5_K: e = gate_up_for<kQ5_K>(s.up_type, s, ga, table, offs, tok, x, ldx, h, st); break;
+            case kQ6_K: e = gate_up_for<kQ6_K>(s.up_type, s, ga, table, offs, tok, x, ldx, h, st); break;
+            case kQ8_0: e = gate_up_for<kQ8_0>(s.up_type, s, ga, table, offs, tok, x, ldx, h, st); break;
+            default: e = hipErrorInvalidValue;
+        }
+        if (e != hipSuccess) return e;
+        if ((e = hipGetLastError()) != hipSuccess) return e;
     }
-    if (e != hipSuccess) return e;
-    if ((e = hipGetLastError()) != hipSuccess) return e;
-    const dim3 gd((unsigned)((s.D + 3) / 4), (unsigned)n_expert);
-    switch (s.down_type) {
-        case kQ4_K: grouped_down_kernel<kQ4_K><<<gd, 256, 0, st>>>(s, table, offs, h, yp); break;
-        case kQ5_K: grouped_down_kernel<kQ5_K><<<gd, 256, 0, st>>>(s, table, offs, h, yp); break;
-        case kQ6_K: grouped_down_kernel<kQ6_K><<<gd, 256, 0, st>>>(s, table, offs, h, yp); break;
-        case kQ8_0: grouped_down_kernel<kQ8_0><<<gd, 256, 0, st>>>(s, table, offs, h, yp); break;
-        default: return hipErrorInvalidValue;
+    if (mf_dn) {
+        if ((e = launch_prep_rows(offs, n_expert, nullptr, h, s.FF, s.FF, (int)P, hh, hl, nullptr, nullptr, hsc, st)) !=
+            hipSuccess)
+            return e;
+        if ((e = launch_down_mfma(s, table, n_expert, offs, nb, hh, hl, hsc, yp, st)) != hipSuccess) return e;
+    } else {
+        const dim3 gd((unsigned)((s.D + 3) / 4), (unsigned)n_expert);
+        switch (s.down_type) {
+            case kQ4_K: grouped_down_kernel<kQ4_K><<<gd, 256, 0, st>>>(s, table, offs, h, yp); break;
+            case kQ5_K: grouped_down_kernel<kQ5_K><<<gd, 256, 0, st>>>(s, table, offs, h, yp); break;
+            case kQ6_K: grouped_down_kernel<kQ6_K><<<gd, 256, 0, st>>>(s, table, offs, h, yp); break;
+            case kQ8_0: grouped_down_kernel<kQ8_0><<<gd, 256, 0, st>>>(s, table, offs, h, yp); break;
+            default: return hipErrorInvalidValue;
+        }
+        if ((e = hipGetLastError()) != hipSuccess) return e;
     }
-    if ((e = hipGetLastError()) != hipSuccess) return e;
     const size_t nthr = (size_t)nb * (s.D / 4);
     grouped_combine_kernel<<<(unsigned)((nthr + 255) / 256), 256, 0, st>>>(ids, pos, pw, nb, k, s.D, yp, y, ldy);
     return hipGetLastError();

@@ -1,0 +1,356 @@
+// kernels_grouped_mfma.hip - matrix-core (MFMA) matmuls of the ragged grouped
+// expert block for the K-quant formats of Q4_K_M layers: gate/up in Q4_K or
+// Q5_K, down in Q6_K.
+//
+// Exactness.  v_mfma_f32_16x16x32_f16 multiplies fp16 operands exactly and
+// accumulates in fp32, so it is fed only values that fp16 holds exactly:
+//   weights      small integers: Q4_K/Q5_K q*sc (<= 31*63 = 1953); Q6_K
+//                (q-32)*sc split as 16*(q-32)*(sc>>4) (a multiple of 16 with
+//                |.| <= 4096) plus (q-32)*(sc&15) (|.| <= 480)
+//   activations  each row scaled by a power of two so that max|v| < 2^13,
+//                then split v = hi + lo with hi = fp16(v), lo = fp16(v - hi)
+//                (about 22 significant bits)
+// The per-super-block factors (d, dmin: fp16 values) and the row's power of
+// two are applied in fp32 after each super-block, and the Q4_K/Q5_K min term
+// sum_j m_j * sum(x over sub-block j) is a second, small MFMA over the
+// sub-block sums.  So the products equal the reference's dequantized weight
+// times activation up to the fp32 rounding of the sums (the same bar as any
+// fp32 matmul).
+//
+// Operand layout (16x16x32): lane l holds A[l%16][8*(l/16) + i],
+// B[8*(l/16) + i][l%16] and C[4*(l/16) + i][l%16], i < 8 (C: i < 4).
+//
+// Work split: a workgroup is 4 waves x 16 rows = 64 output rows of one expert
+// and 64 of its grouped tokens (four 16-token tiles); grid.z walks the
+// expert's tokens in passes of 64 and workgroups past the end leave at once.
+#include "internal.h"
+#include "kquant.h"
+
+namespace eahmmf {
+
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kPassTok = 64;  // tokens per pass: four 16-token tiles
+constexpr int kWgRows = 64;   // rows per workgroup: four waves x 16
+constexpr float kSumScale = 1.0f / 16.0f;  // sub-block sums (32 values) kept below 2^14
+
+struct __attribute__((packed, aligned(2))) Bytes8A2 { uint32_t x, y; };
+__device__ __forceinline__ uint2 ld8_a2(const uint8_t* p) {
+    const Bytes8A2 v = *reinterpret_cast<const Bytes8A2*>(p);
+    return make_uint2(v.x, v.y);
+}
+__device__ __forceinline__ uint2 ld8(const uint8_t* p) { return *reinterpret_cast<const uint2*>(p); }
+
+// Two fp16 values b0, b1 from bytes 2m, 2m+1 of w (each < 256): the byte is
+// placed under the exponent of 1024 (0x64XX = 1024 + XX) and 1024 removed.
+template <int M>
+__device__ __forceinline__ f16x2 byte_pair(uint32_t w) {
+    constexpr uint32_t sel = M == 0 ? 0x04010400u : 0x04030402u;
+    const f16x2 v = __builtin_bit_cast(f16x2, __builtin_amdgcn_perm(0x64646464u, w, sel));
+    return v - (f16x2){(_Float16)1024.0f, (_Float16)1024.0f};
+}
+
+// Eight codes (bytes of c) times an integer factor f (|code * f| exact in fp16).
+__device__ __forceinline__ f16x8 codes_times(uint2 c, _Float16 f, _Float16 bias) {
+    const f16x2 fv = {f, f}, bv = {bias, bias};
+    const f16x2 a = (byte_pair<0>(c.x) + bv) * fv, b = (byte_pair<1>(c.x) + bv) * fv;
+    const f16x2 d = (byte_pair<0>(c.y) + bv) * fv, e = (byte_pair<1>(c.y) + bv) * fv;
+    return (f16x8){a.x, a.y, b.x, b.y, d.x, d.y, e.x, e.y};
+}
+
+__device__ __forceinline__ f32x4 mfma(f16x8 a, f16x8 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ float half_at(const uint8_t* p) {
+    return (float)__builtin_bit_cast(_Float16, *reinterpret_cast<const uint16_t*>(p));
+}
+
+// ---------------------------------------------------------------------------
+// Activation rows -> scaled fp16 hi/lo (+ 32-value sums).  One workgroup per
+// position q < offs[E]; the row is src + (tok ? tok[q] : q) * ld, n values.
+__global__ __launch_bounds__(256) void prep_rows_kernel(const int* __restrict__ offs, int E,
+                                                        const int* __restrict__ tok, const float* __restrict__ src,
+                                                        int ld, int n, _Float16* __restrict__ vh,
+                                                        _Float16* __restrict__ vl, _Float16* __restrict__ sh,
+                                                        _Float16* __restrict__ sl, float* __restrict__ vscale) {
+    __shared__ float wmax[4];
+    const int q = blockIdx.x;
+    if (q >= offs[E]) return;
+    const float* row = src + (size_t)(tok ? tok[q] : q) * ld;
+    const int tid = threadIdx.x;
+    float m = 0.f;
+    for (int c = tid; c < n / 8; c += 256) {
+        const float4 a = reinterpret_cast<const float4*>(row)[2 * c], b = reinterpret_cast<const float4*>(row)[2 * c + 1];
+        m = fmaxf(m, fmaxf(fmaxf(fabsf(a.x), fabsf(a.y)), fmaxf(fabsf(a.z), fabsf(a.w))));
+        m = fmaxf(m, fmaxf(fmaxf(fabsf(b.x), fabsf(b.y)), fmaxf(fabsf(b.z), fabsf(b.w))));
+    }
+    for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
+    if ((tid & 63) == 0) wmax[tid >> 6] = m;
+    __syncthreads();
+    m = fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
+    int ex = 0;
+    if (m > 0.f) (void)frexpf(m, &ex);  // m < 2^ex
+    const float up = ldexpf(1.0f, 13 - ex), down = ldexpf(1.0f, ex - 13);
+    if (tid == 0) vscale[q] = m > 0.f ? down : 1.0f;
+    const float sc = m > 0.f ? up : 1.0f;
+    for (int c = tid; c < n / 8; c += 256) {  // a 32-value block is four consecutive c (lanes)
+        const float4 a = reinterpret_cast<const float4*>(row)[2 * c], b = reinterpret_cast<const float4*>(row)[2 * c + 1];
+        const float v[8] = {a.x * sc, a.y * sc, a.z * sc, a.w * sc, b.x * sc, b.y * sc, b.z * sc, b.w * sc};
+        f16x8 hi, lo;
+        float s = 0.f;
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            hi[i] = (_Float16)v[i];
+            lo[i] = (_Float16)(v[i] - (float)hi[i]);
+            s += v[i];
+        }
+        *reinterpret_cast<f16x8*>(vh + (size_t)q * n + 8 * c) = hi;
+        *reinterpret_cast<f16x8*>(vl + (size_t)q * n + 8 * c) = lo;
+        if (sh) {
+            s += __shfl_xor(s, 1, 64);
+            s += __shfl_xor(s, 2, 64);
+            if ((c & 3) == 0) {
+                const float ss = s * kSumScale;
+                const _Float16 h = (_Float16)ss;
+                sh[(size_t)q * (n / 32) + c / 4] = h;
+                sl[(size_t)q * (n / 32) + c / 4] = (_Float16)(ss - (float)h);
+            }
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// gate/up (Q4_K or Q5_K, same type) for one expert: h[q][r] = silu(g) * u.
+template <int T>
+__global__ __launch_bounds__(256) void gate_up_mfma_kernel(MoeShape s, const ExpertEntry* __restrict__ table,
+                                                           const int* __restrict__ offs,
+                                                           const _Float16* __restrict__ xh,
+                                                           const _Float16* __restrict__ xl,
+                                                           const _Float16* __restrict__ xsh,
+                                                           const _Float16* __restrict__ xsl,
+                                                           const float* __restrict__ xscale, float* __restrict__ h) {
+    static_assert(T == kQ4_K || T == kQ5_K, "gate/up MFMA path: Q4_K or Q5_K");
+    constexpr int BB = Fmt<T>::bytes;
+    constexpr int QS = T == kQ5_K ? 48 : 16;  // offset of the 4-bit codes in a super-block
+    const int e = blockIdx.y;
+    const int p0 = offs[e], p1 = offs[e + 1];
+    const int pb = p0 + (int)blockIdx.z * kPassTok;
+    if (pb >= p1) return;
+    const int wave = threadIdx.x >> 6, l = threadIdx.x & 63;
+    const int r0 = blockIdx.x * kWgRows + wave * 16;
+    if (r0 >= s.FF) return;  // whole wave
+    const int lr = l & 15, kq = l >> 4;
+    const int D = s.D, nsb = D / 256, nsub = D / 32;
+    const ExpertEntry ent = table[e];
+    const uint8_t* ga = ent.gate + (size_t)(r0 + lr) * s.gate_rb;
+    const uint8_t* ua = ent.up + (size_t)(r0 + lr) * s.up_rb;
+    int qp[4];
+    bool qok[4], tile[4];
+#pragma unroll
+    for (int nt = 0; nt < 4; nt++) {
+        qp[nt] = pb + nt * 16 + lr;
+        qok[nt] = qp[nt] < p1;
+        tile[nt] = pb + nt * 16 < p1;  // wave-uniform
+    }
+    const f16x8 zero8 = {};
+    f32x4 og[4], ou[4];
+#pragma unroll
+    for (int nt = 0; nt < 4; nt++) og[nt] = ou[nt] = (f32x4){0.f, 0.f, 0.f, 0.f};
+    for (int b = 0; b < nsb; b++) {
+        const uint8_t* gb = ga + (size_t)b * BB;
+        const uint8_t* ub = ua + (size_t)b * BB;
+        const uint4 gh = *reinterpret_cast<const uint4*>(gb), uh = *reinterpret_cast<const uint4*>(ub);
+        uint2 gqh = make_uint2(0, 0), uqh = make_uint2(0, 0);
+        if (T == kQ5_K) {
+            gqh = ld8(gb + 16 + kq * 8);
+            uqh = ld8(ub + 16 + kq * 8);
+        }
+        f32x4 ag[4], au[4];
+#pragma unroll
+        for (int nt = 0; nt < 4; nt++) ag[nt] = au[nt] = (f32x4){0.f, 0.f, 0.f, 0.f};
+        f16x8 mg = zero8, mu = zero8;  // mins m_0..m_7 of this lane's row (used on lanes kq == 0)
+#pragma unroll
+        for (int g = 0; g < 4; g++) {
+            const uint2 gq = ld8(gb + QS + 32 * g + kq * 8), uq = ld8(ub + QS + 32 * g + kq * 8);
+#pragma unroll
+            for (int hh = 0; hh < 2; hh++) {
+                const int j = 2 * g + hh;
+                uint32_t scg, mng, scu, mnu;
+                scale_min_k4(j, gh.y, gh.z, gh.w, scg, mng);
+                scale_min_k4(j, uh.y, uh.z, uh.w, scu, mnu);
+                mg[j] = (_Float16)(float)mng;
+                mu[j] = (_Float16)(float)mnu;
+                uint2 cg = make_uint2((gq.x >> (4 * hh)) & 0x0F0F0F0Fu, (gq.y >> (4 * hh)) & 0x0F0F0F0Fu);
+                uint2 cu = make_uint2((uq.x >> (4 * hh)) & 0x0F0F0F0Fu, (uq.y >> (4 * hh)) & 0x0F0F0F0Fu);
+                if (T == kQ5_K) {
+                    cg.x |= ((gqh.x >> j) & 0x01010101u) << 4;
+                    cg.y |= ((gqh.y >> j) & 0x01010101u) << 4;
+                    cu.x |= ((uqh.x >> j) & 0x01010101u) << 4;
+                    cu.y |= ((uqh.y >> j) & 0x01010101u) << 4;
+                }
+                const f16x8 Ag = codes_times(cg, (_Float16)(float)scg, (_Float16)0.0f);
+                const f16x8 Au = codes_times(cu, (_Float16)(float)scu, (_Float16)0.0f);
+                const int kk = b * 256 + 32 * j + kq * 8;
+#pragma unroll
+                for (int nt = 0; nt < 4; nt++) {
+                    if (!tile[nt]) continue;
+                    const f16x8 bh = qok[nt] ? *reinterpret_cast<const f16x8*>(xh + (size_t)qp[nt] * D + kk) : zero8;
+                    const f16x8 bl = qok[nt] ? *reinterpret_cast<const f16x8*>(xl + (size_t)qp[nt] * D + kk) : zero8;
+                    ag[nt] = mfma(Ag, bh, ag[nt]);
+                    ag[nt] = mfma(Ag, bl, ag[nt]);
+                    au[nt] = mfma(Au, bh, au[nt]);
+                    au[nt] = mfma(Au, bl, au[nt]);
+                }
+            }
+        }
+        // min term: sum_j m_j * (sum of x over sub-block j), K = the 8 sub-blocks
+        const f16x8 Amg = kq == 0 ? mg : zero8, Amu = kq == 0 ? mu : zero8;
+        f32x4 zg[4], zu[4];
+#pragma unroll
+        for (int nt = 0; nt < 4; nt++) {
+            zg[nt] = zu[nt] = (f32x4){0.f, 0.f, 0.f, 0.f};
+            if (!tile[nt]) continue;
+            const bool ld = kq == 0 && qok[nt];
+            const f16x8 sh8 = ld ? *reinterpret_cast<const f16x8*>(xsh + (size_t)qp[nt] * nsub + 8 * b) : zero8;
+            const f16x8 sl8 = ld ? *reinterpret_cast<const f16x8*>(xsl + (size_t)qp[nt] * nsub + 8 * b) : zero8;
+            zg[nt] = mfma(Amg, sh8, zg[nt]);
+            zg[nt] = mfma(Amg, sl8, zg[nt]);
+            zu[nt] = mfma(Amu, sh8, zu[nt]);
+            zu[nt] = mfma(Amu, sl8, zu[nt]);
+        }
+        // apply d, dmin of the rows this lane's accumulators hold (rows r0 + 4*kq + i)
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const uint8_t* gr = ent.gate + (size_t)(r0 + 4 * kq + i) * s.gate_rb + (size_t)b * BB;
+            const uint8_t* ur = ent.up + (size_t)(r0 + 4 * kq + i) * s.up_rb + (size_t)b * BB;
+            const float dg = half_at(gr), dmg = half_at(gr + 2) / kSumScale;
+            const float du = half_at(ur), dmu = half_at(ur + 2) / kSumScale;
+#pragma unroll
+            for (int nt = 0; nt < 4; nt++) {
+                og[nt][i] += dg * ag[nt][i] - dmg * zg[nt][i];
+                ou[nt][i] += du * au[nt][i] - dmu * zu[nt][i];
+            }
+        }
+    }
+#pragma unroll
+    for (int nt = 0; nt < 4; nt++) {
+        if (!qok[nt]) continue;
+        const float xs = xscale[qp[nt]];
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const float g = og[nt][i] * xs, u = ou[nt][i] * xs;
+            h[(size_t)qp[nt] * s.FF + r0 + 4 * kq + i] = g / (1.0f + expf(-g)) * u;
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// down (Q6_K) for one expert: yp[q][r] = down_r . h[q].
+__global__ __launch_bounds__(256) void down_mfma_q6k_kernel(MoeShape s, const ExpertEntry* __restrict__ table,
+                                                            const int* __restrict__ offs,
+                                                            const _Float16* __restrict__ hh,
+                                                            const _Float16* __restrict__ hl,
+                                                            const float* __restrict__ hscale,
+                                                            float* __restrict__ yp) {
+    const int e = blockIdx.y;
+    const int p0 = offs[e], p1 = offs[e + 1];
+    const int pb = p0 + (int)blockIdx.z * kPassTok;
+    if (pb >= p1) return;
+    const int wave = threadIdx.x >> 6, l = threadIdx.x & 63;
+    const int r0 = blockIdx.x * kWgRows + wave * 16;
+    if (r0 >= s.D) return;
+    const int lr = l & 15, kq = l >> 4;
+    const int FF = s.FF, nsb = FF / 256;
+    const uint8_t* dbase = table[e].down;
+    const uint8_t* da = dbase + (size_t)(r0 + lr) * s.down_rb;
+    int qp[4];
+    bool qok[4], tile[4];
+#pragma unroll
+    for (int nt = 0; nt < 4; nt++) {
+        qp[nt] = pb + nt * 16 + lr;
+        qok[nt] = qp[nt] < p1;
+        tile[nt] = pb + nt * 16 < p1;
+    }
+    const f16x8 zero8 = {};
+    f32x4 out[4];
+#pragma unroll
+    for (int nt = 0; nt < 4; nt++) out[nt] = (f32x4){0.f, 0.f, 0.f, 0.f};
+    for (int b = 0; b < nsb; b++) {
+        const uint8_t* blk = da + (size_t)b * 210;
+        f32x4 acc[4];
+#pragma unroll
+        for (int nt = 0; nt < 4; nt++) acc[nt] = (f32x4){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int c = 0; c < 8; c++) {  // 32-value chunk = quarter u of half n
+            const int n = c >> 2, u = c & 3;
+            const uint2 ql = ld8_a2(blk + 64 * n + 32 * (u & 1) + kq * 8);
+            const uint2 qh = ld8_a2(blk + 128 + 32 * n + kq * 8);
+            const int sc = (int)(int8_t)blk[192 + 8 * n + (kq >> 1) + 2 * u];
+            const int sh4 = u >= 2 ? 4 : 0;
+            const uint2 code = make_uint2(((ql.x >> sh4) & 0x0F0F0F0Fu) | (((qh.x >> (2 * u)) & 0x03030303u) << 4),
+                                          ((ql.y >> sh4) & 0x0F0F0F0Fu) | (((qh.y >> (2 * u)) & 0x03030303u) << 4));
+            const f16x8 A1 = codes_times(code, (_Float16)(float)(16 * (sc >> 4)), (_Float16)-32.0f);
+            const f16x8 A2 = codes_times(code, (_Float16)(float)(sc & 15), (_Float16)-32.0f);
+            const int kk = b * 256 + 32 * c + kq * 8;
+#pragma unroll
+            for (int nt = 0; nt < 4; nt++) {
+                if (!tile[nt]) continue;
+                const f16x8 bh = qok[nt] ? *reinterpret_cast<const f16x8*>(hh + (size_t)qp[nt] * FF + kk) : zero8;
+                const f16x8 bl = qok[nt] ? *reinterpret_cast<const f16x8*>(hl + (size_t)qp[nt] * FF + kk) : zero8;
+                acc[nt] = mfma(A1, bh, acc[nt]);
+                acc[nt] = mfma(A1, bl, acc[nt]);
+                acc[nt] = mfma(A2, bh, acc[nt]);
+                acc[nt] = mfma(A2, bl, acc[nt]);
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const float d = half_at(dbase + (size_t)(r0 + 4 * kq + i) * s.down_rb + (size_t)b * 210 + 208);
+#pragma unroll
+            for (int nt = 0; nt < 4; nt++) out[nt][i] += d * acc[nt][i];
+        }
+    }
+#pragma unroll
+    for (int nt = 0; nt < 4; nt++) {
+        if (!qok[nt]) continue;
+        const float hs = hscale[qp[nt]];
+#pragma unroll
+        for (int i = 0; i < 4; i++) yp[(size_t)qp[nt] * s.D + r0 + 4 * kq + i] = out[nt][i] * hs;
+    }
+}
+
+// ---------------------------------------------------------------------------
+bool grouped_mfma_gate_up_ok(const MoeShape& s) {
+    return (s.gate_type == kQ4_K || s.gate_type == kQ5_K) && s.up_type == s.gate_type && s.FF % 16 == 0 &&
+           s.D % 256 == 0;
+}
+bool grouped_mfma_down_ok(const MoeShape& s) { return s.down_type == kQ6_K && s.D % 16 == 0 && s.FF % 256 == 0; }
+
+hipError_t launch_prep_rows(const int* offs, int E, const int* tok, const float* src, int ld, int n, int P,
+                            _Float16* vh, _Float16* vl, _Float16* sh, _Float16* sl, float* vscale, hipStream_t st) {
+    prep_rows_kernel<<<(unsigned)P, 256, 0, st>>>(offs, E, tok, src, ld, n, vh, vl, sh, sl, vscale);
+    return hipGetLastError();
+}
+
+hipError_t launch_gate_up_mfma(const MoeShape& s, const ExpertEntry* table, int E, const int* offs, int nb,
+                               const _Float16* xh, const _Float16* xl, const _Float16* xsh, const _Float16* xsl,
+                               const float* xscale, float* h, hipStream_t st) {
+    const dim3 g((unsigned)((s.FF + kWgRows - 1) / kWgRows), (unsigned)E, (unsigned)((nb + kPassTok - 1) / kPassTok));
+    if (s.gate_type == kQ4_K)
+        gate_up_mfma_kernel<kQ4_K><<<g, 256, 0, st>>>(s, table, offs, xh, xl, xsh, xsl, xscale, h);
+    else
+        gate_up_mfma_kernel<kQ5_K><<<g, 256, 0, st>>>(s, table, offs, xh, xl, xsh, xsl, xscale, h);
+    return hipGetLastError();
+}
+
+hipError_t launch_down_mfma(const MoeShape& s, const ExpertEntry* table, int E, const int* offs, int nb,
+                            const _Float16* hh, const _Float16* hl, const float* hscale, float* yp, hipStream_t st) {
+    const dim3 g((unsigned)((s.D + kWgRows - 1) / kWgRows), (unsigned)E, (unsigned)((nb + kPassTok - 1) / kPassTok));
+    down_mfma_q6k_kernel<<<g, 256, 0, st>>>(s, table, offs, hh, hl, hscale, yp);
+    return hipGetLastError();
+}
+
+}  // namespace eahmmf

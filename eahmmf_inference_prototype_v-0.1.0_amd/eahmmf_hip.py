@@ -23,7 +23,7 @@ EXPORTS = (
     "eahmmf_hip_free", "eahmmf_hip_h2d", "eahmmf_hip_d2h", "eahmmf_hip_sync", "eahmmf_hip_mem_info",
     "eahmmf_hip_last_error", "eahmmf_hip_device_count", "eahmmf_hip_shutdown", "eahmmf_hip_moe_layer_decode_async",
     "eahmmf_hip_set_fused", "eahmmf_hip_device_flags", "eahmmf_hip_fused_exchange", "eahmmf_hip_moe_grouped",
-    "eahmmf_hip_moe_grouped_async",
+    "eahmmf_hip_moe_grouped_async", "eahmmf_hip_set_grouped_mfma",
 )
 
 
@@ -87,6 +87,7 @@ def load(path=LIB_PATH):
         "eahmmf_hip_set_fused": (c_int, [c_int]),
         "eahmmf_hip_device_flags": (c_int, []),
         "eahmmf_hip_fused_exchange": (c_int, []),
+        "eahmmf_hip_set_grouped_mfma": (c_int, [c_int]),
         "eahmmf_hip_moe_grouped": (c_bool, [ctypes.POINTER(Expert), c_int, vp, vp, vp, c_int, vp, vp]),
         "eahmmf_hip_moe_grouped_async": (c_int, [ctypes.POINTER(MoeShape), vp, c_int, vp, vp, c_int, c_int, vp, vp,
                                                  vp]),

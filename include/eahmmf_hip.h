@@ -175,6 +175,11 @@ int eahmmf_hip_set_fused(int enable);
  * on XCD b % 8, checked once per device), 0 through device-coherent memory,
  * -1 on error. */
 int eahmmf_hip_fused_exchange(void);
+/* Selects matrix-core (MFMA) matmuls in the grouped block where the formats
+ * allow (1, the default: Q4_K/Q5_K gate/up, Q6_K down) or the vector-ALU
+ * kernels only (0); a negative argument only queries.  Returns the previous
+ * setting. */
+int eahmmf_hip_set_grouped_mfma(int enable);
 /* Nonzero if a fused launch on the current device hit its bounded wait since
  * the last call (its output is then not valid); clears the flag. */
 int eahmmf_hip_device_flags(void);

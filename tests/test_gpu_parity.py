@@ -352,11 +352,20 @@ GROUPED_CASES = [
     ("c2_shape_q4_k_m", (Q4_K, Q4_K, Q6_K), 2048, 768, 16, 8, 40),
     ("c3_q5_k", (Q5_K, Q5_K, Q5_K), 2048, 768, 8, 4, 9),
     ("q8_0_down_ne0_96", (Q8_0, Q8_0, Q8_0), 128, 96, 6, 2, 130),
+    ("q5_k_gate_up_q6_k_down", (Q5_K, Q5_K, Q6_K), 1024, 512, 8, 4, 150),
+    ("c5_shape", (Q4_K, Q4_K, Q6_K), 4096, 1536, 4, 2, 33),
 ]
 
 
+@pytest.fixture(params=[1, 0], ids=["mfma", "valu"])
+def grouped_mode(request, hip):
+    prev = hip.eahmmf_hip_set_grouped_mfma(request.param)
+    yield request.param
+    hip.eahmmf_hip_set_grouped_mfma(prev)
+
+
 @pytest.mark.parametrize("name,types,D,FF,E,k,nb", GROUPED_CASES, ids=[c[0] for c in GROUPED_CASES])
-def test_grouped_vs_oracle(torch_dev, binding, hip, name, types, D, FF, E, k, nb):
+def test_grouped_vs_oracle(torch_dev, binding, hip, grouped_mode, name, types, D, FF, E, k, nb):
     """Host by_exp lists in, host y out: every token's y within tolerance of
     the oracle's MoE block over the same routing."""
     torch = torch_dev
@@ -387,7 +396,7 @@ def test_grouped_vs_oracle(torch_dev, binding, hip, name, types, D, FF, E, k, nb
 
 
 @pytest.mark.parametrize("nb,E,k,skew", [(64, 32, 8, 0.0), (200, 128, 8, 1.1), (1, 16, 4, 0.0), (129, 64, 6, 2.0)])
-def test_grouped_async_device_routing(torch_dev, binding, hip, nb, E, k, skew):
+def test_grouped_async_device_routing(torch_dev, binding, hip, grouped_mode, nb, E, k, skew):
     """Routing on the device (route_topk), grouping on the device, Zipf-skewed
     expert popularity: y of every token matches the oracle on the same ids."""
     torch = torch_dev
