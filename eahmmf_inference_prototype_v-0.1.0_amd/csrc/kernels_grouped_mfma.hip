@@ -20,9 +20,10 @@
 // Operand layout (16x16x32): lane l holds A[l%16][8*(l/16) + i],
 // B[8*(l/16) + i][l%16] and C[4*(l/16) + i][l%16], i < 8 (C: i < 4).
 //
-// Work split: a workgroup is 4 waves x 16 rows = 64 output rows of one expert
-// and 64 of its grouped tokens (four 16-token tiles); grid.z walks the
-// expert's tokens in passes of 64 and workgroups past the end leave at once.
+// Work split: a workgroup covers 64 of an expert's grouped tokens (four
+// 16-token tiles) and a block of its output rows (16 per wave); grid.z walks
+// the expert's tokens in passes of 64 and workgroups past the end leave at
+// once.
 #include "internal.h"
 #include "kquant.h"
 
@@ -124,8 +125,32 @@ __global__ __launch_bounds__(256) void prep_rows_kernel(const int* __restrict__ 
 
 // ---------------------------------------------------------------------------
 // gate/up (Q4_K or Q5_K, same type) for one expert: h[q][r] = silu(g) * u.
+//
+// A workgroup of 8 waves covers 128 rows (16 per wave) and 64 tokens.  The
+// tokens' fp16 hi/lo activations are staged through LDS in chunks of 64 K
+// values (double-buffered, shared by the 8 waves); the next chunk's
+// activations and weight bytes are loaded into registers while the current
+// chunk runs on the matrix cores.  The sub-block sums of the min term are
+// staged once per super-block.
+constexpr int kGuWaves = 8;
+constexpr int kGuRows = 16 * kGuWaves;
+constexpr int kChunkK = 64;
+constexpr int kBRow = kChunkK + 8;  // halfs per token row in LDS: 144 B, so 16 lanes' 16-B reads hit distinct banks
+
+struct GuLds {
+    _Float16 b[2][2][kPassTok][kBRow];  // [stage][hi, lo][token][k]
+    _Float16 sm[2][2][kPassTok][8];     // [super-block parity][hi, lo][token][sub-block]: scaled sums
+};
+
 template <int T>
-__global__ __launch_bounds__(256) void gate_up_mfma_kernel(MoeShape s, const ExpertEntry* __restrict__ table,
+struct GuA {  // one lane's weight bytes for a chunk (gate and up)
+    uint4 gh, uh;    // super-block headers (d, dmin, scales)
+    uint2 gqh, uqh;  // Q5_K high bits of the lane's 8 columns
+    uint2 gq, uq;    // 4-bit codes of the lane's 8 columns, both nibbles (sub-blocks 2g, 2g+1)
+};
+
+template <int T>
+__global__ __launch_bounds__(512) void gate_up_mfma_kernel(MoeShape s, const ExpertEntry* __restrict__ table,
                                                            const int* __restrict__ offs,
                                                            const _Float16* __restrict__ xh,
                                                            const _Float16* __restrict__ xl,
@@ -135,114 +160,193 @@ __global__ __launch_bounds__(256) void gate_up_mfma_kernel(MoeShape s, const Exp
     static_assert(T == kQ4_K || T == kQ5_K, "gate/up MFMA path: Q4_K or Q5_K");
     constexpr int BB = Fmt<T>::bytes;
     constexpr int QS = T == kQ5_K ? 48 : 16;  // offset of the 4-bit codes in a super-block
+    __shared__ GuLds L;
     const int e = blockIdx.y;
     const int p0 = offs[e], p1 = offs[e + 1];
     const int pb = p0 + (int)blockIdx.z * kPassTok;
-    if (pb >= p1) return;
-    const int wave = threadIdx.x >> 6, l = threadIdx.x & 63;
-    const int r0 = blockIdx.x * kWgRows + wave * 16;
-    if (r0 >= s.FF) return;  // whole wave
+    if (pb >= p1) return;  // whole workgroup
+    const int tid = threadIdx.x, wave = tid >> 6, l = tid & 63;
     const int lr = l & 15, kq = l >> 4;
-    const int D = s.D, nsb = D / 256, nsub = D / 32;
+    const int r0 = blockIdx.x * kGuRows + wave * 16;
+    const bool on = r0 < s.FF;  // wave-uniform; idle waves still stage and synchronise
+    const int D = s.D, nsub = D / 32, nch = D / kChunkK;
     const ExpertEntry ent = table[e];
-    const uint8_t* ga = ent.gate + (size_t)(r0 + lr) * s.gate_rb;
-    const uint8_t* ua = ent.up + (size_t)(r0 + lr) * s.up_rb;
-    int qp[4];
-    bool qok[4], tile[4];
+    const uint8_t* ga = ent.gate + (size_t)(on ? r0 + lr : 0) * s.gate_rb;
+    const uint8_t* ua = ent.up + (size_t)(on ? r0 + lr : 0) * s.up_rb;
+    bool tile[4];
 #pragma unroll
-    for (int nt = 0; nt < 4; nt++) {
-        qp[nt] = pb + nt * 16 + lr;
-        qok[nt] = qp[nt] < p1;
-        tile[nt] = pb + nt * 16 < p1;  // wave-uniform
-    }
-    const f16x8 zero8 = {};
-    f32x4 og[4], ou[4];
-#pragma unroll
-    for (int nt = 0; nt < 4; nt++) og[nt] = ou[nt] = (f32x4){0.f, 0.f, 0.f, 0.f};
-    for (int b = 0; b < nsb; b++) {
+    for (int nt = 0; nt < 4; nt++) tile[nt] = pb + nt * 16 < p1;
+    // staging: thread -> (token, 8 k values) of a chunk, hi and lo
+    const int st_t = tid >> 3, st_k = (tid & 7) * 8;
+    const bool st_ok = pb + st_t < p1;
+    const size_t st_row = (size_t)(pb + st_t) * D;
+    auto gload = [&](int c, uint4& vh, uint4& vl) {
+        if (st_ok) {
+            vh = *reinterpret_cast<const uint4*>(xh + st_row + (size_t)c * kChunkK + st_k);
+            vl = *reinterpret_cast<const uint4*>(xl + st_row + (size_t)c * kChunkK + st_k);
+        } else {
+            vh = vl = make_uint4(0, 0, 0, 0);
+        }
+    };
+    // sums of a super-block: threads 0..127 stage one 16-B piece each
+    auto sload = [&](int b, uint4& v) {
+        v = make_uint4(0, 0, 0, 0);
+        if (tid < 2 * kPassTok) {
+            const int t = tid & (kPassTok - 1);
+            if (pb + t < p1)
+                v = *reinterpret_cast<const uint4*>((tid < kPassTok ? xsh : xsl) + (size_t)(pb + t) * nsub + 8 * b);
+        }
+    };
+    auto swrite_sums = [&](int b, uint4 v) {
+        if (tid < 2 * kPassTok)
+            *reinterpret_cast<uint4*>(&L.sm[b & 1][tid >= kPassTok][tid & (kPassTok - 1)][0]) = v;
+    };
+    auto aload = [&](int c, GuA<T>& a) {
+        const int b = c >> 2, g = c & 3;
         const uint8_t* gb = ga + (size_t)b * BB;
         const uint8_t* ub = ua + (size_t)b * BB;
-        const uint4 gh = *reinterpret_cast<const uint4*>(gb), uh = *reinterpret_cast<const uint4*>(ub);
-        uint2 gqh = make_uint2(0, 0), uqh = make_uint2(0, 0);
-        if (T == kQ5_K) {
-            gqh = ld8(gb + 16 + kq * 8);
-            uqh = ld8(ub + 16 + kq * 8);
+        if (g == 0) {
+            a.gh = *reinterpret_cast<const uint4*>(gb);
+            a.uh = *reinterpret_cast<const uint4*>(ub);
+            if (T == kQ5_K) {
+                a.gqh = ld8(gb + 16 + kq * 8);
+                a.uqh = ld8(ub + 16 + kq * 8);
+            }
         }
-        f32x4 ag[4], au[4];
+        a.gq = ld8(gb + QS + 32 * g + kq * 8);
+        a.uq = ld8(ub + QS + 32 * g + kq * 8);
+    };
+    // (d, dmin) of the rows this lane's accumulators hold, for super-block b
+    auto dload = [&](int b, uint32_t (&dg)[4], uint32_t (&du)[4]) {
 #pragma unroll
-        for (int nt = 0; nt < 4; nt++) ag[nt] = au[nt] = (f32x4){0.f, 0.f, 0.f, 0.f};
-        f16x8 mg = zero8, mu = zero8;  // mins m_0..m_7 of this lane's row (used on lanes kq == 0)
+        for (int i = 0; i < 4; i++) {
+            const size_t row = (size_t)(on ? r0 + 4 * kq + i : 0);
+            dg[i] = *reinterpret_cast<const uint32_t*>(ent.gate + row * s.gate_rb + (size_t)b * BB);
+            du[i] = *reinterpret_cast<const uint32_t*>(ent.up + row * s.up_rb + (size_t)b * BB);
+        }
+    };
+
+    GuA<T> cur{}, nxt{};
+    uint32_t dgc[4], duc[4], dgn[4] = {}, dun[4] = {};
+    uint4 vh, vl, vs;
+    if (on) {
+        aload(0, cur);
+        dload(0, dgc, duc);
+    }
+    gload(0, vh, vl);
+    sload(0, vs);
+    *reinterpret_cast<uint4*>(&L.b[0][0][st_t][st_k]) = vh;
+    *reinterpret_cast<uint4*>(&L.b[0][1][st_t][st_k]) = vl;
+    swrite_sums(0, vs);
+    __syncthreads();
+
+    const f16x8 zero8 = {};
+    f32x4 og[4], ou[4], ag[4], au[4];
 #pragma unroll
-        for (int g = 0; g < 4; g++) {
-            const uint2 gq = ld8(gb + QS + 32 * g + kq * 8), uq = ld8(ub + QS + 32 * g + kq * 8);
+    for (int nt = 0; nt < 4; nt++) og[nt] = ou[nt] = ag[nt] = au[nt] = (f32x4){0.f, 0.f, 0.f, 0.f};
+    f16x8 mg = zero8, mu = zero8;
+    for (int c = 0; c < nch; c++) {
+        const int stg = c & 1, b = c >> 2, g = c & 3;
+        const bool more = c + 1 < nch;
+        const bool next_sb = more && ((c + 1) & 3) == 0;
+        if (more) {
+            gload(c + 1, vh, vl);
+            if (next_sb) sload((c + 1) >> 2, vs);
+            if (on) {
+                aload(c + 1, nxt);
+                if (next_sb) dload((c + 1) >> 2, dgn, dun);
+            }
+        }
+        if (on) {
+            if (g == 0) {
+#pragma unroll
+                for (int nt = 0; nt < 4; nt++) ag[nt] = au[nt] = (f32x4){0.f, 0.f, 0.f, 0.f};
+            }
 #pragma unroll
             for (int hh = 0; hh < 2; hh++) {
                 const int j = 2 * g + hh;
                 uint32_t scg, mng, scu, mnu;
-                scale_min_k4(j, gh.y, gh.z, gh.w, scg, mng);
-                scale_min_k4(j, uh.y, uh.z, uh.w, scu, mnu);
+                scale_min_k4(j, cur.gh.y, cur.gh.z, cur.gh.w, scg, mng);
+                scale_min_k4(j, cur.uh.y, cur.uh.z, cur.uh.w, scu, mnu);
                 mg[j] = (_Float16)(float)mng;
                 mu[j] = (_Float16)(float)mnu;
-                uint2 cg = make_uint2((gq.x >> (4 * hh)) & 0x0F0F0F0Fu, (gq.y >> (4 * hh)) & 0x0F0F0F0Fu);
-                uint2 cu = make_uint2((uq.x >> (4 * hh)) & 0x0F0F0F0Fu, (uq.y >> (4 * hh)) & 0x0F0F0F0Fu);
+                uint2 cg = make_uint2((cur.gq.x >> (4 * hh)) & 0x0F0F0F0Fu, (cur.gq.y >> (4 * hh)) & 0x0F0F0F0Fu);
+                uint2 cu = make_uint2((cur.uq.x >> (4 * hh)) & 0x0F0F0F0Fu, (cur.uq.y >> (4 * hh)) & 0x0F0F0F0Fu);
                 if (T == kQ5_K) {
-                    cg.x |= ((gqh.x >> j) & 0x01010101u) << 4;
-                    cg.y |= ((gqh.y >> j) & 0x01010101u) << 4;
-                    cu.x |= ((uqh.x >> j) & 0x01010101u) << 4;
-                    cu.y |= ((uqh.y >> j) & 0x01010101u) << 4;
+                    cg.x |= ((cur.gqh.x >> j) & 0x01010101u) << 4;
+                    cg.y |= ((cur.gqh.y >> j) & 0x01010101u) << 4;
+                    cu.x |= ((cur.uqh.x >> j) & 0x01010101u) << 4;
+                    cu.y |= ((cur.uqh.y >> j) & 0x01010101u) << 4;
                 }
                 const f16x8 Ag = codes_times(cg, (_Float16)(float)scg, (_Float16)0.0f);
                 const f16x8 Au = codes_times(cu, (_Float16)(float)scu, (_Float16)0.0f);
-                const int kk = b * 256 + 32 * j + kq * 8;
 #pragma unroll
                 for (int nt = 0; nt < 4; nt++) {
                     if (!tile[nt]) continue;
-                    const f16x8 bh = qok[nt] ? *reinterpret_cast<const f16x8*>(xh + (size_t)qp[nt] * D + kk) : zero8;
-                    const f16x8 bl = qok[nt] ? *reinterpret_cast<const f16x8*>(xl + (size_t)qp[nt] * D + kk) : zero8;
+                    const f16x8 bh = *reinterpret_cast<const f16x8*>(&L.b[stg][0][nt * 16 + lr][hh * 32 + kq * 8]);
+                    const f16x8 bl = *reinterpret_cast<const f16x8*>(&L.b[stg][1][nt * 16 + lr][hh * 32 + kq * 8]);
                     ag[nt] = mfma(Ag, bh, ag[nt]);
                     ag[nt] = mfma(Ag, bl, ag[nt]);
                     au[nt] = mfma(Au, bh, au[nt]);
                     au[nt] = mfma(Au, bl, au[nt]);
                 }
             }
+            if (g == 3) {  // end of the super-block: min term, then d / dmin
+                const f16x8 Amg = kq == 0 ? mg : zero8, Amu = kq == 0 ? mu : zero8;
+#pragma unroll
+                for (int nt = 0; nt < 4; nt++) {
+                    if (!tile[nt]) continue;
+                    const f16x8 sh8 = kq == 0 ? *reinterpret_cast<const f16x8*>(&L.sm[b & 1][0][nt * 16 + lr][0]) : zero8;
+                    const f16x8 sl8 = kq == 0 ? *reinterpret_cast<const f16x8*>(&L.sm[b & 1][1][nt * 16 + lr][0]) : zero8;
+                    f32x4 zg = {0.f, 0.f, 0.f, 0.f}, zu = {0.f, 0.f, 0.f, 0.f};
+                    zg = mfma(Amg, sh8, zg);
+                    zg = mfma(Amg, sl8, zg);
+                    zu = mfma(Amu, sh8, zu);
+                    zu = mfma(Amu, sl8, zu);
+#pragma unroll
+                    for (int i = 0; i < 4; i++) {
+                        const float dg = (float)__builtin_bit_cast(_Float16, (uint16_t)(dgc[i] & 0xFFFFu));
+                        const float dmg = (float)__builtin_bit_cast(_Float16, (uint16_t)(dgc[i] >> 16)) / kSumScale;
+                        const float du = (float)__builtin_bit_cast(_Float16, (uint16_t)(duc[i] & 0xFFFFu));
+                        const float dmu = (float)__builtin_bit_cast(_Float16, (uint16_t)(duc[i] >> 16)) / kSumScale;
+                        og[nt][i] += dg * ag[nt][i] - dmg * zg[i];
+                        ou[nt][i] += du * au[nt][i] - dmu * zu[i];
+                    }
+                }
+            }
         }
-        // min term: sum_j m_j * (sum of x over sub-block j), K = the 8 sub-blocks
-        const f16x8 Amg = kq == 0 ? mg : zero8, Amu = kq == 0 ? mu : zero8;
-        f32x4 zg[4], zu[4];
-#pragma unroll
-        for (int nt = 0; nt < 4; nt++) {
-            zg[nt] = zu[nt] = (f32x4){0.f, 0.f, 0.f, 0.f};
-            if (!tile[nt]) continue;
-            const bool ld = kq == 0 && qok[nt];
-            const f16x8 sh8 = ld ? *reinterpret_cast<const f16x8*>(xsh + (size_t)qp[nt] * nsub + 8 * b) : zero8;
-            const f16x8 sl8 = ld ? *reinterpret_cast<const f16x8*>(xsl + (size_t)qp[nt] * nsub + 8 * b) : zero8;
-            zg[nt] = mfma(Amg, sh8, zg[nt]);
-            zg[nt] = mfma(Amg, sl8, zg[nt]);
-            zu[nt] = mfma(Amu, sh8, zu[nt]);
-            zu[nt] = mfma(Amu, sl8, zu[nt]);
+        if (more) {
+            *reinterpret_cast<uint4*>(&L.b[stg ^ 1][0][st_t][st_k]) = vh;
+            *reinterpret_cast<uint4*>(&L.b[stg ^ 1][1][st_t][st_k]) = vl;
+            if (next_sb) swrite_sums((c + 1) >> 2, vs);
         }
-        // apply d, dmin of the rows this lane's accumulators hold (rows r0 + 4*kq + i)
+        __syncthreads();
+        if (more && on) {
+            cur.gq = nxt.gq;
+            cur.uq = nxt.uq;
+            if (next_sb) {
+                cur.gh = nxt.gh;
+                cur.uh = nxt.uh;
+                cur.gqh = nxt.gqh;
+                cur.uqh = nxt.uqh;
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const uint8_t* gr = ent.gate + (size_t)(r0 + 4 * kq + i) * s.gate_rb + (size_t)b * BB;
-            const uint8_t* ur = ent.up + (size_t)(r0 + 4 * kq + i) * s.up_rb + (size_t)b * BB;
-            const float dg = half_at(gr), dmg = half_at(gr + 2) / kSumScale;
-            const float du = half_at(ur), dmu = half_at(ur + 2) / kSumScale;
-#pragma unroll
-            for (int nt = 0; nt < 4; nt++) {
-                og[nt][i] += dg * ag[nt][i] - dmg * zg[nt][i];
-                ou[nt][i] += du * au[nt][i] - dmu * zu[nt][i];
+                for (int i = 0; i < 4; i++) {
+                    dgc[i] = dgn[i];
+                    duc[i] = dun[i];
+                }
             }
         }
     }
+    if (!on) return;
 #pragma unroll
     for (int nt = 0; nt < 4; nt++) {
-        if (!qok[nt]) continue;
-        const float xs = xscale[qp[nt]];
+        const int q = pb + nt * 16 + lr;
+        if (q >= p1) continue;
+        const float xs = xscale[q];
 #pragma unroll
         for (int i = 0; i < 4; i++) {
-            const float g = og[nt][i] * xs, u = ou[nt][i] * xs;
-            h[(size_t)qp[nt] * s.FF + r0 + 4 * kq + i] = g / (1.0f + expf(-g)) * u;
+            const float gv = og[nt][i] * xs, uv = ou[nt][i] * xs;
+            h[(size_t)q * s.FF + r0 + 4 * kq + i] = gv / (1.0f + expf(-gv)) * uv;
         }
     }
 }
@@ -325,7 +429,7 @@ __global__ __launch_bounds__(256) void down_mfma_q6k_kernel(MoeShape s, const Ex
 // ---------------------------------------------------------------------------
 bool grouped_mfma_gate_up_ok(const MoeShape& s) {
     return (s.gate_type == kQ4_K || s.gate_type == kQ5_K) && s.up_type == s.gate_type && s.FF % 16 == 0 &&
-           s.D % 256 == 0;
+           s.D % 256 == 0 && s.gate_rb % 16 == 0 && s.up_rb % 16 == 0;
 }
 bool grouped_mfma_down_ok(const MoeShape& s) { return s.down_type == kQ6_K && s.D % 16 == 0 && s.FF % 256 == 0; }
 
@@ -338,11 +442,11 @@ hipError_t launch_prep_rows(const int* offs, int E, const int* tok, const float*
 hipError_t launch_gate_up_mfma(const MoeShape& s, const ExpertEntry* table, int E, const int* offs, int nb,
                                const _Float16* xh, const _Float16* xl, const _Float16* xsh, const _Float16* xsl,
                                const float* xscale, float* h, hipStream_t st) {
-    const dim3 g((unsigned)((s.FF + kWgRows - 1) / kWgRows), (unsigned)E, (unsigned)((nb + kPassTok - 1) / kPassTok));
+    const dim3 g((unsigned)((s.FF + kGuRows - 1) / kGuRows), (unsigned)E, (unsigned)((nb + kPassTok - 1) / kPassTok));
     if (s.gate_type == kQ4_K)
-        gate_up_mfma_kernel<kQ4_K><<<g, 256, 0, st>>>(s, table, offs, xh, xl, xsh, xsl, xscale, h);
+        gate_up_mfma_kernel<kQ4_K><<<g, 512, 0, st>>>(s, table, offs, xh, xl, xsh, xsl, xscale, h);
     else
-        gate_up_mfma_kernel<kQ5_K><<<g, 256, 0, st>>>(s, table, offs, xh, xl, xsh, xsl, xscale, h);
+        gate_up_mfma_kernel<kQ5_K><<<g, 512, 0, st>>>(s, table, offs, xh, xl, xsh, xsl, xscale, h);
     return hipGetLastError();
 }
 
