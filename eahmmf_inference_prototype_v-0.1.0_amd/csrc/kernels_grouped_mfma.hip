@@ -34,7 +34,6 @@ typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kPassTok = 64;  // tokens per pass: four 16-token tiles
-constexpr int kWgRows = 64;   // rows per workgroup: four waves x 16
 constexpr float kSumScale = 1.0f / 16.0f;  // sub-block sums (32 values) kept below 2^14
 
 struct __attribute__((packed, aligned(2))) Bytes8A2 { uint32_t x, y; };
@@ -173,9 +172,6 @@ __global__ __launch_bounds__(512) void gate_up_mfma_kernel(MoeShape s, const Exp
     const ExpertEntry ent = table[e];
     const uint8_t* ga = ent.gate + (size_t)(on ? r0 + lr : 0) * s.gate_rb;
     const uint8_t* ua = ent.up + (size_t)(on ? r0 + lr : 0) * s.up_rb;
-    bool tile[4];
-#pragma unroll
-    for (int nt = 0; nt < 4; nt++) tile[nt] = pb + nt * 16 < p1;
     // staging: thread -> (token, 8 k values) of a chunk, hi and lo
     const int st_t = tid >> 3, st_k = (tid & 7) * 8;
     const bool st_ok = pb + st_t < p1;
@@ -226,114 +222,145 @@ __global__ __launch_bounds__(512) void gate_up_mfma_kernel(MoeShape s, const Exp
         }
     };
 
-    GuA<T> cur{}, nxt{};
+    // Prefetch distance 2: chunk c computes while chunks c+1 (registers, written
+    // to LDS at the end of the iteration) and c+2 (loads in flight) arrive.
+    GuA<T> cur{}, nx1{}, nx2{};
     uint32_t dgc[4], duc[4], dgn[4] = {}, dun[4] = {};
-    uint4 vh, vl, vs;
+    uint4 vh, vl, vs, vh1, vl1, vh2 = {}, vl2 = {};
     if (on) {
         aload(0, cur);
         dload(0, dgc, duc);
+        if (nch > 1) aload(1, nx1);
     }
     gload(0, vh, vl);
     sload(0, vs);
+    if (nch > 1) gload(1, vh1, vl1);
     *reinterpret_cast<uint4*>(&L.b[0][0][st_t][st_k]) = vh;
     *reinterpret_cast<uint4*>(&L.b[0][1][st_t][st_k]) = vl;
     swrite_sums(0, vs);
     __syncthreads();
 
+    // Tokens past the group's end were staged as zeros, so every tile runs
+    // unconditionally (no branches around the matrix instructions).
     const f16x8 zero8 = {};
-    f32x4 og[4], ou[4], ag[4], au[4];
+    f32x4 og[4], ou[4];
 #pragma unroll
-    for (int nt = 0; nt < 4; nt++) og[nt] = ou[nt] = ag[nt] = au[nt] = (f32x4){0.f, 0.f, 0.f, 0.f};
-    f16x8 mg = zero8, mu = zero8;
-    for (int c = 0; c < nch; c++) {
-        const int stg = c & 1, b = c >> 2, g = c & 3;
-        const bool more = c + 1 < nch;
-        const bool next_sb = more && ((c + 1) & 3) == 0;
-        if (more) {
-            gload(c + 1, vh, vl);
-            if (next_sb) sload((c + 1) >> 2, vs);
-            if (on) {
-                aload(c + 1, nxt);
-                if (next_sb) dload((c + 1) >> 2, dgn, dun);
-            }
+    for (int nt = 0; nt < 4; nt++) og[nt] = ou[nt] = (f32x4){0.f, 0.f, 0.f, 0.f};
+    const int nsb = D / 256;
+    for (int b = 0; b < nsb; b++) {
+        f32x4 ag[4], au[4];
+#pragma unroll
+        for (int nt = 0; nt < 4; nt++) ag[nt] = au[nt] = (f32x4){0.f, 0.f, 0.f, 0.f};
+        // scales and mins of this lane's row for the 8 sub-blocks (static indices)
+        uint32_t scg[8], mng[8], scu[8], mnu[8];
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            scale_min_k4(j, cur.gh.y, cur.gh.z, cur.gh.w, scg[j], mng[j]);
+            scale_min_k4(j, cur.uh.y, cur.uh.z, cur.uh.w, scu[j], mnu[j]);
         }
-        if (on) {
-            if (g == 0) {
+        const uint2 gqh = cur.gqh, uqh = cur.uqh;
 #pragma unroll
-                for (int nt = 0; nt < 4; nt++) ag[nt] = au[nt] = (f32x4){0.f, 0.f, 0.f, 0.f};
+        for (int g = 0; g < 4; g++) {
+            const int c = 4 * b + g;
+            const int stg = c & 1;
+            const bool more = c + 1 < nch;
+            const bool next_sb = more && g == 3;
+            if (c + 2 < nch) {
+                gload(c + 2, vh2, vl2);
+                if (on) aload(c + 2, nx2);
             }
-#pragma unroll
-            for (int hh = 0; hh < 2; hh++) {
-                const int j = 2 * g + hh;
-                uint32_t scg, mng, scu, mnu;
-                scale_min_k4(j, cur.gh.y, cur.gh.z, cur.gh.w, scg, mng);
-                scale_min_k4(j, cur.uh.y, cur.uh.z, cur.uh.w, scu, mnu);
-                mg[j] = (_Float16)(float)mng;
-                mu[j] = (_Float16)(float)mnu;
-                uint2 cg = make_uint2((cur.gq.x >> (4 * hh)) & 0x0F0F0F0Fu, (cur.gq.y >> (4 * hh)) & 0x0F0F0F0Fu);
-                uint2 cu = make_uint2((cur.uq.x >> (4 * hh)) & 0x0F0F0F0Fu, (cur.uq.y >> (4 * hh)) & 0x0F0F0F0Fu);
-                if (T == kQ5_K) {
-                    cg.x |= ((cur.gqh.x >> j) & 0x01010101u) << 4;
-                    cg.y |= ((cur.gqh.y >> j) & 0x01010101u) << 4;
-                    cu.x |= ((cur.uqh.x >> j) & 0x01010101u) << 4;
-                    cu.y |= ((cur.uqh.y >> j) & 0x01010101u) << 4;
-                }
-                const f16x8 Ag = codes_times(cg, (_Float16)(float)scg, (_Float16)0.0f);
-                const f16x8 Au = codes_times(cu, (_Float16)(float)scu, (_Float16)0.0f);
-#pragma unroll
-                for (int nt = 0; nt < 4; nt++) {
-                    if (!tile[nt]) continue;
-                    const f16x8 bh = *reinterpret_cast<const f16x8*>(&L.b[stg][0][nt * 16 + lr][hh * 32 + kq * 8]);
-                    const f16x8 bl = *reinterpret_cast<const f16x8*>(&L.b[stg][1][nt * 16 + lr][hh * 32 + kq * 8]);
-                    ag[nt] = mfma(Ag, bh, ag[nt]);
-                    ag[nt] = mfma(Ag, bl, ag[nt]);
-                    au[nt] = mfma(Au, bh, au[nt]);
-                    au[nt] = mfma(Au, bl, au[nt]);
-                }
+            if (next_sb) {
+                sload(b + 1, vs);
+                if (on) dload(b + 1, dgn, dun);
             }
-            if (g == 3) {  // end of the super-block: min term, then d / dmin
-                const f16x8 Amg = kq == 0 ? mg : zero8, Amu = kq == 0 ? mu : zero8;
+            if (on) {
 #pragma unroll
-                for (int nt = 0; nt < 4; nt++) {
-                    if (!tile[nt]) continue;
-                    const f16x8 sh8 = kq == 0 ? *reinterpret_cast<const f16x8*>(&L.sm[b & 1][0][nt * 16 + lr][0]) : zero8;
-                    const f16x8 sl8 = kq == 0 ? *reinterpret_cast<const f16x8*>(&L.sm[b & 1][1][nt * 16 + lr][0]) : zero8;
-                    f32x4 zg = {0.f, 0.f, 0.f, 0.f}, zu = {0.f, 0.f, 0.f, 0.f};
-                    zg = mfma(Amg, sh8, zg);
-                    zg = mfma(Amg, sl8, zg);
-                    zu = mfma(Amu, sh8, zu);
-                    zu = mfma(Amu, sl8, zu);
+                for (int hh = 0; hh < 2; hh++) {
+                    const int j = 2 * g + hh;
+                    uint2 cg = make_uint2((cur.gq.x >> (4 * hh)) & 0x0F0F0F0Fu, (cur.gq.y >> (4 * hh)) & 0x0F0F0F0Fu);
+                    uint2 cu = make_uint2((cur.uq.x >> (4 * hh)) & 0x0F0F0F0Fu, (cur.uq.y >> (4 * hh)) & 0x0F0F0F0Fu);
+                    if (T == kQ5_K) {
+                        cg.x |= ((gqh.x >> j) & 0x01010101u) << 4;
+                        cg.y |= ((gqh.y >> j) & 0x01010101u) << 4;
+                        cu.x |= ((uqh.x >> j) & 0x01010101u) << 4;
+                        cu.y |= ((uqh.y >> j) & 0x01010101u) << 4;
+                    }
+                    const f16x8 Ag = codes_times(cg, (_Float16)(float)scg[j], (_Float16)0.0f);
+                    const f16x8 Au = codes_times(cu, (_Float16)(float)scu[j], (_Float16)0.0f);
+                    f16x8 bh[4], bl[4];
+#pragma unroll
+                    for (int nt = 0; nt < 4; nt++) {
+                        bh[nt] = *reinterpret_cast<const f16x8*>(&L.b[stg][0][nt * 16 + lr][hh * 32 + kq * 8]);
+                        bl[nt] = *reinterpret_cast<const f16x8*>(&L.b[stg][1][nt * 16 + lr][hh * 32 + kq * 8]);
+                    }
+                    // independent accumulators back to back
+#pragma unroll
+                    for (int nt = 0; nt < 4; nt++) {
+                        ag[nt] = mfma(Ag, bh[nt], ag[nt]);
+                        au[nt] = mfma(Au, bh[nt], au[nt]);
+                    }
+#pragma unroll
+                    for (int nt = 0; nt < 4; nt++) {
+                        ag[nt] = mfma(Ag, bl[nt], ag[nt]);
+                        au[nt] = mfma(Au, bl[nt], au[nt]);
+                    }
+                }
+                if (g == 3) {  // end of the super-block: min term, then d / dmin
+                    f16x8 mgv = zero8, muv = zero8;
+                    if (kq == 0) {
+#pragma unroll
+                        for (int j = 0; j < 8; j++) {
+                            mgv[j] = (_Float16)(float)mng[j];
+                            muv[j] = (_Float16)(float)mnu[j];
+                        }
+                    }
+                    f32x4 zg[4], zu[4];
+#pragma unroll
+                    for (int nt = 0; nt < 4; nt++) {
+                        const f16x8 sh8 = *reinterpret_cast<const f16x8*>(&L.sm[b & 1][0][nt * 16 + lr][0]);
+                        const f16x8 sl8 = *reinterpret_cast<const f16x8*>(&L.sm[b & 1][1][nt * 16 + lr][0]);
+                        zg[nt] = mfma(mgv, sh8, (f32x4){0.f, 0.f, 0.f, 0.f});
+                        zu[nt] = mfma(muv, sh8, (f32x4){0.f, 0.f, 0.f, 0.f});
+                        zg[nt] = mfma(mgv, sl8, zg[nt]);
+                        zu[nt] = mfma(muv, sl8, zu[nt]);
+                    }
 #pragma unroll
                     for (int i = 0; i < 4; i++) {
                         const float dg = (float)__builtin_bit_cast(_Float16, (uint16_t)(dgc[i] & 0xFFFFu));
                         const float dmg = (float)__builtin_bit_cast(_Float16, (uint16_t)(dgc[i] >> 16)) / kSumScale;
                         const float du = (float)__builtin_bit_cast(_Float16, (uint16_t)(duc[i] & 0xFFFFu));
                         const float dmu = (float)__builtin_bit_cast(_Float16, (uint16_t)(duc[i] >> 16)) / kSumScale;
-                        og[nt][i] += dg * ag[nt][i] - dmg * zg[i];
-                        ou[nt][i] += du * au[nt][i] - dmu * zu[i];
+#pragma unroll
+                        for (int nt = 0; nt < 4; nt++) {
+                            og[nt][i] += dg * ag[nt][i] - dmg * zg[nt][i];
+                            ou[nt][i] += du * au[nt][i] - dmu * zu[nt][i];
+                        }
                     }
                 }
             }
-        }
-        if (more) {
-            *reinterpret_cast<uint4*>(&L.b[stg ^ 1][0][st_t][st_k]) = vh;
-            *reinterpret_cast<uint4*>(&L.b[stg ^ 1][1][st_t][st_k]) = vl;
-            if (next_sb) swrite_sums((c + 1) >> 2, vs);
-        }
-        __syncthreads();
-        if (more && on) {
-            cur.gq = nxt.gq;
-            cur.uq = nxt.uq;
-            if (next_sb) {
-                cur.gh = nxt.gh;
-                cur.uh = nxt.uh;
-                cur.gqh = nxt.gqh;
-                cur.uqh = nxt.uqh;
+            if (more) {
+                *reinterpret_cast<uint4*>(&L.b[stg ^ 1][0][st_t][st_k]) = vh1;
+                *reinterpret_cast<uint4*>(&L.b[stg ^ 1][1][st_t][st_k]) = vl1;
+                if (next_sb) swrite_sums(b + 1, vs);
+            }
+            __syncthreads();
+            vh1 = vh2;
+            vl1 = vl2;
+            if (more && on) {
+                cur.gq = nx1.gq;
+                cur.uq = nx1.uq;
+                if (next_sb) {
+                    cur.gh = nx1.gh;
+                    cur.uh = nx1.uh;
+                    cur.gqh = nx1.gqh;
+                    cur.uqh = nx1.uqh;
 #pragma unroll
-                for (int i = 0; i < 4; i++) {
-                    dgc[i] = dgn[i];
-                    duc[i] = dun[i];
+                    for (int i = 0; i < 4; i++) {
+                        dgc[i] = dgn[i];
+                        duc[i] = dun[i];
+                    }
                 }
+                nx1 = nx2;
             }
         }
     }
@@ -352,77 +379,148 @@ __global__ __launch_bounds__(512) void gate_up_mfma_kernel(MoeShape s, const Exp
 }
 
 // ---------------------------------------------------------------------------
-// down (Q6_K) for one expert: yp[q][r] = down_r . h[q].
-__global__ __launch_bounds__(256) void down_mfma_q6k_kernel(MoeShape s, const ExpertEntry* __restrict__ table,
+// down (Q6_K) for one expert: yp[q][r] = down_r . h[q].  Same organisation
+// as gate/up: 8 waves x 16 rows, 64 tokens, h staged through LDS in chunks of
+// 64 K values (two Q6_K quarters), the next chunk prefetched into registers.
+struct DnA {          // one lane's Q6_K bytes for a chunk (quarters u0 = 2(g&1), u0 + 1 of half n = g/2)
+    uint2 ql0, ql1;   // low-nibble sources of the two quarters
+    uint2 qh;         // high bits (shared by the quarters)
+    int sc0, sc1;     // the quarters' 16-value group scales for this lane's columns
+};
+
+__global__ __launch_bounds__(512) void down_mfma_q6k_kernel(MoeShape s, const ExpertEntry* __restrict__ table,
                                                             const int* __restrict__ offs,
                                                             const _Float16* __restrict__ hh,
                                                             const _Float16* __restrict__ hl,
                                                             const float* __restrict__ hscale,
                                                             float* __restrict__ yp) {
+    __shared__ _Float16 LB[2][2][kPassTok][kBRow];  // [stage][hi, lo][token][k]
     const int e = blockIdx.y;
     const int p0 = offs[e], p1 = offs[e + 1];
     const int pb = p0 + (int)blockIdx.z * kPassTok;
     if (pb >= p1) return;
-    const int wave = threadIdx.x >> 6, l = threadIdx.x & 63;
-    const int r0 = blockIdx.x * kWgRows + wave * 16;
-    if (r0 >= s.D) return;
+    const int tid = threadIdx.x, wave = tid >> 6, l = tid & 63;
     const int lr = l & 15, kq = l >> 4;
-    const int FF = s.FF, nsb = FF / 256;
+    const int r0 = blockIdx.x * kGuRows + wave * 16;
+    const bool on = r0 < s.D;
+    const int FF = s.FF, nch = FF / kChunkK, nsb = FF / 256;
     const uint8_t* dbase = table[e].down;
-    const uint8_t* da = dbase + (size_t)(r0 + lr) * s.down_rb;
-    int qp[4];
-    bool qok[4], tile[4];
+    const uint8_t* da = dbase + (size_t)(on ? r0 + lr : 0) * s.down_rb;
+    const int st_t = tid >> 3, st_k = (tid & 7) * 8;
+    const bool st_ok = pb + st_t < p1;
+    const size_t st_row = (size_t)(pb + st_t) * FF;
+    auto gload = [&](int c, uint4& vh, uint4& vl) {
+        if (st_ok) {
+            vh = *reinterpret_cast<const uint4*>(hh + st_row + (size_t)c * kChunkK + st_k);
+            vl = *reinterpret_cast<const uint4*>(hl + st_row + (size_t)c * kChunkK + st_k);
+        } else {
+            vh = vl = make_uint4(0, 0, 0, 0);
+        }
+    };
+    auto aload = [&](int c, DnA& a) {
+        const int b = c >> 2, g = c & 3, n = g >> 1, u0 = 2 * (g & 1);
+        const uint8_t* blk = da + (size_t)b * 210;
+        a.ql0 = ld8_a2(blk + 64 * n + kq * 8);
+        a.ql1 = ld8_a2(blk + 64 * n + 32 + kq * 8);
+        a.qh = ld8_a2(blk + 128 + 32 * n + kq * 8);
+        a.sc0 = (int)(int8_t)blk[192 + 8 * n + (kq >> 1) + 2 * u0];
+        a.sc1 = (int)(int8_t)blk[192 + 8 * n + (kq >> 1) + 2 * (u0 + 1)];
+    };
+    auto dload = [&](int b, float (&d)[4]) {
 #pragma unroll
-    for (int nt = 0; nt < 4; nt++) {
-        qp[nt] = pb + nt * 16 + lr;
-        qok[nt] = qp[nt] < p1;
-        tile[nt] = pb + nt * 16 < p1;
+        for (int i = 0; i < 4; i++)
+            d[i] = half_at(dbase + (size_t)(on ? r0 + 4 * kq + i : 0) * s.down_rb + (size_t)b * 210 + 208);
+    };
+    DnA cur{}, nx1{}, nx2{};
+    float dc[4] = {}, dn[4] = {};
+    uint4 vh, vl, vh1, vl1, vh2 = {}, vl2 = {};
+    if (on) {
+        aload(0, cur);
+        dload(0, dc);
+        if (nch > 1) aload(1, nx1);
     }
-    const f16x8 zero8 = {};
+    gload(0, vh, vl);
+    if (nch > 1) gload(1, vh1, vl1);
+    *reinterpret_cast<uint4*>(&LB[0][0][st_t][st_k]) = vh;
+    *reinterpret_cast<uint4*>(&LB[0][1][st_t][st_k]) = vl;
+    __syncthreads();
     f32x4 out[4];
 #pragma unroll
     for (int nt = 0; nt < 4; nt++) out[nt] = (f32x4){0.f, 0.f, 0.f, 0.f};
     for (int b = 0; b < nsb; b++) {
-        const uint8_t* blk = da + (size_t)b * 210;
         f32x4 acc[4];
 #pragma unroll
         for (int nt = 0; nt < 4; nt++) acc[nt] = (f32x4){0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int c = 0; c < 8; c++) {  // 32-value chunk = quarter u of half n
-            const int n = c >> 2, u = c & 3;
-            const uint2 ql = ld8_a2(blk + 64 * n + 32 * (u & 1) + kq * 8);
-            const uint2 qh = ld8_a2(blk + 128 + 32 * n + kq * 8);
-            const int sc = (int)(int8_t)blk[192 + 8 * n + (kq >> 1) + 2 * u];
-            const int sh4 = u >= 2 ? 4 : 0;
-            const uint2 code = make_uint2(((ql.x >> sh4) & 0x0F0F0F0Fu) | (((qh.x >> (2 * u)) & 0x03030303u) << 4),
-                                          ((ql.y >> sh4) & 0x0F0F0F0Fu) | (((qh.y >> (2 * u)) & 0x03030303u) << 4));
-            const f16x8 A1 = codes_times(code, (_Float16)(float)(16 * (sc >> 4)), (_Float16)-32.0f);
-            const f16x8 A2 = codes_times(code, (_Float16)(float)(sc & 15), (_Float16)-32.0f);
-            const int kk = b * 256 + 32 * c + kq * 8;
+        for (int g = 0; g < 4; g++) {
+            const int c = 4 * b + g;
+            const int stg = c & 1;
+            const bool more = c + 1 < nch;
+            const bool next_sb = more && g == 3;
+            if (c + 2 < nch) {
+                gload(c + 2, vh2, vl2);
+                if (on) aload(c + 2, nx2);
+            }
+            if (next_sb && on) dload(b + 1, dn);
+            if (on) {
 #pragma unroll
-            for (int nt = 0; nt < 4; nt++) {
-                if (!tile[nt]) continue;
-                const f16x8 bh = qok[nt] ? *reinterpret_cast<const f16x8*>(hh + (size_t)qp[nt] * FF + kk) : zero8;
-                const f16x8 bl = qok[nt] ? *reinterpret_cast<const f16x8*>(hl + (size_t)qp[nt] * FF + kk) : zero8;
-                acc[nt] = mfma(A1, bh, acc[nt]);
-                acc[nt] = mfma(A1, bl, acc[nt]);
-                acc[nt] = mfma(A2, bh, acc[nt]);
-                acc[nt] = mfma(A2, bl, acc[nt]);
+                for (int qq = 0; qq < 2; qq++) {  // the chunk's two quarters
+                    const int u = 2 * (g & 1) + qq;
+                    const uint2 ql = qq ? cur.ql1 : cur.ql0;
+                    const int sc = qq ? cur.sc1 : cur.sc0;
+                    const int sh4 = u >= 2 ? 4 : 0;
+                    const uint2 code =
+                        make_uint2(((ql.x >> sh4) & 0x0F0F0F0Fu) | (((cur.qh.x >> (2 * u)) & 0x03030303u) << 4),
+                                   ((ql.y >> sh4) & 0x0F0F0F0Fu) | (((cur.qh.y >> (2 * u)) & 0x03030303u) << 4));
+                    const f16x8 A1 = codes_times(code, (_Float16)(float)(16 * (sc >> 4)), (_Float16)-32.0f);
+                    const f16x8 A2 = codes_times(code, (_Float16)(float)(sc & 15), (_Float16)-32.0f);
+                    f16x8 bh[4], bl[4];
+#pragma unroll
+                    for (int nt = 0; nt < 4; nt++) {
+                        bh[nt] = *reinterpret_cast<const f16x8*>(&LB[stg][0][nt * 16 + lr][qq * 32 + kq * 8]);
+                        bl[nt] = *reinterpret_cast<const f16x8*>(&LB[stg][1][nt * 16 + lr][qq * 32 + kq * 8]);
+                    }
+#pragma unroll
+                    for (int nt = 0; nt < 4; nt++) acc[nt] = mfma(A1, bh[nt], acc[nt]);
+#pragma unroll
+                    for (int nt = 0; nt < 4; nt++) acc[nt] = mfma(A2, bh[nt], acc[nt]);
+#pragma unroll
+                    for (int nt = 0; nt < 4; nt++) acc[nt] = mfma(A1, bl[nt], acc[nt]);
+#pragma unroll
+                    for (int nt = 0; nt < 4; nt++) acc[nt] = mfma(A2, bl[nt], acc[nt]);
+                }
+                if (g == 3) {
+#pragma unroll
+                    for (int i = 0; i < 4; i++)
+#pragma unroll
+                        for (int nt = 0; nt < 4; nt++) out[nt][i] += dc[i] * acc[nt][i];
+                }
+            }
+            if (more) {
+                *reinterpret_cast<uint4*>(&LB[stg ^ 1][0][st_t][st_k]) = vh1;
+                *reinterpret_cast<uint4*>(&LB[stg ^ 1][1][st_t][st_k]) = vl1;
+            }
+            __syncthreads();
+            vh1 = vh2;
+            vl1 = vl2;
+            if (more && on) {
+                cur = nx1;
+                nx1 = nx2;
+                if (next_sb) {
+#pragma unroll
+                    for (int i = 0; i < 4; i++) dc[i] = dn[i];
+                }
             }
         }
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const float d = half_at(dbase + (size_t)(r0 + 4 * kq + i) * s.down_rb + (size_t)b * 210 + 208);
-#pragma unroll
-            for (int nt = 0; nt < 4; nt++) out[nt][i] += d * acc[nt][i];
-        }
     }
+    if (!on) return;
 #pragma unroll
     for (int nt = 0; nt < 4; nt++) {
-        if (!qok[nt]) continue;
-        const float hs = hscale[qp[nt]];
+        const int q = pb + nt * 16 + lr;
+        if (q >= p1) continue;
+        const float hs = hscale[q];
 #pragma unroll
-        for (int i = 0; i < 4; i++) yp[(size_t)qp[nt] * s.D + r0 + 4 * kq + i] = out[nt][i] * hs;
+        for (int i = 0; i < 4; i++) yp[(size_t)q * s.D + r0 + 4 * kq + i] = out[nt][i] * hs;
     }
 }
 
@@ -452,8 +550,8 @@ hipError_t launch_gate_up_mfma(const MoeShape& s, const ExpertEntry* table, int 
 
 hipError_t launch_down_mfma(const MoeShape& s, const ExpertEntry* table, int E, const int* offs, int nb,
                             const _Float16* hh, const _Float16* hl, const float* hscale, float* yp, hipStream_t st) {
-    const dim3 g((unsigned)((s.D + kWgRows - 1) / kWgRows), (unsigned)E, (unsigned)((nb + kPassTok - 1) / kPassTok));
-    down_mfma_q6k_kernel<<<g, 256, 0, st>>>(s, table, offs, hh, hl, hscale, yp);
+    const dim3 g((unsigned)((s.D + kGuRows - 1) / kGuRows), (unsigned)E, (unsigned)((nb + kPassTok - 1) / kPassTok));
+    down_mfma_q6k_kernel<<<g, 512, 0, st>>>(s, table, offs, hh, hl, hscale, yp);
     return hipGetLastError();
 }
 
