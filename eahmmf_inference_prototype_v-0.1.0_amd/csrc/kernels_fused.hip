@@ -141,14 +141,6 @@ __device__ __forceinline__ unsigned bump_counter(unsigned* p) {
 __device__ __forceinline__ void reset_counter(unsigned* p) {
     __hip_atomic_store(p, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
-// s_waitcnt vmcnt(0): this wave's memory operations have completed (gfx9
-// encoding: vmcnt 0, expcnt 7, lgkmcnt 15).  Compiler fences keep the
-// stores before it.
-__device__ __forceinline__ void wait_vm() {
-    __atomic_signal_fence(__ATOMIC_SEQ_CST);
-    __builtin_amdgcn_s_waitcnt(0x0F70);
-    __atomic_signal_fence(__ATOMIC_SEQ_CST);
-}
 
 // Current value of a counter read with an atomic read-modify-write: it is
 // served where the increments are performed, never from a stale cached copy.

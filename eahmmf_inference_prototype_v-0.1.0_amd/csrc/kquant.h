@@ -173,6 +173,15 @@ __device__ __forceinline__ void decode_row_seg(const uint8_t* row, int s, float*
 }
 
 // Wave-wide float sum (wave64); every lane receives the total.
+// s_waitcnt vmcnt(0): this wave's memory operations have completed (gfx9
+// encoding: vmcnt 0, expcnt 7, lgkmcnt 15).  Compiler fences keep the
+// stores before it.
+__device__ __forceinline__ void wait_vm() {
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __builtin_amdgcn_s_waitcnt(0x0F70);
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
