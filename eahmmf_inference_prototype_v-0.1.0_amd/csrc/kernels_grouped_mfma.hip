@@ -60,6 +60,20 @@ __device__ __forceinline__ f16x8 codes_times(uint2 c, _Float16 f, _Float16 bias)
     return (f16x8){a.x, a.y, b.x, b.y, d.x, d.y, e.x, e.y};
 }
 
+// Workgroup barrier for LDS hand-offs only.  __syncthreads() carries a
+// workgroup release fence, which on this target waits for every outstanding
+// vector-memory operation, loads included (s_waitcnt vmcnt(0)), and so would
+// stall on the next chunk's prefetch at every barrier.  This one waits for
+// this wave's LDS operations (lgkmcnt 0; vmcnt and expcnt left at their
+// maxima), then meets the other waves; global data is consumed only through
+// its own registers, so no global ordering is needed here.
+__device__ __forceinline__ void lds_barrier() {
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __builtin_amdgcn_s_waitcnt(0xC07F);
+    __builtin_amdgcn_s_barrier();
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+
 __device__ __forceinline__ f32x4 mfma(f16x8 a, f16x8 b, f32x4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
 }
@@ -125,27 +139,35 @@ __global__ __launch_bounds__(256) void prep_rows_kernel(const int* __restrict__ 
 // ---------------------------------------------------------------------------
 // gate/up (Q4_K or Q5_K, same type) for one expert: h[q][r] = silu(g) * u.
 //
-// A workgroup of 8 waves covers 128 rows (16 per wave) and 64 tokens.  The
-// tokens' fp16 hi/lo activations are staged through LDS in chunks of 64 K
-// values (double-buffered, shared by the 8 waves); the next chunk's
-// activations and weight bytes are loaded into registers while the current
-// chunk runs on the matrix cores.  The sub-block sums of the min term are
-// staged once per super-block.
+// Weights stationary: a workgroup of 8 waves covers 64 rows (4 row tiles of
+// 16) and 128 of the expert's tokens, one 16-token tile per wave.  For every
+// 32-value sub-block all 512 threads decode the 64 rows' exact-integer fp16
+// A fragments (gate and up) into LDS, double-buffered, so each fragment is
+// built once per workgroup and read by every wave; each wave then runs 4 row
+// tiles x (gate, up) x (hi, lo) MFMAs against its own token tile, whose
+// activations stream from global memory one sub-block ahead.  Per
+// super-block the rows' mins (as A fragments of the min-term MFMA) and their
+// (d, dmin) are staged the same way.  The weight bytes a thread decodes are
+// loaded one super-block ahead.
 constexpr int kGuWaves = 8;
-constexpr int kGuRows = 16 * kGuWaves;
-constexpr int kChunkK = 64;
-constexpr int kBRow = kChunkK + 8;  // halfs per token row in LDS: 144 B, so 16 lanes' 16-B reads hit distinct banks
+constexpr int kGuRowTiles = 4;
+constexpr int kGuRows = 16 * kGuRowTiles;  // 64
+constexpr int kGuFrags = 2 * kGuRowTiles * 64 / 512;  // A fragments each thread decodes per sub-block
+constexpr int kGuTok = 16 * kGuWaves;      // 128 tokens per workgroup pass
+constexpr int kChunkK = 64;                // the down kernel's LDS chunk
+constexpr int kBRow = kChunkK + 8;         // halfs per token row in the down kernel's LDS: 144 B
 
 struct GuLds {
-    _Float16 b[2][2][kPassTok][kBRow];  // [stage][hi, lo][token][k]
-    _Float16 sm[2][2][kPassTok][8];     // [super-block parity][hi, lo][token][sub-block]: scaled sums
+    uint4 a[2][2][kGuRowTiles][64];     // [sub-block parity][gate, up][row tile][lane]: A fragments
+    uint4 amin[2][2][kGuRowTiles][64];  // [super-block parity][gate, up][row tile][lane]: min-term A
+    uint32_t dd[2][2][kGuRows];         // [super-block parity][gate, up][row]: d | dmin << 16
 };
 
 template <int T>
-struct GuA {  // one lane's weight bytes for a chunk (gate and up)
-    uint4 gh, uh;    // super-block headers (d, dmin, scales)
-    uint2 gqh, uqh;  // Q5_K high bits of the lane's 8 columns
-    uint2 gq, uq;    // 4-bit codes of the lane's 8 columns, both nibbles (sub-blocks 2g, 2g+1)
+struct GuRowSb {  // the weight bytes one thread decodes for a super-block (one row of one matrix)
+    uint4 hdr;     // d, dmin, scales
+    uint2 qh;      // Q5_K high bits of the thread's 8 columns
+    uint2 q[4];    // 4-bit codes of the thread's columns for g = 0..3 (both nibbles)
 };
 
 template <int T>
@@ -162,218 +184,170 @@ __global__ __launch_bounds__(512) void gate_up_mfma_kernel(MoeShape s, const Exp
     __shared__ GuLds L;
     const int e = blockIdx.y;
     const int p0 = offs[e], p1 = offs[e + 1];
-    const int pb = p0 + (int)blockIdx.z * kPassTok;
+    const int pb = p0 + (int)blockIdx.z * kGuTok;
     if (pb >= p1) return;  // whole workgroup
     const int tid = threadIdx.x, wave = tid >> 6, l = tid & 63;
     const int lr = l & 15, kq = l >> 4;
-    const int r0 = blockIdx.x * kGuRows + wave * 16;
-    const bool on = r0 < s.FF;  // wave-uniform; idle waves still stage and synchronise
-    const int D = s.D, nsub = D / 32, nch = D / kChunkK;
+    const int rw = blockIdx.x * kGuRows;
+    const int D = s.D, nsub = D / 32, nsb = D / 256;
     const ExpertEntry ent = table[e];
-    const uint8_t* ga = ent.gate + (size_t)(on ? r0 + lr : 0) * s.gate_rb;
-    const uint8_t* ua = ent.up + (size_t)(on ? r0 + lr : 0) * s.up_rb;
-    // staging: thread -> (token, 8 k values) of a chunk, hi and lo
-    const int st_t = tid >> 3, st_k = (tid & 7) * 8;
-    const bool st_ok = pb + st_t < p1;
-    const size_t st_row = (size_t)(pb + st_t) * D;
-    auto gload = [&](int c, uint4& vh, uint4& vl) {
-        if (st_ok) {
-            vh = *reinterpret_cast<const uint4*>(xh + st_row + (size_t)c * kChunkK + st_k);
-            vl = *reinterpret_cast<const uint4*>(xl + st_row + (size_t)c * kChunkK + st_k);
-        } else {
-            vh = vl = make_uint4(0, 0, 0, 0);
+    // this wave's tokens; a wave whose tile starts past the group only decodes
+    const int q = pb + wave * 16 + lr;
+    const bool qok = q < p1;
+    const bool busy = pb + wave * 16 < p1;  // wave-uniform
+    const int qc = qok ? q : p1 - 1;        // a valid row for the activation loads
+    // decode assignment: thread -> (matrix, row tile, lane) fragment(s), fixed for the whole K loop
+    int dm[kGuFrags], drt[kGuFrags], dll[kGuFrags], drow[kGuFrags];
+    bool dok[kGuFrags];
+    const uint8_t* drp[kGuFrags];
+#pragma unroll
+    for (int i = 0; i < kGuFrags; i++) {
+        const int f = tid + 512 * i;
+        dm[i] = f / (kGuRowTiles * 64);
+        drt[i] = (f >> 6) % kGuRowTiles;
+        dll[i] = f & 63;
+        drow[i] = rw + drt[i] * 16 + (dll[i] & 15);
+        dok[i] = drow[i] < s.FF;
+        drp[i] = (dm[i] ? ent.up : ent.gate) + (size_t)(dok[i] ? drow[i] : 0) * (dm[i] ? s.up_rb : s.gate_rb);
+    }
+    auto rload = [&](int b, int i, GuRowSb<T>& r) {
+        const uint8_t* sb = drp[i] + (size_t)b * BB;
+        const int dkq = dll[i] >> 4;
+        r.hdr = *reinterpret_cast<const uint4*>(sb);
+        if (T == kQ5_K) r.qh = ld8(sb + 16 + dkq * 8);
+#pragma unroll
+        for (int g = 0; g < 4; g++) r.q[g] = ld8(sb + QS + 32 * g + dkq * 8);
+    };
+    // the fragment of sub-block j for fragment slot i, written to parity buffer par
+    auto decode = [&](int j, int i, const GuRowSb<T>& r, int par) {
+        uint32_t sc, mn;
+        scale_min_k4(j, r.hdr.y, r.hdr.z, r.hdr.w, sc, mn);
+        const int g = j >> 1, hh = j & 1;
+        uint2 c = make_uint2((r.q[g].x >> (4 * hh)) & 0x0F0F0F0Fu, (r.q[g].y >> (4 * hh)) & 0x0F0F0F0Fu);
+        if (T == kQ5_K) {
+            c.x |= ((r.qh.x >> j) & 0x01010101u) << 4;
+            c.y |= ((r.qh.y >> j) & 0x01010101u) << 4;
         }
+        const f16x8 A = codes_times(c, (_Float16)(float)sc, (_Float16)0.0f);
+        L.a[par][dm[i]][drt[i]][dll[i]] = __builtin_bit_cast(uint4, A);
     };
-    // sums of a super-block: threads 0..127 stage one 16-B piece each
-    auto sload = [&](int b, uint4& v) {
-        v = make_uint4(0, 0, 0, 0);
-        if (tid < 2 * kPassTok) {
-            const int t = tid & (kPassTok - 1);
-            if (pb + t < p1)
-                v = *reinterpret_cast<const uint4*>((tid < kPassTok ? xsh : xsl) + (size_t)(pb + t) * nsub + 8 * b);
-        }
-    };
-    auto swrite_sums = [&](int b, uint4 v) {
-        if (tid < 2 * kPassTok)
-            *reinterpret_cast<uint4*>(&L.sm[b & 1][tid >= kPassTok][tid & (kPassTok - 1)][0]) = v;
-    };
-    auto aload = [&](int c, GuA<T>& a) {
-        const int b = c >> 2, g = c & 3;
-        const uint8_t* gb = ga + (size_t)b * BB;
-        const uint8_t* ub = ua + (size_t)b * BB;
-        if (g == 0) {
-            a.gh = *reinterpret_cast<const uint4*>(gb);
-            a.uh = *reinterpret_cast<const uint4*>(ub);
-            if (T == kQ5_K) {
-                a.gqh = ld8(gb + 16 + kq * 8);
-                a.uqh = ld8(ub + 16 + kq * 8);
+    // per super-block: min-term fragments (m_0..m_7 on lanes with kq == 0) and (d, dmin)
+    auto sbstage = [&](int b, int i, const GuRowSb<T>& r) {
+        f16x8 mv = {};
+        if ((dll[i] >> 4) == 0) {
+#pragma unroll
+            for (int j = 0; j < 8; j++) {
+                uint32_t sc, mn;
+                scale_min_k4(j, r.hdr.y, r.hdr.z, r.hdr.w, sc, mn);
+                mv[j] = (_Float16)(float)mn;
             }
         }
-        a.gq = ld8(gb + QS + 32 * g + kq * 8);
-        a.uq = ld8(ub + QS + 32 * g + kq * 8);
-    };
-    // (d, dmin) of the rows this lane's accumulators hold, for super-block b
-    auto dload = [&](int b, uint32_t (&dg)[4], uint32_t (&du)[4]) {
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const size_t row = (size_t)(on ? r0 + 4 * kq + i : 0);
-            dg[i] = *reinterpret_cast<const uint32_t*>(ent.gate + row * s.gate_rb + (size_t)b * BB);
-            du[i] = *reinterpret_cast<const uint32_t*>(ent.up + row * s.up_rb + (size_t)b * BB);
-        }
+        L.amin[b & 1][dm[i]][drt[i]][dll[i]] = __builtin_bit_cast(uint4, mv);
+        if ((dll[i] >> 4) == 0) L.dd[b & 1][dm[i]][drt[i] * 16 + (dll[i] & 15)] = r.hdr.x;
     };
 
-    // Prefetch distance 2: chunk c computes while chunks c+1 (registers, written
-    // to LDS at the end of the iteration) and c+2 (loads in flight) arrive.
-    GuA<T> cur{}, nx1{}, nx2{};
-    uint32_t dgc[4], duc[4], dgn[4] = {}, dun[4] = {};
-    uint4 vh, vl, vs, vh1, vl1, vh2 = {}, vl2 = {};
-    if (on) {
-        aload(0, cur);
-        dload(0, dgc, duc);
-        if (nch > 1) aload(1, nx1);
+    GuRowSb<T> rc[kGuFrags], rn[kGuFrags];
+#pragma unroll
+    for (int i = 0; i < kGuFrags; i++) {
+        rload(0, i, rc[i]);
+        sbstage(0, i, rc[i]);
+        decode(0, i, rc[i], 0);
     }
-    gload(0, vh, vl);
-    sload(0, vs);
-    if (nch > 1) gload(1, vh1, vl1);
-    *reinterpret_cast<uint4*>(&L.b[0][0][st_t][st_k]) = vh;
-    *reinterpret_cast<uint4*>(&L.b[0][1][st_t][st_k]) = vl;
-    swrite_sums(0, vs);
-    __syncthreads();
+    // activations of the wave's token tile, one sub-block ahead
+    auto xload = [&](int kk, f16x8& bh, f16x8& bl) {
+        bh = *reinterpret_cast<const f16x8*>(xh + (size_t)qc * D + kk + kq * 8);
+        bl = *reinterpret_cast<const f16x8*>(xl + (size_t)qc * D + kk + kq * 8);
+    };
+    f16x8 bh, bl, nbh, nbl;
+    xload(0, bh, bl);
+    lds_barrier();
 
-    // Tokens past the group's end were staged as zeros, so every tile runs
-    // unconditionally (no branches around the matrix instructions).
-    const f16x8 zero8 = {};
-    f32x4 og[4], ou[4];
+    f32x4 og[kGuRowTiles], ou[kGuRowTiles], ag[kGuRowTiles], au[kGuRowTiles];
 #pragma unroll
-    for (int nt = 0; nt < 4; nt++) og[nt] = ou[nt] = (f32x4){0.f, 0.f, 0.f, 0.f};
-    const int nsb = D / 256;
+    for (int rt = 0; rt < kGuRowTiles; rt++) og[rt] = ou[rt] = ag[rt] = au[rt] = (f32x4){0.f, 0.f, 0.f, 0.f};
+    // super-blocks run-time, their 8 sub-blocks unrolled (every register-array
+    // index below is a compile-time constant)
     for (int b = 0; b < nsb; b++) {
-        f32x4 ag[4], au[4];
+        const bool more_sb = b + 1 < nsb;
+        if (more_sb) {  // next super-block's weight bytes, a super-block ahead
 #pragma unroll
-        for (int nt = 0; nt < 4; nt++) ag[nt] = au[nt] = (f32x4){0.f, 0.f, 0.f, 0.f};
-        // scales and mins of this lane's row for the 8 sub-blocks (static indices)
-        uint32_t scg[8], mng[8], scu[8], mnu[8];
+            for (int i = 0; i < kGuFrags; i++) rload(b + 1, i, rn[i]);
+        }
 #pragma unroll
         for (int j = 0; j < 8; j++) {
-            scale_min_k4(j, cur.gh.y, cur.gh.z, cur.gh.w, scg[j], mng[j]);
-            scale_min_k4(j, cur.uh.y, cur.uh.z, cur.uh.w, scu[j], mnu[j]);
-        }
-        const uint2 gqh = cur.gqh, uqh = cur.uqh;
+            const int jj = 8 * b + j, par = j & 1;
+            const bool more = j < 7 || more_sb;
+            if (more) xload((jj + 1) * 32, nbh, nbl);
+            if (busy) {
 #pragma unroll
-        for (int g = 0; g < 4; g++) {
-            const int c = 4 * b + g;
-            const int stg = c & 1;
-            const bool more = c + 1 < nch;
-            const bool next_sb = more && g == 3;
-            if (c + 2 < nch) {
-                gload(c + 2, vh2, vl2);
-                if (on) aload(c + 2, nx2);
-            }
-            if (next_sb) {
-                sload(b + 1, vs);
-                if (on) dload(b + 1, dgn, dun);
-            }
-            if (on) {
-#pragma unroll
-                for (int hh = 0; hh < 2; hh++) {
-                    const int j = 2 * g + hh;
-                    uint2 cg = make_uint2((cur.gq.x >> (4 * hh)) & 0x0F0F0F0Fu, (cur.gq.y >> (4 * hh)) & 0x0F0F0F0Fu);
-                    uint2 cu = make_uint2((cur.uq.x >> (4 * hh)) & 0x0F0F0F0Fu, (cur.uq.y >> (4 * hh)) & 0x0F0F0F0Fu);
-                    if (T == kQ5_K) {
-                        cg.x |= ((gqh.x >> j) & 0x01010101u) << 4;
-                        cg.y |= ((gqh.y >> j) & 0x01010101u) << 4;
-                        cu.x |= ((uqh.x >> j) & 0x01010101u) << 4;
-                        cu.y |= ((uqh.y >> j) & 0x01010101u) << 4;
-                    }
-                    const f16x8 Ag = codes_times(cg, (_Float16)(float)scg[j], (_Float16)0.0f);
-                    const f16x8 Au = codes_times(cu, (_Float16)(float)scu[j], (_Float16)0.0f);
-                    f16x8 bh[4], bl[4];
-#pragma unroll
-                    for (int nt = 0; nt < 4; nt++) {
-                        bh[nt] = *reinterpret_cast<const f16x8*>(&L.b[stg][0][nt * 16 + lr][hh * 32 + kq * 8]);
-                        bl[nt] = *reinterpret_cast<const f16x8*>(&L.b[stg][1][nt * 16 + lr][hh * 32 + kq * 8]);
-                    }
-                    // independent accumulators back to back
-#pragma unroll
-                    for (int nt = 0; nt < 4; nt++) {
-                        ag[nt] = mfma(Ag, bh[nt], ag[nt]);
-                        au[nt] = mfma(Au, bh[nt], au[nt]);
-                    }
-#pragma unroll
-                    for (int nt = 0; nt < 4; nt++) {
-                        ag[nt] = mfma(Ag, bl[nt], ag[nt]);
-                        au[nt] = mfma(Au, bl[nt], au[nt]);
-                    }
+                for (int rt = 0; rt < kGuRowTiles; rt++) {
+                    const f16x8 Ag = __builtin_bit_cast(f16x8, L.a[par][0][rt][l]);
+                    const f16x8 Au = __builtin_bit_cast(f16x8, L.a[par][1][rt][l]);
+                    ag[rt] = mfma(Ag, bh, ag[rt]);
+                    au[rt] = mfma(Au, bh, au[rt]);
                 }
-                if (g == 3) {  // end of the super-block: min term, then d / dmin
-                    f16x8 mgv = zero8, muv = zero8;
-                    if (kq == 0) {
 #pragma unroll
-                        for (int j = 0; j < 8; j++) {
-                            mgv[j] = (_Float16)(float)mng[j];
-                            muv[j] = (_Float16)(float)mnu[j];
+                for (int rt = 0; rt < kGuRowTiles; rt++) {
+                    const f16x8 Ag = __builtin_bit_cast(f16x8, L.a[par][0][rt][l]);
+                    const f16x8 Au = __builtin_bit_cast(f16x8, L.a[par][1][rt][l]);
+                    ag[rt] = mfma(Ag, bl, ag[rt]);
+                    au[rt] = mfma(Au, bl, au[rt]);
+                }
+                if (j == 7) {  // end of the super-block: min term, then d / dmin
+                    const f16x8 zero8 = {};
+                    const f16x8 sh8 = kq == 0 && qok ? *reinterpret_cast<const f16x8*>(xsh + (size_t)q * nsub + 8 * b) : zero8;
+                    const f16x8 sl8 = kq == 0 && qok ? *reinterpret_cast<const f16x8*>(xsl + (size_t)q * nsub + 8 * b) : zero8;
+#pragma unroll
+                    for (int rt = 0; rt < kGuRowTiles; rt++) {
+                        const f16x8 Mg = __builtin_bit_cast(f16x8, L.amin[b & 1][0][rt][l]);
+                        const f16x8 Mu = __builtin_bit_cast(f16x8, L.amin[b & 1][1][rt][l]);
+                        f32x4 zg = mfma(Mg, sh8, (f32x4){0.f, 0.f, 0.f, 0.f});
+                        f32x4 zu = mfma(Mu, sh8, (f32x4){0.f, 0.f, 0.f, 0.f});
+                        zg = mfma(Mg, sl8, zg);
+                        zu = mfma(Mu, sl8, zu);
+                        const uint4 dg4 = *reinterpret_cast<const uint4*>(&L.dd[b & 1][0][rt * 16 + 4 * kq]);
+                        const uint4 du4 = *reinterpret_cast<const uint4*>(&L.dd[b & 1][1][rt * 16 + 4 * kq]);
+                        const uint32_t dgv[4] = {dg4.x, dg4.y, dg4.z, dg4.w}, duv[4] = {du4.x, du4.y, du4.z, du4.w};
+#pragma unroll
+                        for (int i = 0; i < 4; i++) {
+                            const float dg = (float)__builtin_bit_cast(_Float16, (uint16_t)(dgv[i] & 0xFFFFu));
+                            const float dmg = (float)__builtin_bit_cast(_Float16, (uint16_t)(dgv[i] >> 16)) / kSumScale;
+                            const float du = (float)__builtin_bit_cast(_Float16, (uint16_t)(duv[i] & 0xFFFFu));
+                            const float dmu = (float)__builtin_bit_cast(_Float16, (uint16_t)(duv[i] >> 16)) / kSumScale;
+                            og[rt][i] += dg * ag[rt][i] - dmg * zg[i];
+                            ou[rt][i] += du * au[rt][i] - dmu * zu[i];
                         }
-                    }
-                    f32x4 zg[4], zu[4];
-#pragma unroll
-                    for (int nt = 0; nt < 4; nt++) {
-                        const f16x8 sh8 = *reinterpret_cast<const f16x8*>(&L.sm[b & 1][0][nt * 16 + lr][0]);
-                        const f16x8 sl8 = *reinterpret_cast<const f16x8*>(&L.sm[b & 1][1][nt * 16 + lr][0]);
-                        zg[nt] = mfma(mgv, sh8, (f32x4){0.f, 0.f, 0.f, 0.f});
-                        zu[nt] = mfma(muv, sh8, (f32x4){0.f, 0.f, 0.f, 0.f});
-                        zg[nt] = mfma(mgv, sl8, zg[nt]);
-                        zu[nt] = mfma(muv, sl8, zu[nt]);
-                    }
-#pragma unroll
-                    for (int i = 0; i < 4; i++) {
-                        const float dg = (float)__builtin_bit_cast(_Float16, (uint16_t)(dgc[i] & 0xFFFFu));
-                        const float dmg = (float)__builtin_bit_cast(_Float16, (uint16_t)(dgc[i] >> 16)) / kSumScale;
-                        const float du = (float)__builtin_bit_cast(_Float16, (uint16_t)(duc[i] & 0xFFFFu));
-                        const float dmu = (float)__builtin_bit_cast(_Float16, (uint16_t)(duc[i] >> 16)) / kSumScale;
-#pragma unroll
-                        for (int nt = 0; nt < 4; nt++) {
-                            og[nt][i] += dg * ag[nt][i] - dmg * zg[nt][i];
-                            ou[nt][i] += du * au[nt][i] - dmu * zu[nt][i];
-                        }
+                        ag[rt] = au[rt] = (f32x4){0.f, 0.f, 0.f, 0.f};
                     }
                 }
             }
-            if (more) {
-                *reinterpret_cast<uint4*>(&L.b[stg ^ 1][0][st_t][st_k]) = vh1;
-                *reinterpret_cast<uint4*>(&L.b[stg ^ 1][1][st_t][st_k]) = vl1;
-                if (next_sb) swrite_sums(b + 1, vs);
-            }
-            __syncthreads();
-            vh1 = vh2;
-            vl1 = vl2;
-            if (more && on) {
-                cur.gq = nx1.gq;
-                cur.uq = nx1.uq;
-                if (next_sb) {
-                    cur.gh = nx1.gh;
-                    cur.uh = nx1.uh;
-                    cur.gqh = nx1.gqh;
-                    cur.uqh = nx1.uqh;
+            // decode the next sub-block (the next super-block's first one from the prefetched bytes)
+            if (j < 7) {
 #pragma unroll
-                    for (int i = 0; i < 4; i++) {
-                        dgc[i] = dgn[i];
-                        duc[i] = dun[i];
-                    }
+                for (int i = 0; i < kGuFrags; i++) decode(j + 1, i, rc[i], par ^ 1);
+            } else if (more_sb) {
+#pragma unroll
+                for (int i = 0; i < kGuFrags; i++) {
+                    rc[i] = rn[i];
+                    sbstage(b + 1, i, rc[i]);
+                    decode(0, i, rc[i], par ^ 1);
                 }
-                nx1 = nx2;
             }
+            lds_barrier();
+            bh = nbh;
+            bl = nbl;
         }
     }
-    if (!on) return;
+    if (!qok) return;
+    const float xs = xscale[q];
 #pragma unroll
-    for (int nt = 0; nt < 4; nt++) {
-        const int q = pb + nt * 16 + lr;
-        if (q >= p1) continue;
-        const float xs = xscale[q];
+    for (int rt = 0; rt < kGuRowTiles; rt++) {
 #pragma unroll
         for (int i = 0; i < 4; i++) {
-            const float gv = og[nt][i] * xs, uv = ou[nt][i] * xs;
-            h[(size_t)q * s.FF + r0 + 4 * kq + i] = gv / (1.0f + expf(-gv)) * uv;
+            const int r = rw + rt * 16 + 4 * kq + i;
+            if (r >= s.FF) continue;
+            const float gv = og[rt][i] * xs, uv = ou[rt][i] * xs;
+            h[(size_t)q * s.FF + r] = gv / (1.0f + expf(-gv)) * uv;
         }
     }
 }
@@ -382,6 +356,8 @@ __global__ __launch_bounds__(512) void gate_up_mfma_kernel(MoeShape s, const Exp
 // down (Q6_K) for one expert: yp[q][r] = down_r . h[q].  Same organisation
 // as gate/up: 8 waves x 16 rows, 64 tokens, h staged through LDS in chunks of
 // 64 K values (two Q6_K quarters), the next chunk prefetched into registers.
+constexpr int kDnRows = 128;  // down: 8 waves x 16 rows
+
 struct DnA {          // one lane's Q6_K bytes for a chunk (quarters u0 = 2(g&1), u0 + 1 of half n = g/2)
     uint2 ql0, ql1;   // low-nibble sources of the two quarters
     uint2 qh;         // high bits (shared by the quarters)
@@ -401,7 +377,7 @@ __global__ __launch_bounds__(512) void down_mfma_q6k_kernel(MoeShape s, const Ex
     if (pb >= p1) return;
     const int tid = threadIdx.x, wave = tid >> 6, l = tid & 63;
     const int lr = l & 15, kq = l >> 4;
-    const int r0 = blockIdx.x * kGuRows + wave * 16;
+    const int r0 = blockIdx.x * kDnRows + wave * 16;
     const bool on = r0 < s.D;
     const int FF = s.FF, nch = FF / kChunkK, nsb = FF / 256;
     const uint8_t* dbase = table[e].down;
@@ -443,7 +419,7 @@ __global__ __launch_bounds__(512) void down_mfma_q6k_kernel(MoeShape s, const Ex
     if (nch > 1) gload(1, vh1, vl1);
     *reinterpret_cast<uint4*>(&LB[0][0][st_t][st_k]) = vh;
     *reinterpret_cast<uint4*>(&LB[0][1][st_t][st_k]) = vl;
-    __syncthreads();
+    lds_barrier();
     f32x4 out[4];
 #pragma unroll
     for (int nt = 0; nt < 4; nt++) out[nt] = (f32x4){0.f, 0.f, 0.f, 0.f};
@@ -500,7 +476,7 @@ __global__ __launch_bounds__(512) void down_mfma_q6k_kernel(MoeShape s, const Ex
                 *reinterpret_cast<uint4*>(&LB[stg ^ 1][0][st_t][st_k]) = vh1;
                 *reinterpret_cast<uint4*>(&LB[stg ^ 1][1][st_t][st_k]) = vl1;
             }
-            __syncthreads();
+            lds_barrier();
             vh1 = vh2;
             vl1 = vl2;
             if (more && on) {
@@ -540,7 +516,7 @@ hipError_t launch_prep_rows(const int* offs, int E, const int* tok, const float*
 hipError_t launch_gate_up_mfma(const MoeShape& s, const ExpertEntry* table, int E, const int* offs, int nb,
                                const _Float16* xh, const _Float16* xl, const _Float16* xsh, const _Float16* xsl,
                                const float* xscale, float* h, hipStream_t st) {
-    const dim3 g((unsigned)((s.FF + kGuRows - 1) / kGuRows), (unsigned)E, (unsigned)((nb + kPassTok - 1) / kPassTok));
+    const dim3 g((unsigned)((s.FF + kGuRows - 1) / kGuRows), (unsigned)E, (unsigned)((nb + kGuTok - 1) / kGuTok));
     if (s.gate_type == kQ4_K)
         gate_up_mfma_kernel<kQ4_K><<<g, 512, 0, st>>>(s, table, offs, xh, xl, xsh, xsl, xscale, h);
     else
@@ -550,7 +526,7 @@ hipError_t launch_gate_up_mfma(const MoeShape& s, const ExpertEntry* table, int 
 
 hipError_t launch_down_mfma(const MoeShape& s, const ExpertEntry* table, int E, const int* offs, int nb,
                             const _Float16* hh, const _Float16* hl, const float* hscale, float* yp, hipStream_t st) {
-    const dim3 g((unsigned)((s.D + kGuRows - 1) / kGuRows), (unsigned)E, (unsigned)((nb + kPassTok - 1) / kPassTok));
+    const dim3 g((unsigned)((s.D + kDnRows - 1) / kDnRows), (unsigned)E, (unsigned)((nb + kPassTok - 1) / kPassTok));
     down_mfma_q6k_kernel<<<g, 512, 0, st>>>(s, table, offs, hh, hl, hscale, yp);
     return hipGetLastError();
 }
