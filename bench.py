@@ -28,7 +28,7 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 PKG_DIR = os.path.join(ROOT, "eahmmf_inference_prototype_v-0.1.0_amd")
 HBM_PEAK_GBS = 8000.0
 D, FF, E, K = 2048, 768, 128, 8
-Q4_K, Q6_K = 12, 14
+Q4_K, Q5_K, Q6_K = 12, 13, 14
 COPY_BYTES = 256 << 20
 
 
@@ -197,6 +197,101 @@ def bench_c5(args, torch, b, hip):
         "expert_only_decode_tokens_per_s_94_layers": round(1.0 / (94 * el / steps), 1)}), flush=True)
 
 
+def bench_c3(args, torch, b, hip):
+    """Expert-only decode of one token through all 48 MoE layers of the
+    Qwen3-30B-A3B shape (D=2048, FF=768, 128 experts, top-8), every layer
+    resident at its own HBM addresses; one step = 48 layer launches (routing on
+    device).  Runs the Q4_K_M variant (Q4_K gate/up, Q6_K down) and the Q5_K
+    variant (all three components Q5_K)."""
+    D_, FF_, E_, K_, NL = 2048, 768, 128, 8, 48
+    rng = np.random.default_rng(3)
+    stream = torch.cuda.current_stream()
+    sp, vp = ctypes.c_void_p(stream.cuda_stream), ctypes.c_void_p
+    results = {}
+    for name, gt, dt in (("q4_k_m", Q4_K, Q6_K), ("q5_k", Q5_K, Q5_K)):
+        uniq, grb, drb = build_layer_replicated(b, rng, D_, FF_, E_, 16, gt, dt)
+        comps, tables = upload_layers(torch, uniq, E_, NL)  # 48 distinct layers in HBM
+        shape = b.MoeShape(gt, gt, dt, D_, FF_, grb, grb, drb)
+        NS = 16
+        xs = torch.from_numpy(rng.normal(0, 1, (NS, NL, D_)).astype(np.float32)).cuda()
+        dl = torch.from_numpy(rng.normal(0, 1, (NS, NL, E_)).astype(np.float32)).cuda()
+        dy = torch.empty((NS, NL, D_), dtype=torch.float32, device="cuda")
+
+        def token(i):
+            s_ = i % NS
+            for layer in range(NL):
+                rc = hip.eahmmf_hip_moe_layer_decode_async(ctypes.byref(shape), vp(tables[layer].data_ptr()), E_,
+                                                           vp(dl[s_, layer].data_ptr()), K_,
+                                                           vp(xs[s_, layer].data_ptr()), vp(dy[s_, layer].data_ptr()),
+                                                           None, None, sp)
+                assert rc == 0, b.last_error()
+
+        steps = args.steps if args.steps else 100
+        for i in range(args.warmup if args.warmup else 5):
+            token(i)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for i in range(steps):
+            token(i)
+        e1.record(stream)
+        torch.cuda.synchronize()
+        assert hip.eahmmf_hip_device_flags() == 0
+        el = e0.elapsed_time(e1) * 1e-3
+        bytes_tok = NL * K_ * (2 * FF_ * grb + D_ * drb)
+        results[name] = {"tokens_per_s": round(steps / el, 1), "ms_per_token": round(el * 1e3 / steps, 4),
+                         "GB_s": round(bytes_tok * steps / el / 1e9, 1), "bytes_per_token": bytes_tok,
+                         "pct_of_hbm_peak": round(100 * bytes_tok * steps / el / 1e9 / HBM_PEAK_GBS, 2)}
+        del comps, tables
+        torch.cuda.empty_cache()
+    print(json.dumps({
+        "metric": "expert-only decode tokens/s, 48 MoE layers of the Qwen3-30B-A3B shape", "unit": "tokens/s",
+        "value": results["q4_k_m"]["tokens_per_s"], "n_gpus": 1, "higher_is_better": True, "dtype": "f32",
+        "data": "synthetic",
+        "config": {"workload": "one decode token through 48 resident MoE layers (D=2048 FF=768 128 experts top-8), "
+                               "routing on device, one fused launch per layer; attention and the router matmul "
+                               "are not part of the step"},
+        "variants": results}), flush=True)
+
+
+def host_io_rate(b, hip, torch, dgate, dup, ddown, steps=2000):
+    """The reference's calling convention at C2: routing on the host, then the
+    synchronous eahmmf_hip_moe_decode with pageable host x / y (two 8 KB copies
+    and a stream synchronisation per call).  GB/s over the routed experts' bytes."""
+    rng = np.random.default_rng(7)
+    xs = rng.normal(0, 1, (64, D)).astype(np.float32)
+    logits = rng.normal(0, 1, (64, E)).astype(np.float32)
+    grb, drb = b.row_bytes(Q4_K, D), b.row_bytes(Q6_K, FF)
+    y = np.empty(D, np.float32)
+    sets = []
+    for s_ in range(64):
+        lg = logits[s_]
+        e_ = np.exp(lg - lg.max())
+        ids = sorted(range(E), key=lambda i: (-e_[i], i))[:K]
+        tot = np.float32(0)
+        for i in ids:
+            tot = np.float32(tot + np.float32(e_[i]))
+        ex = (b.Expert * K)()
+        w = np.array([np.float32(e_[i]) / tot for i in ids], np.float32)
+        r = s_ % dgate.shape[0]
+        for j, e in enumerate(ids):
+            ex[j].gate = b.Weight(dgate[r, e].data_ptr(), Q4_K, D, FF, grb)
+            ex[j].up = b.Weight(dup[r, e].data_ptr(), Q4_K, D, FF, grb)
+            ex[j].down = b.Weight(ddown[r, e].data_ptr(), Q6_K, FF, D, drb)
+        sets.append((ex, w))
+    for i in range(20):
+        ex, w = sets[i % 64]
+        assert hip.eahmmf_hip_moe_decode(ex, w.ctypes.data, K, xs[i % 64].ctypes.data, y.ctypes.data)
+    t0 = time.perf_counter()
+    for i in range(steps):
+        ex, w = sets[i % 64]
+        assert hip.eahmmf_hip_moe_decode(ex, w.ctypes.data, K, xs[i % 64].ctypes.data, y.ctypes.data)
+    el = time.perf_counter() - t0
+    bytes_step = K * (2 * FF * grb + D * drb)
+    return {"GB_s": round(bytes_step * steps / el / 1e9, 2), "us_per_call": round(el * 1e6 / steps, 2),
+            "what": "synchronous eahmmf_hip_moe_decode, pageable host x/y, host routing outside the timed call"}
+
+
 def cpu_baseline(gate, up, down, xs, logits, budget_s):
     """Times the reference CPU expert path on a bounded sample of layer-tokens:
     the compiled reference's own matmul (oracle/_ref) when present, else the
@@ -285,9 +380,9 @@ def main():
     ap.add_argument("--replicas", type=int, default=None, help="layer copies in HBM (c2 16, c4 4, c5 4)")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--workload", choices=("c2", "c4", "c5"), default="c2",
-                    help="c2 (default): the headline single-token layer; c4: ragged grouped prefill; "
-                         "c5: single-token layer at the 235B shape")
+    ap.add_argument("--workload", choices=("c2", "c3", "c4", "c5"), default="c2",
+                    help="c2 (default): the headline single-token layer; c3: one token through 48 layers; "
+                         "c4: ragged grouped prefill; c5: single-token layer at the 235B shape")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a plain 256 MiB device copy (the reference kernel for scaling HBM counters)")
     args = ap.parse_args()
@@ -308,7 +403,7 @@ def main():
     if args.workload != "c2":
         hip_ = b.lib()
         torch.cuda.set_device(0)
-        (bench_c4 if args.workload == "c4" else bench_c5)(args, torch, b, hip_)
+        {"c3": bench_c3, "c4": bench_c4, "c5": bench_c5}[args.workload](args, torch, b, hip_)
         return
     hip = b.lib()
     torch.cuda.set_device(0)
@@ -369,17 +464,26 @@ def main():
     value = bytes_step * args.steps / el / 1e9
     ms = el * 1e3 / args.steps
 
-    # the layer kernel alone, HIP events on the launch stream
-    n_ev = 200
-    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(n_ev)]
+    # the layer kernel's average launch duration: HIP events on the launch
+    # stream bracketing n_ev back-to-back launches (each step is one launch)
+    n_ev = 400
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    ev0.record(stream)
     for i in range(n_ev):
+        step(i)
+    ev1.record(stream)
+    torch.cuda.synchronize()
+    kern_us = ev0.elapsed_time(ev1) * 1e3 / n_ev
+    achieved = bytes_step / (kern_us * 1e-6) / 1e9
+    # spread: per-launch event pairs (each includes the events' own overhead)
+    n_sp = 200
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(n_sp)]
+    for i in range(n_sp):
         ev[i][0].record(stream)
         step(i)
         ev[i][1].record(stream)
     torch.cuda.synchronize()
     durs = np.array([a.elapsed_time(z) for a, z in ev]) * 1e3  # us
-    kern_us = float(np.mean(durs))
-    achieved = bytes_step / (kern_us * 1e-6) / 1e9
 
     out = {
         "metric": "expert-FFN HBM GB/s (% of peak) + decode tokens/s at Qwen3-30B-A3B Q4_K_M",
@@ -395,10 +499,12 @@ def main():
         "roofline": {"bound": "hbm", "kernel": kernel_name,
                      "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": measured_traffic(fused),
-                     "avg_us": round(kern_us, 3), "p10_us": round(float(np.percentile(durs, 10)), 3),
-                     "p90_us": round(float(np.percentile(durs, 90)), 3),
+                     "avg_us": round(kern_us, 3),
+                     "p10_us_with_event_overhead": round(float(np.percentile(durs, 10)), 3),
+                     "p90_us_with_event_overhead": round(float(np.percentile(durs, 90)), 3),
                      "xcd_local_exchange": int(hip.eahmmf_hip_fused_exchange())},
     }
+    out["host_io"] = host_io_rate(b, hip, torch, dgate, dup, ddown)
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline(gate, up, down, xs, logits, args.cpu_seconds)
     print(json.dumps(out), flush=True)
