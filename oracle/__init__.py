@@ -77,6 +77,8 @@ def lib():
         L.orc_state_free.argtypes = [vp]
         L.orc_state_trace.argtypes = [vp, vp, vp, ctypes.c_int, ctypes.POINTER(ctypes.c_int)]
         L.orc_forward.argtypes = [vp, vp, ctypes.c_int, ctypes.c_int, vp]
+        L.orc_state_set_moe_hook.argtypes = [vp, vp, vp]
+        L.orc_state_set_moe_hook.restype = None
         L.orc_init()
         _lib = L
     return _lib
@@ -217,6 +219,36 @@ class OracleModel:
         m.experts = ex
         self._model = m
         self.state = lib().orc_state_new(ctypes.byref(m))
+
+    MoeHook = ctypes.CFUNCTYPE(ctypes.c_int, vp, ctypes.c_int, ctypes.POINTER(ctypes.c_float), ctypes.c_int,
+                               ctypes.c_int, ctypes.POINTER(ctypes.c_int), ctypes.POINTER(ctypes.c_float),
+                               ctypes.POINTER(ctypes.c_float))
+
+    def set_moe_hook(self, fn):
+        """Replace the expert block of every layer with fn(layer, xn[nb][D],
+        ids[nb][k], wts[nb][k]) -> out[nb][D] (numpy arrays); None restores the
+        oracle's own block."""
+        if fn is None:
+            self._hook = None
+            lib().orc_state_set_moe_hook(self.state, None, None)
+            return
+        D = self.spec.D
+
+        def tramp(ctx, layer, xn, nb, k, ids, wts, out):
+            try:
+                x = np.ctypeslib.as_array(xn, shape=(nb, D)).copy()
+                i = np.ctypeslib.as_array(ids, shape=(nb, k)).copy()
+                w = np.ctypeslib.as_array(wts, shape=(nb, k)).copy()
+                y = np.asarray(fn(layer, x, i, w), dtype=np.float32)
+                np.ctypeslib.as_array(out, shape=(nb, D))[:] = y
+                return 0
+            except Exception:  # reported as a failed forward
+                import traceback
+                traceback.print_exc()
+                return 1
+
+        self._hook = self.MoeHook(tramp)
+        lib().orc_state_set_moe_hook(self.state, ctypes.cast(self._hook, vp), None)
 
     def forward(self, toks, p0, want_logits=True):
         """One batch at positions p0.. (Engine::forward)."""

@@ -290,7 +290,14 @@ struct orc_state {
     int* trace_ids;
     float* trace_w;
     int trace_cap, trace_n;
+    orc_moe_hook hook;  /* optional replacement of the expert block */
+    void* hook_ctx;
 };
+
+void orc_state_set_moe_hook(orc_state* s, orc_moe_hook fn, void* ctx) {
+    s->hook = fn;
+    s->hook_ctx = ctx;
+}
 
 orc_state* orc_state_new(const orc_model* m) {
     orc_init();
@@ -432,7 +439,15 @@ int orc_forward(orc_state* s, const int* toks, int nb, int p0, float* logits) {
         for (int i = 0; i < nb * K; i++) trace_push(s, ids[i], wts[i]);
         for (int e = 0; e < E * 3; e++) ev[e] = m->experts[(size_t)l * E * 3 + e];
         orc_experts ex = {E, D, m->FF, ev};
-        orc_moe_layer(&ex, xn, nb, K, ids, wts, tmp);
+        if (s->hook) {
+            if (s->hook(s->hook_ctx, l, xn, nb, K, ids, wts, tmp) != 0) {
+                free(x); free(xn); free(q); free(kk); free(vv); free(att); free(tmp); free(rl); free(sc);
+                free(rc); free(rs); free(ids); free(wts); free(ev);
+                return -2;
+            }
+        } else {
+            orc_moe_layer(&ex, xn, nb, K, ids, wts, tmp);
+        }
         for (int i = 0; i < nb * D; i++) x[i] += tmp[i];
     }
     if (logits) {

@@ -97,6 +97,14 @@ typedef struct {
 
 typedef struct orc_state orc_state;
 orc_state* orc_state_new(const orc_model* m);
+/* Optional replacement of the expert block inside orc_forward, so that another
+ * implementation of qwen3moe.cpp:1024-1067 can be checked end to end against
+ * the reference's logits: called per layer with the normalised activations
+ * xn[nb][D], the routing ids/wts[nb][k] and out[nb][D]; nonzero aborts the
+ * forward (orc_forward then returns -2). */
+typedef int (*orc_moe_hook)(void* ctx, int layer, const float* xn, int nb, int k, const int* ids,
+                            const float* wts, float* out);
+void orc_state_set_moe_hook(orc_state* s, orc_moe_hook fn, void* ctx);
 void orc_state_free(orc_state* s);
 /* Optional routing trace: every (id, w) chosen, in token/rank order. */
 void orc_state_trace(orc_state* s, int* ids, float* wts, int cap, int* count);

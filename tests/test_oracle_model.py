@@ -138,3 +138,31 @@ def test_config0_greedy_matches_reference():
     # differs from the reference's omp-simd reduction, so weights agree to a
     # few ulps of the logits rather than bit for bit
     np.testing.assert_allclose(w, ref["trace_w"], rtol=5e-5, atol=0)
+
+
+def test_moe_hook_with_oracle_block_reproduces_forward(tiny):
+    """The expert-block hook used for end-to-end checks of the HIP path: with
+    the oracle's own block plugged in, logits are bit-identical."""
+    spec, ref = tiny
+    E = spec.n_expert
+    layers = []
+    for l in range(spec.n_layer):
+        comps = []
+        for nm in ("ffn_gate_exps", "ffn_up_exps", "ffn_down_exps"):
+            t, ne, data = spec.tensors[f"blk.{l}.{nm}.weight"]
+            data = np.ascontiguousarray(data).reshape(E, -1)
+            comps.append((t, data))
+        layers.append([[(comps[c][0], comps[c][1][e].reshape(-1)) for c in range(3)] for e in range(E)])
+    a = oracle.OracleModel(spec)
+    want = a.eval(ref["prompt"], 0, 32)
+    b = oracle.OracleModel(spec)
+    calls = []
+
+    def hook(layer, x, ids, w):
+        calls.append((layer, x.shape[0]))
+        return oracle.moe_layer(layers[layer], x, ids, w)
+
+    b.set_moe_hook(hook)
+    got = b.eval(ref["prompt"], 0, 32)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    assert calls == [(l, len(ref["prompt"])) for l in range(spec.n_layer)]
