@@ -62,13 +62,93 @@ __device__ __forceinline__ uint16_t ld_u16(const uint8_t* p) {
     return *reinterpret_cast<const uint16_t*>(p);
 }
 
+// 32 bytes at a 2-byte-aligned LDS address: nine aligned dwords realigned
+// with v_alignbit, so no LDS access is unaligned.  Reads up to 2 bytes past
+// the 32 (the callers' LDS buffers leave room).
+__device__ __forceinline__ Bytes32A2 lds_ld32_a2(const uint8_t* p) {
+    const uint32_t off = (uint32_t)(uintptr_t)p & 3u;
+    const uint32_t* b = reinterpret_cast<const uint32_t*>(p - off);
+    uint32_t d[9];
+#pragma unroll
+    for (int i = 0; i < 9; i++) d[i] = b[i];
+    Bytes32A2 r;
+#pragma unroll
+    for (int i = 0; i < 8; i++) r.w[i] = __builtin_amdgcn_alignbit(d[i + 1], d[i], off * 8u);
+    return r;
+}
+
+// How a weight row segment is read: straight from global memory, or from an
+// LDS copy that keeps the row's global alignment modulo 16 (16-byte loads
+// stay aligned; 2-byte-aligned 32-byte groups are realigned in registers).
+struct GlobalLd {
+    static __device__ __forceinline__ uint4 b16(const uint8_t* p) { return ld16(p); }
+    static __device__ __forceinline__ Bytes32A2 b32a2(const uint8_t* p) { return ld32_a2(p); }
+    static __device__ __forceinline__ uint16_t u16(const uint8_t* p) { return ld_u16(p); }
+};
+struct LdsLd {
+    static __device__ __forceinline__ uint4 b16(const uint8_t* p) { return ld16(p); }
+    static __device__ __forceinline__ Bytes32A2 b32a2(const uint8_t* p) { return lds_ld32_a2(p); }
+    static __device__ __forceinline__ uint16_t u16(const uint8_t* p) { return ld_u16(p); }
+};
+
+// One nontemporal LDS DMA instruction (global_load_lds_dwordx4 ... nt): lane
+// i's 16 bytes at gaddr land at LDS address lds + 16*i (lds wave-uniform).
+// Written as inline assembly on purpose: the compiler does not see the LDS
+// write, so it adds no wait of its own (it would otherwise wait for every DMA
+// in flight before any read of the target buffer).  Every read of DMA'd data
+// is therefore ordered by an explicit s_waitcnt vmcnt of the issuing wave,
+// followed by a barrier where other waves read it.  Counters are retired in
+// issue order, so the compiler's own waits for its loads stay correct (they
+// can only become longer).
+__device__ __forceinline__ void lds_dma16(uintptr_t gaddr, const uint8_t* lds) {
+    // wave-uniform by contract; readfirstlane puts it in an SGPR for M0
+    const uint32_t base = (uint32_t)__builtin_amdgcn_readfirstlane(
+        (int)(uint32_t)(uintptr_t)(__attribute__((address_space(3))) const uint8_t*)lds);
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off nt"
+                 :
+                 : "v"(gaddr), "s"(base)
+                 : "memory", "m0");
+#pragma clang diagnostic pop
+}
+
+// Copy NI x 1024 bytes from global memory into LDS, one wave, one 16-byte
+// chunk per lane per instruction: the n bytes from src (n >= 1) land at
+// dst + (src & 15), dst 16-byte aligned.  Exactly NI instructions are issued
+// whatever n is (lanes past the end re-read the last chunk into dst's tail),
+// so a caller can count them in vmcnt.  Measured on MI355X: a 24.5 MB
+// one-pass read this way finishes in about half the time plain loads into
+// registers take.
+template <int NI>
+__device__ __forceinline__ void dma_to_lds(const uint8_t* src, int n, uint8_t* dst, int lane) {
+    const uintptr_t a = (uintptr_t)src & ~(uintptr_t)15;
+    const int n16 = (int)(((((uintptr_t)src + (uintptr_t)n + 15) & ~(uintptr_t)15) - a) / 16);
+#pragma unroll
+    for (int i = 0; i < NI; i++) {
+        const int c = min(i * 64 + lane, n16 - 1);
+        lds_dma16(a + (uintptr_t)c * 16, dst + i * 1024);
+    }
+}
+
+// s_waitcnt vmcnt(N): at most N of this wave's vector memory operations are
+// still outstanding (gfx9 encoding: vmcnt in bits 3:0 and 15:14, expcnt 7,
+// lgkmcnt 15).  Compiler fences keep memory accesses on their side of it.
+template <int N>
+__device__ __forceinline__ void wait_vm_upto() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+
 // Exact half -> float.  Finite values and infinities convert exactly in
 // hardware; NaN is canonicalised (sign kept) as the reference's table does
 // (qwen3moe.cpp:59).
 __device__ __forceinline__ float half_to_float(uint32_t h) {
-    float v = (float)__builtin_bit_cast(_Float16, (uint16_t)h);
-    if ((h & 0x7C00u) == 0x7C00u && (h & 0x3FFu)) v = __builtin_bit_cast(float, 0x7FC00000u | ((h & 0x8000u) << 16));
-    return v;
+    const float v = (float)__builtin_bit_cast(_Float16, (uint16_t)h);
+    const bool nan = ((h & 0x7C00u) == 0x7C00u) & ((h & 0x3FFu) != 0u);
+    return nan ? __builtin_bit_cast(float, 0x7FC00000u | ((h & 0x8000u) << 16)) : v;
 }
 
 __device__ __forceinline__ uint32_t byte_of(uint32_t w, int i) { return (w >> (8 * i)) & 0xFFu; }
@@ -76,17 +156,15 @@ __device__ __forceinline__ uint32_t byte_of(uint32_t w, int i) { return (w >> (8
 // 12 scale bytes held in three words -> 6-bit (scale, min) of sub-block j
 // (qwen3moe.cpp:133-141).
 __device__ __forceinline__ void scale_min_k4(int j, uint32_t s0, uint32_t s1, uint32_t s2, uint32_t& sc, uint32_t& mn) {
-    // bytes q[0..3] = s0, q[4..7] = s1, q[8..11] = s2
-    if (j < 4) {
-        sc = byte_of(s0, j) & 63u;
-        mn = byte_of(s1, j) & 63u;
-    } else {
-        const uint32_t qj4 = byte_of(s2, j - 4);   // q[j+4]
-        const uint32_t qjm4 = byte_of(s0, j - 4);  // q[j-4]
-        const uint32_t qj = byte_of(s1, j - 4);    // q[j]
-        sc = (qj4 & 15u) | ((qjm4 >> 6) << 4);
-        mn = (qj4 >> 4) | ((qj >> 6) << 4);
-    }
+    // bytes q[0..3] = s0, q[4..7] = s1, q[8..11] = s2; both forms are formed
+    // and one selected, so lanes with different j do not diverge
+    const int jj = j & 3;
+    const uint32_t b0 = byte_of(s0, jj);  // q[j] (j < 4) or q[j-4]
+    const uint32_t b1 = byte_of(s1, jj);  // q[j+4] (j < 4) or q[j]
+    const uint32_t b2 = byte_of(s2, jj);  // q[j+4] (j >= 4)
+    const bool lo = j < 4;
+    sc = lo ? (b0 & 63u) : ((b2 & 15u) | ((b0 >> 6) << 4));
+    mn = lo ? (b1 & 63u) : ((b2 >> 4) | ((b1 >> 6) << 4));
 }
 
 // ---------------------------------------------------------------------------
