@@ -50,7 +50,7 @@ struct DeviceBuf {
 
 struct DevCtx {
     hipStream_t stream = nullptr;
-    DeviceBuf dx, dy, dy2, dh, dids, dw, dyp, dgs, dtab;  // device scratch
+    DeviceBuf dx, dy, dy2, dh, dids, dw, dyp, dhx, dgs, dtab;  // device scratch
     DeviceBuf px, py, py2;                // pinned host staging
     unsigned* dsync = nullptr;            // fused-launch counters and flags (zeroed once)
     unsigned epoch = 0;                   // fused launches issued on dsync
@@ -146,7 +146,27 @@ void unstage_rows(const float* dense, int nb, int n, float* host, int ld) {
 }
 
 // the fused launch's per-partition partial outputs (8 partitions x D floats)
-bool grow_fused(DevCtx* c, const MoeShape& s) { return grow_device(c->dyp, (size_t)8 * s.D * sizeof(float)); }
+// The fused kernel's exchange words (h and the per-partition partials, each
+// a value and a launch epoch): zeroed when allocated, so that no stale word
+// can carry the epoch of a launch to come (epochs start at 1).
+static bool grow_zeroed(DeviceBuf& b, size_t need) {
+    if (need <= b.cap) return true;
+    if (!grow_device(b, need)) return false;
+    // complete before any launch: the fused kernel runs on non-blocking streams
+    if (!hip_ok(hipMemset(b.p, 0, b.cap), "hipMemset(exchange words)") ||
+        !hip_ok(hipDeviceSynchronize(), "hipDeviceSynchronize(exchange words)")) {
+        (void)hipFree(b.p);
+        b.p = nullptr;
+        b.cap = 0;
+        return false;
+    }
+    return true;
+}
+
+bool grow_fused(DevCtx* c, const MoeShape& s, int k) {
+    return grow_zeroed(c->dyp, (size_t)8 * s.D * sizeof(uint64_t)) &&
+           grow_zeroed(c->dhx, (size_t)k * s.FF * sizeof(uint64_t));
+}
 
 bool weight_ok(const eahmmf_hip_weight& w) { return w.dev && type_supported(w.type) && w.ne0 > 0 && w.ne1 > 0; }
 
@@ -242,7 +262,7 @@ bool eahmmf_hip_moe_decode(const eahmmf_hip_expert* experts, const float* w, int
     bool ok = grow_device(c->dy, ybytes) && grow_pinned(c->py, ybytes) &&
               grow_device(c->dh, (size_t)k * s.FF * sizeof(float)) && stage_x(c, host_x, 1, s.D, s.D);
     if (ok) {
-        if (fused_enabled() && fused_supported(s, k, 0) && grow_fused(c, s)) {
+        if (fused_enabled() && fused_supported(s, k, 0) && grow_fused(c, s, k)) {
             FusedArgsHost f;
             f.shape = s;
             f.k = k;
@@ -250,9 +270,9 @@ bool eahmmf_hip_moe_decode(const eahmmf_hip_expert* experts, const float* w, int
             f.direct = slots;
             f.x = (const float*)c->dx.p;
             f.y = (float*)c->dy.p;
-            f.h = (float*)c->dh.p;
+            f.hx = (uint64_t*)c->dhx.p;
             f.sync = c->dsync;
-            f.ypart = (float*)c->dyp.p;
+            f.ypart = (uint64_t*)c->dyp.p;
             f.epoch = ++c->epoch;
             ok = hip_ok(launch_moe_fused(f, c->stream), "fused moe decode launch");
         } else {
@@ -299,7 +319,7 @@ int eahmmf_hip_moe_decode_async(const eahmmf_hip_moe_shape* shape, const eahmmf_
     DevCtx* c = ctx_for_current_device();
     if (!c) return -2;
     if (!grow_device(c->dh, (size_t)k * s.FF * sizeof(float))) return -2;
-    if (fused_enabled() && fused_supported(s, k, 0) && grow_fused(c, s)) {
+    if (fused_enabled() && fused_supported(s, k, 0) && grow_fused(c, s, k)) {
         FusedArgsHost f;
         f.shape = s;
         f.k = k;
@@ -307,9 +327,9 @@ int eahmmf_hip_moe_decode_async(const eahmmf_hip_moe_shape* shape, const eahmmf_
         f.direct = slots;
         f.x = dev_x;
         f.y = dev_y;
-        f.h = (float*)c->dh.p;
+        f.hx = (uint64_t*)c->dhx.p;
         f.sync = c->dsync;
-        f.ypart = (float*)c->dyp.p;
+        f.ypart = (uint64_t*)c->dyp.p;
         f.epoch = ++c->epoch;
         return hip_ok(launch_moe_fused(f, (hipStream_t)stream), "fused moe decode launch") ? 0 : -3;
     }
@@ -329,7 +349,7 @@ int eahmmf_hip_moe_decode_routed_async(const eahmmf_hip_moe_shape* shape, const 
     DevCtx* c = ctx_for_current_device();
     if (!c) return -2;
     if (!grow_device(c->dh, (size_t)k * s.FF * sizeof(float))) return -2;
-    if (fused_enabled() && fused_supported(s, k, 0) && grow_fused(c, s)) {
+    if (fused_enabled() && fused_supported(s, k, 0) && grow_fused(c, s, k)) {
         FusedArgsHost f;
         f.shape = s;
         f.k = k;
@@ -340,9 +360,9 @@ int eahmmf_hip_moe_decode_routed_async(const eahmmf_hip_moe_shape* shape, const 
         f.w_in = dev_w;
         f.x = dev_x;
         f.y = dev_y;
-        f.h = (float*)c->dh.p;
+        f.hx = (uint64_t*)c->dhx.p;
         f.sync = c->dsync;
-        f.ypart = (float*)c->dyp.p;
+        f.ypart = (uint64_t*)c->dyp.p;
         f.epoch = ++c->epoch;
         return hip_ok(launch_moe_fused(f, (hipStream_t)stream), "fused routed moe decode launch") ? 0 : -3;
     }
@@ -365,7 +385,7 @@ int eahmmf_hip_moe_layer_decode_async(const eahmmf_hip_moe_shape* shape, const e
     if (!c) return -2;
     if (!grow_device(c->dh, (size_t)k * s.FF * sizeof(float))) return -2;
     hipStream_t st = (hipStream_t)stream;
-    if (fused_enabled() && fused_supported(s, k, n_expert) && grow_fused(c, s)) {
+    if (fused_enabled() && fused_supported(s, k, n_expert) && grow_fused(c, s, k)) {
         FusedArgsHost f;
         f.shape = s;
         f.k = k;
@@ -377,9 +397,9 @@ int eahmmf_hip_moe_layer_decode_async(const eahmmf_hip_moe_shape* shape, const e
         f.w_out = dev_w_out;
         f.x = dev_x;
         f.y = dev_y;
-        f.h = (float*)c->dh.p;
+        f.hx = (uint64_t*)c->dhx.p;
         f.sync = c->dsync;
-        f.ypart = (float*)c->dyp.p;
+        f.ypart = (uint64_t*)c->dyp.p;
         f.epoch = ++c->epoch;
         return hip_ok(launch_moe_fused(f, st), "fused moe layer launch") ? 0 : -3;
     }
@@ -600,7 +620,7 @@ void eahmmf_hip_shutdown(void) {
     if (it == g_ctx.end()) return;
     DevCtx& c = it->second;
     if (c.stream) (void)hipStreamSynchronize(c.stream);
-    for (DeviceBuf* b : {&c.dx, &c.dy, &c.dy2, &c.dh, &c.dids, &c.dw, &c.dyp, &c.dgs, &c.dtab})
+    for (DeviceBuf* b : {&c.dx, &c.dy, &c.dy2, &c.dh, &c.dids, &c.dw, &c.dyp, &c.dhx, &c.dgs, &c.dtab})
         if (b->p) (void)hipFree(b->p);
     for (DeviceBuf* b : {&c.px, &c.py, &c.py2})
         if (b->p) (void)hipHostFree(b->p);

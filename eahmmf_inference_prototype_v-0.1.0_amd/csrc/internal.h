@@ -62,10 +62,10 @@ struct FusedArgsHost {
     float* w_out = nullptr;
     const float* x = nullptr;
     float* y = nullptr;
-    float* h = nullptr;           // k * FF floats
-    float* ypart = nullptr;       // 8 * D floats: per-partition partial outputs
-    unsigned* sync = nullptr;     // kSyncWords counters, zero before the first launch
-    unsigned epoch = 0;           // launch number on this sync buffer, starting at 1
+    uint64_t* hx = nullptr;       // k * FF exchange words (h value | epoch << 32), zeroed when allocated
+    uint64_t* ypart = nullptr;    // 8 * D exchange words: per-partition partial outputs, zeroed when allocated
+    unsigned* sync = nullptr;     // kSyncWords words, zero before the first launch (error flag)
+    unsigned epoch = 0;           // launch number on these buffers, starting at 1
 };
 constexpr int kSyncWords = 4096;
 constexpr int kSyncFlagWord = 1020;  // error flag word inside the sync buffer

@@ -27,35 +27,35 @@
 //   1. routing: wave 0 reads the logits and the expert table and forms the
 //      keys e_i = expf(l_i - max) while waves 1-7 turn x into three int8
 //      levels per 64-value segment in LDS; then every thread ranks
-//      candidates by counting (e desc, id asc - the reference's order) and
-//      the top k land in LDS slots.
+//      candidates by counting larger keys (e desc, id asc - the reference's
+//      order) and the top k land in LDS slots.
 //   2. A waves: lane groups of D/64 lanes own one 64-value segment of x each.
 //      A pass of an A wave is GW = 64 / (D/64) consecutive (expert, row)
 //      pairs of the workgroup's slice; the wave DMAs the gate and up rows of
 //      up to NPA passes into its own LDS ring, waits for each pass with an
 //      exact vmcnt, dots the rows exactly in int32 (v_dot4) against the
-//      activation levels, reduces in the group and keeps h = silu(g) * u in
-//      LDS; the next pass is issued into the slot just consumed.
-//      B waves: once the A waves' first passes are issued, DMA this
-//      workgroup's down rows of the partition's experts (its output-row
-//      chunk) into LDS; wave 4 renormalises the routing weights.
-//   3. partition barrier.  Each A wave stores its h values; the last A wave
-//      of a workgroup to see its stores complete publishes the workgroup's
-//      arrival.  XCD-local: a flag word per workgroup set to the launch epoch,
-//      all m of them polled by wave 0 with agent-scope loads (which miss the
-//      CU's L1); otherwise one atomic counter per partition.  B waves take no
-//      part, so their outstanding DMA never delays the flag.
-//   4. all threads turn the partition's h into int8 levels in LDS; all eight
-//      waves compute w_j * down_j[r].h_j per (row, 64-value segment) unit
-//      from the staged rows, and the units of each row are summed in a fixed
-//      order into this partition's partial ypart[p][r].  Chunks with more
-//      rows than the stage holds take several rounds.
-//   5. per row chunk, one workgroup adds the NP partials in partition order
-//      (deterministic) and writes y: partition q % NP once all NP epoch flags
-//      of the chunk are set (XCD-local), else the last partition to arrive.
-// Counters are reset by the last workgroup through each stage, so every
-// launch starts from zero; epoch flags need no reset.  Every wait is bounded;
-// if a bound is ever hit an error flag is raised and the kernel still exits.
+//      activation levels, reduces in the group and stores h = silu(g) * u
+//      with the launch epoch in one 64-bit word; the next pass is issued into
+//      the slot just consumed.  B waves: once the A waves' first passes are
+//      issued, DMA this workgroup's down rows (its output-row chunk of the
+//      partition's experts) into LDS; wave 4 renormalises the routing
+//      weights.
+//   3. once the down rows have landed every wave decodes its first NPD
+//      phase-B tasks into registers.
+//   4. all threads read the partition's h - polling until every word
+//      carries this launch's epoch - and turn it into int8 levels in LDS;
+//      every wave computes w_j * down_j[r].h_j per (row, 64-value segment)
+//      unit from the staged rows, and the units of each row are summed in a
+//      fixed order into this partition's partial ypart[p][r] (value and
+//      epoch again).  Chunks with more rows than the stage holds take
+//      several rounds.
+//   5. workgroup q of partition q % NP polls the NP partials of each row of
+//      chunk q until all carry this epoch and adds them in partition order
+//      (deterministic) into y.
+// Nothing is reset between launches: a word is current exactly when it
+// carries this launch's epoch (launches are numbered from 1 and the exchange
+// buffers are zeroed when allocated).  Every wait is bounded; if a bound is
+// ever hit an error flag is raised and the kernel still exits.
 #include <mutex>
 
 #include "internal.h"
@@ -65,16 +65,17 @@ namespace eahmmf {
 
 constexpr int kThreads = 512;
 constexpr int kWaves = kThreads / 64;
-constexpr int kAWaves = 4;  // waves 0-3: gate/up; waves 4-7: down staging
+constexpr int kAWaves = 4;  // waves 0-3: gate/up passes; waves 4-7: down staging
 constexpr int kAThreads = 64 * kAWaves;
 constexpr int kMaxD = 4096;
 constexpr int kMaxE = 256;
-constexpr int kMaxHP = 4096;     // floats of h held per partition
+constexpr int kMaxHP = 4096;     // values of h held per partition
 constexpr int kMaxPart = 2048;   // (row, segment) partials of one round
-constexpr int kMaxHW = 128;      // h values one workgroup computes
-constexpr int NPD = 3;           // phase-B tasks each B wave decodes before the barrier
+constexpr int kMaxHW = 128;      // (expert, row) pairs one workgroup computes
+constexpr int NPD = 2;           // phase-B tasks each wave decodes before the barrier
 constexpr int kSlotA = 20 * 1024;   // LDS ring of one A wave
 constexpr int kStageB = 40 * 1024;  // LDS for one round of down rows
+constexpr int kDmaB = kStageB / 1024 / (kWaves - kAWaves);  // round-0 down copies per B wave
 constexpr unsigned kSpinLimit = 1u << 22;
 
 // One A pass: GW rows of gate and GW rows of up, GW * row bytes =
@@ -86,17 +87,13 @@ struct PassA {
     static constexpr int bytes = 4096 * Fmt<T>::bytes / Fmt<T>::blck;
     static constexpr int nir = (bytes + 32 + 1023) / 1024;
     static constexpr int slot = 2 * nir * 1024;
-    static constexpr int n = kSlotA / slot < 3 ? kSlotA / slot : 3;
+    // two passes in flight: more data in flight per CU only delays the first
+    // pass (the memory system interleaves every CU's outstanding copies)
+    static constexpr int n = kSlotA / slot < 2 ? kSlotA / slot : 2;
     static_assert(n >= 1, "an A pass must fit the ring");
 };
 
-// sync buffer layout (unsigned words, kSyncWords in all).  Atomic counters
-// serve the device-coherent protocol; epoch flags serve the XCD-local one.
-constexpr int kSyncArrive = 0, kSyncPass = 8, kSyncChunk = 16, kSyncErr = kSyncFlagWord;
-constexpr int kMaxChunks = 512;
-constexpr int kMaxM = 128;                             // workgroups per partition (epoch flags, 2 per lane)
-constexpr int kFlagArrive = 1024, kFlagChunk = 2048;  // [8][kMaxM] each
-static_assert(kSyncChunk + kMaxChunks <= kSyncErr && kFlagChunk + 8 * kMaxM <= kSyncWords, "sync layout");
+constexpr int kSyncErr = kSyncFlagWord;  // the only word of the sync buffer this kernel uses
 
 struct FusedArgs {
     MoeShape s;
@@ -108,7 +105,7 @@ struct FusedArgs {
     int stride_b;           // LDS bytes per expert in the phase-B stage (multiple of 1024)
     int rank_shift, rank_c;  // routing: log2 of the threads per candidate, keys each of them compares
     int local_l2;            // 1: partition p runs on XCD p, so h is exchanged through that XCD's L2
-    unsigned epoch;         // launch number (>= 1): the value this launch's flags carry
+    unsigned epoch;          // launch number (>= 1): the high word of this launch's exchange words
     const ExpertEntry* table;
     const float* logits;
     const int* ids_in;
@@ -117,8 +114,8 @@ struct FusedArgs {
     float* w_out;
     const float* x;
     float* y;
-    float* h;      // k * FF
-    float* ypart;  // np * D
+    uint64_t* hx;     // k * FF words: h value bits | epoch << 32
+    uint64_t* ypart;  // np * D words: partial value bits | epoch << 32
     unsigned* sync;
     // last: read only in mode 0, so the fields above share the first few
     // cache lines of the argument block (the kernel rereads them as it goes)
@@ -145,33 +142,22 @@ __device__ __forceinline__ float dpp_max(float v) {
     return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
 }
 
-// Device-coherent (sc1) accesses: visible across the XCDs' separate L2s
-// without whole-cache writeback or invalidate.
-__device__ __forceinline__ void store_coherent(float* p, float v) {
-    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+// Exchange words: a float and the launch epoch in one 64-bit word, so that a
+// reader polls the data itself.  Stores are single-copy atomic; a reader in
+// another XCD needs the device-coherent (sc1) store, a reader in the same XCD
+// finds a plain store in the shared L2.  Reads are agent-scope (sc1) loads:
+// they miss the CU's L1 and never see a stale line (measured: a completed
+// store from another CU of the XCD is seen within ~0.2 us).
+__device__ __forceinline__ uint64_t epoch_word(float v, unsigned epoch) {
+    return ((uint64_t)epoch << 32) | __builtin_bit_cast(uint32_t, v);
 }
-__device__ __forceinline__ float load_coherent(const float* p) {
-    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+__device__ __forceinline__ void store_word(uint64_t* p, uint64_t w, bool device) {
+    if (device)
+        __hip_atomic_store(p, w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    else
+        __hip_atomic_store(p, w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
 }
-__device__ __forceinline__ unsigned bump_counter(unsigned* p) {
-    return __hip_atomic_fetch_add(p, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ void reset_counter(unsigned* p) {
-    __hip_atomic_store(p, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-// Current value of a counter read with an atomic read-modify-write: it is
-// served where the increments are performed, never from a stale cached copy.
-__device__ __forceinline__ unsigned poll_counter(unsigned* p) {
-    return __hip_atomic_fetch_add(p, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-// Poll of a flag another CU of the same XCD stores with a plain store.  The
-// load must miss the CU's L1: an sc0 (workgroup-scope) load, even after
-// "buffer_inv sc0", is served by a stale L1 line until that line is evicted
-// (measured: never within 20 ms on an idle CU), while an agent-scope (sc1)
-// load sees the completed store within ~0.2 us.
-__device__ __forceinline__ unsigned load_flag(const unsigned* p) {
+__device__ __forceinline__ uint64_t load_word(const uint64_t* p) {
     return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
@@ -220,19 +206,16 @@ struct alignas(16) FusedLds {
         } b;
     };
     alignas(16) float part[kMaxPart];  // (row, segment) partials of one phase-B round
-    float hw[kMaxHW];      // h of this workgroup's (expert, row) pairs before they are stored
     ExpertEntry table[kMaxE];
-    alignas(16) uint32_t rkey[kMaxE];  // routing order keys
+    alignas(16) uint64_t rkey[kMaxE];  // routing order keys
     float slot_key[kMaxSlots];
     int slot_id[kMaxSlots];
     const uint8_t* gate[kMaxSlots];
     const uint8_t* up[kMaxSlots];
     const uint8_t* down[kMaxSlots];
     float w[kMaxSlots];
-    unsigned a_issued;  // A waves whose first passes are issued (the down copies go out after them)
-    unsigned b_landed;  // B waves whose down copies have landed
-    unsigned a_done;    // A waves whose h stores have completed
-    int flag;
+    unsigned a_issued;  // A waves whose passes are all issued (the down copies go out after them)
+    unsigned b_landed;  // B waves whose round-0 down copies have landed
 };
 
 // Activation levels.  n fp32 values (n % 64 == 0) become 3 int8 levels per
@@ -242,22 +225,44 @@ struct alignas(16) FusedLds {
 // eight values each.
 
 // This thread's eight values of segment seg (zeros when inactive).
-template <bool COHERENT>
 __device__ __forceinline__ void load8(const float* src, int seg, int part, bool active, float (&v)[8]) {
     if (active) {
         const float* sp = src + seg * 64 + part * 8;
-        if (COHERENT) {
-#pragma unroll
-            for (int i = 0; i < 8; i++) v[i] = __hip_atomic_load(sp + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        } else {
-            const float4 v0 = reinterpret_cast<const float4*>(sp)[0], v1 = reinterpret_cast<const float4*>(sp)[1];
-            v[0] = v0.x; v[1] = v0.y; v[2] = v0.z; v[3] = v0.w;
-            v[4] = v1.x; v[5] = v1.y; v[6] = v1.z; v[7] = v1.w;
-        }
+        const float4 v0 = reinterpret_cast<const float4*>(sp)[0], v1 = reinterpret_cast<const float4*>(sp)[1];
+        v[0] = v0.x; v[1] = v0.y; v[2] = v0.z; v[3] = v0.w;
+        v[4] = v1.x; v[5] = v1.y; v[6] = v1.z; v[7] = v1.w;
     } else {
 #pragma unroll
         for (int i = 0; i < 8; i++) v[i] = 0.f;
     }
+}
+
+// The same from exchange words, polled until all eight carry this launch's
+// epoch (bounded: on a timeout the error flag is raised and the values are
+// used as they are).
+__device__ __forceinline__ void load8_words(const uint64_t* src, int seg, int part, bool active, unsigned epoch,
+                                            unsigned* sync, float (&v)[8]) {
+    uint64_t w[8];
+#pragma unroll
+    for (int i = 0; i < 8; i++) w[i] = 0;
+    if (active) {
+        const uint64_t* sp = src + seg * 64 + part * 8;
+        for (unsigned spins = 0;; spins++) {
+#pragma unroll
+            for (int i = 0; i < 8; i++) w[i] = load_word(sp + i);
+            bool ok = true;
+#pragma unroll
+            for (int i = 0; i < 8; i++) ok &= (unsigned)(w[i] >> 32) == epoch;
+            if (ok) break;
+            if (spins == kSpinLimit) {
+                raise_error(sync, 1u);
+                break;
+            }
+            __builtin_amdgcn_s_sleep(1);
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < 8; i++) v[i] = __builtin_bit_cast(float, (uint32_t)w[i]);
 }
 
 // Levels of the eight values v of segment seg; every lane of the wave calls it
@@ -304,15 +309,15 @@ __device__ __forceinline__ void quantize8(const float (&v)[8], int seg, int part
     if ((part & 3) == 0) s32[seg * 2 + part / 4] = sum;
 }
 
-// All n values by threads t in [0, nthr) (nthr a multiple of 64).
-template <bool COHERENT>
-__device__ void quantize_levels(const float* src, int n, int8_t* q, int qstride, float* sc, int scstride, float* s32,
-                                int t, int nthr) {
+// Levels of n values held as exchange words, by threads t in [0, nthr) (nthr
+// a multiple of 64).
+__device__ void quantize_words(const uint64_t* src, int n, unsigned epoch, unsigned* sync, int8_t* q, int qstride,
+                               float* sc, int scstride, float* s32, int t, int nthr) {
     const int nseg = n / 64;
     for (int base = 0; base < nseg; base += nthr / 8) {
         const int seg = base + t / 8, part = t % 8;
         float v[8];
-        load8<COHERENT>(src, seg, part, seg < nseg, v);
+        load8_words(src, seg, part, seg < nseg, epoch, sync, v);
         quantize8(v, seg, part, seg < nseg, q, qstride, sc, scstride, s32);
     }
 }
@@ -336,9 +341,10 @@ __device__ __forceinline__ void load_xseg(XSeg& xs, const int8_t* q, int qstride
 }
 
 // Routing, step 1 (wave 0): the expert table into LDS and every candidate's
-// order key: e_i = expf(l_i - max) as the reference forms it, stored as its
-// bits + 1 (non-negative floats order as their bits); 0 for a NaN e_i and for
-// ids past n_expert up to 256, which then never rank ahead of a real one.
+// order key.  e_i = expf(l_i - max) as the reference forms it; the key holds
+// e_i's bits + 1 in the high word (non-negative floats order as their bits;
+// 0 for a NaN e_i and for ids past n_expert up to 256) and ~i in the low
+// word, so keys are distinct and order exactly as (e desc, id asc).
 __device__ void route_keys(const FusedArgs& a, FusedLds& L, int lane) {
     const int n = a.n_expert;
     // every global load of this step goes out before the first use
@@ -356,40 +362,71 @@ __device__ void route_keys(const FusedArgs& a, FusedLds& L, int lane) {
     for (int c = 0; c < 4; c++) {
         const int id = lane + 64 * c;
         const float e = expf(l[c] - mx);
-        L.rkey[id] = (id < n && e == e) ? __builtin_bit_cast(uint32_t, e) + 1u : 0u;
+        const uint32_t hi = (id < n && e == e) ? __builtin_bit_cast(uint32_t, e) + 1u : 0u;
+        L.rkey[id] = ((uint64_t)hi << 32) | (uint32_t)~id;
         if (id < n) L.table[id] = ent[c];
     }
 }
 
-// Routing, step 2 (all threads): candidate i's rank in (e desc, id asc), the
-// reference's order (qwen3moe.cpp:1016), is the number of candidates ahead of
-// it: larger key, or equal key and lower id.  T = 2^rank_shift adjacent
-// threads count over C = rank_c consecutive keys each (read four at a time).
-// Ranks are distinct, so the top k fill slots 0..k-1 without collisions.
+// acc + (key (hi, lo) > ki) for 64-bit keys, as the borrow out of ki - key:
+// three full-rate VALU instructions (a 64-bit compare is not full rate).
+__device__ __forceinline__ int add_if_greater(int acc, uint32_t lo, uint32_t hi, uint64_t ki) {
+    int r;
+    uint32_t t;
+    asm("v_sub_co_u32 %1, vcc, %2, %3\n\t"
+        "v_subb_co_u32 %1, vcc, %4, %5, vcc\n\t"
+        "v_addc_co_u32 %0, vcc, 0, %6, vcc"
+        : "=v"(r), "=&v"(t)
+        : "v"((uint32_t)ki), "v"(lo), "v"((uint32_t)(ki >> 32)), "v"(hi), "v"(acc)
+        : "vcc");
+    return r;
+}
+
+// Routing, step 2 (all threads): candidate i's rank in the reference's order
+// (qwen3moe.cpp:1016) is the number of larger keys.  T = 2^rank_shift
+// adjacent threads count over C = rank_c keys each: thread part reads the key
+// pairs 2 part + 2 T j (C even), so the T threads of a candidate read
+// adjacent banks and the wave's candidates share those reads (broadcast).
+// Ranks are distinct, so the top k fill slots 0..k-1.
 __device__ void route_rank(const FusedArgs& a, FusedLds& L, int tid) {
     const int n = a.n_expert, C = a.rank_c;
     const int i = tid >> a.rank_shift, part = tid & ((1 << a.rank_shift) - 1);
     int ahead = 0;
-    uint32_t ki = 0;
+    uint64_t ki = 0;
     if (i < n) {
         ki = L.rkey[i];
-        const int j0 = part * C;
-        if (C >= 4) {
-            for (int jb = 0; jb < C; jb += 4) {
-                const uint4 v = *reinterpret_cast<const uint4*>(&L.rkey[j0 + jb]);
-                const uint32_t kv[4] = {v.x, v.y, v.z, v.w};
+        const int T = 1 << a.rank_shift;
+        if ((C & 1) == 0) {
+            const uint64_t* kp = &L.rkey[2 * part];
+            const int P = C / 2;
+            int j = 0;
+            for (; j + 8 <= P; j += 8) {  // eight reads in flight before the first use
+                uint4 v[8];
 #pragma unroll
-                for (int c = 0; c < 4; c++) ahead += (kv[c] > ki) | ((kv[c] == ki) & (j0 + jb + c < i));
+                for (int u = 0; u < 8; u++) v[u] = *reinterpret_cast<const uint4*>(kp + 2 * T * (j + u));
+#pragma unroll
+                for (int u = 0; u < 8; u++) {
+                    ahead = add_if_greater(ahead, v[u].x, v[u].y, ki);
+                    ahead = add_if_greater(ahead, v[u].z, v[u].w, ki);
+                }
+            }
+            for (; j < P; j++) {
+                const uint4 v = *reinterpret_cast<const uint4*>(kp + 2 * T * j);
+                ahead = add_if_greater(ahead, v.x, v.y, ki);
+                ahead = add_if_greater(ahead, v.z, v.w, ki);
             }
         } else {
-            for (int j = j0; j < j0 + C; j++) ahead += (L.rkey[j] > ki) | ((L.rkey[j] == ki) & (j < i));
+            for (int j = 0; j < C; j++) {
+                const uint64_t kj = L.rkey[part + T * j];
+                ahead = add_if_greater(ahead, (uint32_t)kj, (uint32_t)(kj >> 32), ki);
+            }
         }
     }
     for (int off = (1 << a.rank_shift) / 2; off > 0; off >>= 1) ahead += __shfl_xor(ahead, off, 64);
     if (i < n && part == 0 && ahead < a.k) {
-        const bool valid = ki != 0u;
-        L.slot_key[ahead] = valid ? __builtin_bit_cast(float, ki - 1u) : -1.0f;
-        L.slot_id[ahead] = valid ? i : -1;
+        const uint32_t hi = (uint32_t)(ki >> 32);
+        L.slot_key[ahead] = hi != 0u ? __builtin_bit_cast(float, hi - 1u) : -1.0f;
+        L.slot_id[ahead] = hi != 0u ? i : -1;
     }
 }
 
@@ -424,70 +461,95 @@ __device__ __forceinline__ const uint8_t* slot_ptr(const FusedArgs& a, const Fus
     return c == 0 ? L.gate[j] : (c == 1 ? L.up[j] : L.down[j]);
 }
 
-// ypart[0][r] + ... + ypart[np-1][r] (np <= 8) in partition order, all
-// loads issued before the first add.
-__device__ __forceinline__ float sum_partials(const float* ypart, int D, int r, int np) {
-    float v[8];
+// ypart[0][r] + ... + ypart[np-1][r] (np <= 8) in partition order, once
+// every partial carries this launch's epoch (all loads of a poll in flight
+// together; bounded like every wait).
+__device__ __forceinline__ float reduce_row(const uint64_t* ypart, int D, int r, int np, unsigned epoch,
+                                            unsigned* sync) {
+    uint64_t v[8];
+    for (unsigned spins = 0;; spins++) {
 #pragma unroll
-    for (int pp = 0; pp < 8; pp++) v[pp] = pp < np ? load_coherent(&ypart[pp * D + r]) : 0.f;
+        for (int pp = 0; pp < 8; pp++) v[pp] = pp < np ? load_word(&ypart[pp * D + r]) : ((uint64_t)epoch << 32);
+        bool ok = true;
+#pragma unroll
+        for (int pp = 0; pp < 8; pp++) ok &= (unsigned)(v[pp] >> 32) == epoch;
+        if (ok) break;
+        if (spins == kSpinLimit) {
+            raise_error(sync, 1u);
+            break;
+        }
+        __builtin_amdgcn_s_sleep(1);
+    }
     float t = 0.f;
 #pragma unroll
     for (int pp = 0; pp < 8; pp++)
-        if (pp < np) t += v[pp];
+        if (pp < np) t += __builtin_bit_cast(float, (uint32_t)v[pp]);
     return t;
 }
 
-// vmcnt(n * NI) for a run-time n in [0, 2].
-template <int NI>
+// vmcnt(n * NI + EXTRA) for a run-time n in [0, 2].
+template <int NI, int EXTRA>
 __device__ __forceinline__ void wait_passes(int n) {
-    if (n <= 0) wait_vm_upto<0>();
-    else if (n == 1) wait_vm_upto<NI>();
-    else wait_vm_upto<2 * NI>();
+    if (n <= 0) wait_vm_upto<EXTRA>();
+    else if (n == 1) wait_vm_upto<NI + EXTRA>();
+    else wait_vm_upto<2 * NI + EXTRA>();
 }
 
-// Geometry of A pass pp of wave w: GW consecutive (expert, row) pairs from
-// t0; nr of them are real rows of expert slot j starting at row f0.
+// Geometry of A pass pp of a wave: GW consecutive (expert, row) pairs from
+// t0; nr of them are real rows of partition expert e starting at row f0; g
+// and u are where the gate and up copies start.
 struct PassRows {
-    int t0, nr, j, f0;
+    int t0, nr, e, f0;
     bool ok;
     const uint8_t* g;
     const uint8_t* u;
 };
 
+// LDS flag or counter of the workgroup reaching v (acquire; bounded: the
+// waves it waits for always progress).
+__device__ __forceinline__ void wait_lds(const unsigned* c, unsigned v) {
+    for (unsigned spins = 0; spins < (1u << 20); spins++) {
+        if (__hip_atomic_load(c, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) >= v) break;
+        __builtin_amdgcn_s_sleep(1);
+    }
+}
+
 template <int LA, int GT, int UT, int DT>
 __device__ void fused_body(const FusedArgs& a, FusedLds& L) {
-    constexpr int GA = kAThreads / LA;  // A lane groups
-    constexpr int GW = 64 / LA;         // A lane groups per wave = rows per pass
+    constexpr int GW = 64 / LA;        // lane groups per wave = rows per pass
+    constexpr int GA = kAWaves * GW;   // rows per pass of the four A waves
+    static_assert(GT == UT, "gate and up share a format");
     using PA = PassA<GT>;
-    static_assert(PassA<UT>::nir == PA::nir, "gate and up share a format");
     constexpr int NPA = PA::n;
     const int tid = threadIdx.x;
     const int wave = __builtin_amdgcn_readfirstlane(tid / 64), lane = tid % 64;
     const MoeShape& s = a.s;
     const int D = s.D, FF = s.FF, k = a.k;
-    const int np = a.np, m = a.m;
+    const int np = a.np;
     const int xcc = a.local_l2 ? xcc_id() : 0;
     const bool xcc_bad = xcc >= np;  // never on a device that passed the host's placement check
     const int p = a.local_l2 ? (xcc_bad ? 0 : xcc) : (int)blockIdx.x % np, q = blockIdx.x / np;
-    const int ep = k / np;  // experts per partition
+    const int ep = k / np;  // experts per partition (1 or 2)
     const int segB = FF / 64;
     const int drb = (int)s.down_rb;
+    const bool device_words = !a.local_l2;  // h words are read in other XCDs
     // output rows of this workgroup's chunk (the host gives every workgroup at least one)
     const int r_begin = q * a.rows_b;
     const int r_end = min(D, r_begin + a.rows_b);
 
-    // ---- 1. routing / slots and activation levels (one barrier)
-    // this thread's eight values of x (at most one segment part per thread),
-    // loaded first so that their latency overlaps the routing's
-    static_assert(kMaxD / 64 * 8 <= kThreads, "one x segment part per thread");
-    const int xseg = tid / 8, xpart = tid % 8;
+    // ---- 1. routing / slots and activation levels
+    // x in parts of eight values, loaded first so that their latency overlaps
+    // the routing's; with routing, threads 64.. take the parts (two rounds
+    // for D > 3584) while wave 0 forms the keys
+    static_assert(kMaxD / 8 <= 2 * (kThreads - 64), "two rounds of x parts");
+    const int xt0 = a.mode == 1 ? 64 : 0, xnt = kThreads - xt0, nxp = D / 8;
+    const int xp = tid - xt0;
     float xv[8];
-    load8<false>(a.x, xseg, xpart, xseg < D / 64, xv);
+    load8(a.x, xp / 8, xp % 8, xp >= 0 && xp < nxp, xv);
     if (wave == 0) {
         if (lane == 0) {
-            L.a_issued = 0;
-            L.b_landed = 0;
-            L.a_done = 0;
+            L.a_issued = 0u;
+            L.b_landed = 0u;
         }
         if (a.mode == 1) {
             // ranks are a permutation of 0..n_expert-1, so the routing
@@ -513,41 +575,66 @@ __device__ void fused_body(const FusedArgs& a, FusedLds& L) {
             }
         }
     }
-    // wave 0 forms the routing keys while waves 1-7 turn x into levels
-    // (wave 0's own segments follow its keys); all threads then rank
     if (wave == 0 && a.mode == 1) route_keys(a, L, lane);
-    quantize8(xv, xseg, xpart, xseg < D / 64, &L.a.xq[0][0], kMaxD, &L.a.xsc[0][0], kMaxD / 64, L.a.xs32);
+    if (xp >= 0) {  // wave-uniform
+        quantize8(xv, xp / 8, xp % 8, xp < nxp, &L.a.xq[0][0], kMaxD, &L.a.xsc[0][0], kMaxD / 64, L.a.xs32);
+        const int xp2 = xp + xnt;
+        if (wave * 64 - xt0 + xnt < nxp) {  // wave-uniform: this wave has parts in the second round
+            float xv2[8];
+            load8(a.x, xp2 / 8, xp2 % 8, xp2 < nxp, xv2);
+            quantize8(xv2, xp2 / 8, xp2 % 8, xp2 < nxp, &L.a.xq[0][0], kMaxD, &L.a.xsc[0][0], kMaxD / 64, L.a.xs32);
+        }
+    }
     __syncthreads();
     if (a.mode == 1) {
         route_rank(a, L, tid);
         __syncthreads();
     }
 
+    // weight pointers of the partition's (at most two) experts
+    const uint8_t* gptr[2] = {slot_ptr(a, L, p * ep, 0), ep > 1 ? slot_ptr(a, L, p * ep + 1, 0) : nullptr};
+    const uint8_t* uptr[2] = {slot_ptr(a, L, p * ep, 1), ep > 1 ? slot_ptr(a, L, p * ep + 1, 1) : nullptr};
+    const uint8_t* dptr[2] = {slot_ptr(a, L, p * ep, 2), ep > 1 ? slot_ptr(a, L, p * ep + 1, 2) : nullptr};
+
     // phase-B stage: rows [r0, r0 + rr) of the chunk, expert e of the
     // partition at stage_b + e * stride_b + (its source & 15)
     auto down_src = [&](int e, int r0) -> const uint8_t* {
-        const uint8_t* dw = slot_ptr(a, L, p * ep + e, 2);
+        const uint8_t* dw = dptr[e];
         return dw ? dw + (size_t)(r_begin + r0) * drb : reinterpret_cast<const uint8_t*>(a.x);
     };
-    // B waves copy the round's rows, one 1 KB instruction each in turn
-    auto stage_round = [&](int r0, int rr, int wave_b, int nwaves_b) {
+    // global source of 1 KB stage instruction ii of expert e (lanes past the
+    // end re-read the last 16 bytes)
+    auto stage_src = [&](int e, int ii, int r0, int rr) -> uintptr_t {
+        const uint8_t* src = down_src(e, r0);
+        const int n = dptr[e] ? rr * drb : 16;
+        const uintptr_t base = (uintptr_t)src & ~(uintptr_t)15;
+        const int n16 = (int)(((((uintptr_t)src + (uintptr_t)n + 15) & ~(uintptr_t)15) - base) / 16);
+        return base + (uintptr_t)min(ii * 64 + lane, n16 - 1) * 16;
+    };
+    // rounds after the first: all waves copy, one 1 KB instruction each in turn
+    auto stage_round = [&](int r0, int rr) {
         const int ni = a.stride_b / 1024;
-        for (int e = 0; e < ep; e++) {
-            const uint8_t* src = down_src(e, r0);
-            const int n = slot_ptr(a, L, p * ep + e, 2) ? rr * drb : 16;
-            const uintptr_t base = (uintptr_t)src & ~(uintptr_t)15;
-            const int n16 = (int)(((((uintptr_t)src + (uintptr_t)n + 15) & ~(uintptr_t)15) - base) / 16);
-            for (int i = wave_b; i < ni; i += nwaves_b) {
-                const int c = min(i * 64 + lane, n16 - 1);
-                lds_dma16(base + (uintptr_t)c * 16, L.stage_b + e * a.stride_b + i * 1024);
-            }
+        for (int e = 0; e < ep; e++)
+            for (int i = wave; i < ni; i += kWaves) lds_dma16(stage_src(e, i, r0, rr), L.stage_b + e * a.stride_b + i * 1024);
+    };
+    // round 0, B wave wb: exactly kDmaB instructions f = wb + 4i over the
+    // experts' stage instructions in order (expert e's instruction ii lands at
+    // stage_b + f KB); indices past the last real one copy 16 bytes of x into
+    // the unused tail of the stage
+    const int rr0 = min(a.rows_round, r_end - r_begin);
+    auto stage_round0 = [&](int wb) {
+        const int ni = a.stride_b / 1024;
+        for (int i = 0; i < kDmaB; i++) {
+            const int f = wb + (kWaves - kAWaves) * i;
+            const int e = f / ni;
+            const uintptr_t g = e < ep ? stage_src(e, f - e * ni, 0, rr0) : ((uintptr_t)a.x & ~(uintptr_t)15);
+            lds_dma16(g, L.stage_b + f * 1024);
         }
     };
 
     // Phase-B tasks of a round: (expert e of the partition, 64-value segment
-    // sg, 64-row block); a lane is one row.  The B waves decode the first NPD
-    // tasks each of round 0 into registers before the barrier.
-    const int rr0 = min(a.rows_round, r_end - r_begin);
+    // sg, 64-row block); a lane is one row.  Every wave decodes its first NPD
+    // tasks of round 0 into registers before the barrier.
     const int nrb0 = (rr0 + 63) / 64;
     const int n_tasks0 = ep * segB * nrb0;
     struct BTask {
@@ -565,152 +652,100 @@ __device__ void fused_body(const FusedArgs& a, FusedLds& L) {
         t.row = L.stage_b + t.e * a.stride_b + ((uintptr_t)src & 15) + min(t.r, rr - 1) * drb;
         return t;
     };
-    SegCodes<DT> pre[NPD];
 
-    // ---- 2. gate/up passes.  A pass of A wave w is GW consecutive (expert,
-    // row) pairs; w DMAs its passes into its own LDS ring and dots them.
+    // ---- 2. passes.  Pass pp of A wave w: GW consecutive (expert, row)
+    // pairs from t0 = ra0 + pp * GA + w * GW, gate and up rows both
     const int gl = lane / LA, li = lane % LA;
     const int rows_a = ep * FF;
     const int ra0 = min(rows_a, q * a.rows_a), ra1 = min(rows_a, ra0 + a.rows_a);
     const int npass = (ra1 - ra0 + GA - 1) / GA;
+    const int grb = (int)s.gate_rb, urb = (int)s.up_rb;
     auto rows_of = [&](int pp) {
         PassRows r;
         r.t0 = ra0 + pp * GA + wave * GW;
         r.nr = max(0, min(GW, ra1 - r.t0));
         const int tt = min(r.t0, rows_a - 1);
-        r.j = p * ep + tt / FF;
-        r.f0 = tt - (tt / FF) * FF;
-        const uint8_t* gw = slot_ptr(a, L, r.j, 0);
-        const uint8_t* uw = slot_ptr(a, L, r.j, 1);
+        r.e = tt >= FF ? 1 : 0;
+        r.f0 = tt - r.e * FF;
+        const uint8_t* gw = gptr[r.e];
+        const uint8_t* uw = uptr[r.e];
         r.ok = (r.nr > 0) & (gw != nullptr) & (uw != nullptr);
         // a pass without weights copies 16 bytes of x instead; nothing of it is used
-        r.g = r.ok ? gw + (size_t)r.f0 * s.gate_rb : reinterpret_cast<const uint8_t*>(a.x);
-        r.u = r.ok ? uw + (size_t)r.f0 * s.up_rb : reinterpret_cast<const uint8_t*>(a.x);
+        r.g = r.ok ? gw + (size_t)r.f0 * grb : reinterpret_cast<const uint8_t*>(a.x);
+        r.u = r.ok ? uw + (size_t)r.f0 * urb : reinterpret_cast<const uint8_t*>(a.x);
         return r;
-    };
-    auto wait_lds_count = [&](const unsigned* c, unsigned v) {  // bounded: the other waves always progress
-        for (unsigned spins = 0; spins < (1u << 20); spins++) {
-            if (__hip_atomic_load(c, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) >= v) break;
-            __builtin_amdgcn_s_sleep(1);
-        }
     };
 
     if (wave < kAWaves) {
-        // ---- 2A. this wave's passes through its LDS ring
+        // ---- 2A. this wave's passes through its LDS ring.  Every load the
+        // compiler issued is retired first: the copies below are invisible to
+        // it, and a wait it inserts later for one of its own loads (for
+        // instance before reusing the load's register) would also wait for
+        // every copy in flight.
+        wait_vm();
+        auto slot_of = [&](int pp) { return L.stage_a[wave] + (pp % NPA) * PA::slot; };
         auto issue = [&](int pp) {
             const PassRows r = rows_of(pp);
-            uint8_t* sl = L.stage_a[wave] + (pp % NPA) * PA::slot;
-            dma_to_lds<PA::nir>(r.g, r.ok ? r.nr * (int)s.gate_rb : 16, sl, lane);
-            dma_to_lds<PA::nir>(r.u, r.ok ? r.nr * (int)s.up_rb : 16, sl + PA::nir * 1024, lane);
+            uint8_t* sl = slot_of(pp);
+            dma_to_lds<PA::nir>(r.g, r.ok ? r.nr * grb : 16, sl, lane);
+            dma_to_lds<PA::nir>(r.u, r.ok ? r.nr * urb : 16, sl + PA::nir * 1024, lane);
         };
         for (int pp = 0; pp < min(NPA, npass); pp++) issue(pp);
-        if (lane == 0) atomicAdd(&L.a_issued, 1u);
+        // the B waves copy the down rows once every pass of every A wave is issued
+        const int plast = max(-1, npass - 1 - NPA);  // iteration that issues the last pass (-1: none)
+        if (plast < 0 && lane == 0) __hip_atomic_fetch_add(&L.a_issued, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
         XSeg xs;  // read while the first pass is in flight
         load_xseg(xs, &L.a.xq[0][0], kMaxD, &L.a.xsc[0][0], kMaxD / 64, L.a.xs32, li);
+        const int goff = gl * grb, uoff = PA::nir * 1024 + gl * urb;
         for (int pp = 0; pp < npass; pp++) {
             // passes pp+1 .. are still allowed in flight: 2 * nir instructions each
-            wait_passes<2 * PA::nir>(min(npass - 1 - pp, NPA - 1));
+            wait_passes<2 * PA::nir, 0>(min(npass - 1 - pp, NPA - 1));
             const PassRows r = rows_of(pp);
-            const uint8_t* sl = L.stage_a[wave] + (pp % NPA) * PA::slot;
-            const uint8_t* grow = sl + ((uintptr_t)r.g & 15) + gl * s.gate_rb;
-            const uint8_t* urow = sl + PA::nir * 1024 + ((uintptr_t)r.u & 15) + gl * s.up_rb;
+            const uint8_t* sl = slot_of(pp);
+            const bool live = r.ok && gl < r.nr;
             RawSeg<GT> g;
             RawSeg<UT> u;
-            g.template load<LdsLd>(r.ok && gl < r.nr ? grow : sl, li);
-            u.template load<LdsLd>(r.ok && gl < r.nr ? urow : sl, li);
+            g.template load<LdsLd>(live ? sl + ((uintptr_t)r.g & 15) + goff : sl, li);
+            u.template load<LdsLd>(live ? sl + ((uintptr_t)r.u & 15) + uoff : sl, li);
             const float dg = group_sum<LA>(g.dot_q8(li, xs));
             const float du = group_sum<LA>(u.dot_q8(li, xs));
-            if (li == LA - 1 && gl < r.nr) L.hw[r.t0 + gl - ra0] = dg / (1.0f + expf(-dg)) * du;
+            // every pair of the workgroup gets a word, 0 for a slot without an expert
+            if (li == LA - 1 && gl < r.nr) {
+                const float hv = r.ok ? dg / (1.0f + expf(-dg)) * du : 0.f;
+                store_word(&a.hx[(p * ep + r.e) * FF + r.f0 + gl], epoch_word(hv, a.epoch), device_words);
+            }
             // every lane's reads of this slot have returned (their values are used above)
             if (pp + NPA < npass) issue(pp + NPA);
-        }
-        // ---- 3. h stores, then the workgroup's arrival
-        for (int e = lane; e < npass * GW; e += 64) {
-            const int pp = e / GW, g2 = e % GW;
-            const PassRows r = rows_of(pp);
-            if (r.ok && g2 < r.nr) {
-                const float hv = L.hw[r.t0 + g2 - ra0];
-                float* dst = &a.h[r.j * FF + r.f0 + g2];
-                if (a.local_l2)  // the partition's readers share this XCD's L2
-                    *dst = hv;
-                else
-                    store_coherent(dst, hv);
-            }
-        }
-        wait_vm();
-        if (lane == 0) {
-            const unsigned before = atomicAdd(&L.a_done, 1u);
-            if (before == kAWaves - 1) {
-                if (a.local_l2) {
-                    if (xcc_bad)  // the XCD-to-partition mapping this exchange relies on does not hold
-                        raise_error(a.sync, 2u);
-                    a.sync[kFlagArrive + p * kMaxM + q] = a.epoch;
-                } else {
-                    bump_counter(&a.sync[kSyncArrive + p]);
-                }
-            }
-        }
-        if (wave == 0) {
-            if (a.local_l2) {
-                unsigned spins = 0;
-                for (;;) {
-                    const unsigned* fl = &a.sync[kFlagArrive + p * kMaxM];
-                    const bool mine = (lane >= m || load_flag(fl + lane) == a.epoch) &&
-                                      (lane + 64 >= m || load_flag(fl + lane + 64) == a.epoch);
-                    if (__all(mine)) break;
-                    __builtin_amdgcn_s_sleep(1);
-                    if (++spins == kSpinLimit) {
-                        if (lane == 0) raise_error(a.sync, 1u);
-                        break;
-                    }
-                }
-            } else if (lane == 0) {
-                unsigned spins = 0;
-                while (poll_counter(&a.sync[kSyncArrive + p]) < (unsigned)m) {
-                    __builtin_amdgcn_s_sleep(2);
-                    if (++spins == kSpinLimit) {
-                        raise_error(a.sync, 1u);
-                        break;
-                    }
-                }
-                if (bump_counter(&a.sync[kSyncPass + p]) == (unsigned)m - 1) {  // everyone has passed: reset
-                    reset_counter(&a.sync[kSyncArrive + p]);
-                    reset_counter(&a.sync[kSyncPass + p]);
-                }
-            }
+            if (pp == plast && lane == 0)
+                __hip_atomic_fetch_add(&L.a_issued, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
         }
     } else {
-        // ---- 2B. the first round of down rows into LDS, queued behind the
-        // A waves' first passes (the CU serves its copies in issue order, and
-        // h, the barrier and everything after it wait on gate/up first); once
-        // they land, this wave decodes its first NPD phase-B tasks into
-        // registers, so that after the barrier only their dot with h remains
-        wait_lds_count(&L.a_issued, (unsigned)kAWaves);
-        stage_round(0, rr0, wave - kAWaves, kWaves - kAWaves);
+        // ---- 2B. the round-0 down rows into LDS, queued behind the A waves'
+        // passes (h, the barrier and everything after it wait on gate/up first)
+        wait_lds(&L.a_issued, (unsigned)kAWaves);
+        stage_round0(wave - kAWaves);
         if (a.mode == 1 && wave == kAWaves) route_weights(a, L, lane);
         wait_vm();
-        if (lane == 0) atomicAdd(&L.b_landed, 1u);
-        wait_lds_count(&L.b_landed, (unsigned)(kWaves - kAWaves));
+        if (lane == 0) __hip_atomic_fetch_add(&L.b_landed, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+    }
+
+    // ---- 3. every wave decodes its first NPD phase-B tasks once the down
+    // rows have landed
+    wait_lds(&L.b_landed, (unsigned)(kWaves - kAWaves));
+    SegCodes<DT> pre[NPD];
 #pragma unroll
-        for (int i = 0; i < NPD; i++) {
-            const int task = (wave - kAWaves) + (kWaves - kAWaves) * i;
-            const BTask t = btask(min(task, n_tasks0 - 1), rr0, 0);
-            RawSeg<DT> raw;
-            raw.template load<LdsLd>(t.row, t.sg);
-            pre[i] = raw.decode(t.sg);
-        }
+    for (int i = 0; i < NPD; i++) {
+        const BTask t = btask(min(wave + kWaves * i, n_tasks0 - 1), rr0, 0);
+        RawSeg<DT> raw;
+        raw.template load<LdsLd>(t.row, t.sg);
+        pre[i] = raw.decode(t.sg);
+        pre[i].pin_all();  // decoded here, not after the barrier
     }
     __syncthreads();  // the activation levels are dead from here: the LDS union switches to h
 
-    // ---- 4. the partition's h as int8 levels (from this XCD's L2 when the
-    // partition shares an XCD, with device-coherent loads otherwise)
-    const int hn = ep * FF;
-    if (a.local_l2)
-        quantize_levels<false>(a.h + p * ep * FF, hn, &L.b.hq[0][0], kMaxHP, &L.b.hsc[0][0], kMaxHP / 64, L.b.hs32,
-                               tid, kThreads);
-    else
-        quantize_levels<true>(a.h + p * ep * FF, hn, &L.b.hq[0][0], kMaxHP, &L.b.hsc[0][0], kMaxHP / 64, L.b.hs32,
-                              tid, kThreads);
+    // ---- 4. the partition's h as int8 levels, once every word is current
+    quantize_words(a.hx + p * ep * FF, ep * FF, a.epoch, a.sync, &L.b.hq[0][0], kMaxHP, &L.b.hsc[0][0], kMaxHP / 64,
+                   L.b.hs32, tid, kThreads);
     __syncthreads();
 
     // Phase B rounds: every wave takes (expert, segment, 64-row block) tasks;
@@ -720,7 +755,7 @@ __device__ void fused_body(const FusedArgs& a, FusedLds& L) {
         const int rr = min(a.rows_round, r_end - r_begin - r0);
         if (r0 > 0) {
             __syncthreads();  // the previous round's rows and partials are consumed
-            stage_round(r0, rr, wave, kWaves);
+            stage_round(r0, rr);
             wait_vm();
             __syncthreads();
         }
@@ -728,20 +763,16 @@ __device__ void fused_body(const FusedArgs& a, FusedLds& L) {
             XSeg hs;  // the same address in every lane: one LDS broadcast per read
             load_xseg(hs, &L.b.hq[0][0], kMaxHP, &L.b.hsc[0][0], kMaxHP / 64, L.b.hs32, t.e * segB + t.sg);
             const float v = k.dot(hs);
-            if (t.r < rr)
-                L.part[(t.e * rr + t.r) * segB + t.sg] = slot_ptr(a, L, p * ep + t.e, 2) ? L.w[p * ep + t.e] * v : 0.f;
+            if (t.r < rr) L.part[(t.e * rr + t.r) * segB + t.sg] = dptr[t.e] ? L.w[p * ep + t.e] * v : 0.f;
         };
         int first = 0;
         if (r0 == 0) {
-            // the decoded tasks (B waves), then the rest from LDS
-            if (wave >= kAWaves) {
 #pragma unroll
-                for (int i = 0; i < NPD; i++) {
-                    const int task = (wave - kAWaves) + (kWaves - kAWaves) * i;
-                    if (task < n_tasks0) finish(btask(task, rr, r0), pre[i]);
-                }
+            for (int i = 0; i < NPD; i++) {
+                const int task = wave + kWaves * i;
+                if (task < n_tasks0) finish(btask(task, rr, r0), pre[i]);
             }
-            first = (kWaves - kAWaves) * NPD;
+            first = kWaves * NPD;
         }
         for (int task = first + wave; task < ep * segB * ((rr + 63) / 64); task += kWaves) {
             const BTask t = btask(task, rr, r0);
@@ -768,47 +799,13 @@ __device__ void fused_body(const FusedArgs& a, FusedLds& L) {
                     for (int u = 0; u < segB; u++) v += pr[u];
                 }
             }
-            store_coherent(&a.ypart[p * D + r_begin + r0 + r], v);
+            store_word(&a.ypart[p * D + r_begin + r0 + r], epoch_word(v, a.epoch), true);
         }
     }
 
-    // ---- 5. combine the partitions' partials of this row chunk into y
-    wait_vm();
-    __syncthreads();
-    if (a.local_l2) {
-        // partition q % 8 reduces chunk q once all eight partials carry this epoch
-        if (tid == 0)
-            __hip_atomic_store(&a.sync[kFlagChunk + p * kMaxM + q], a.epoch, __ATOMIC_RELAXED,
-                               __HIP_MEMORY_SCOPE_AGENT);
-        if (p == q % np) {
-            if (wave == 0) {
-                unsigned spins = 0;
-                for (;;) {
-                    const bool mine =
-                        lane >= np || __hip_atomic_load(&a.sync[kFlagChunk + lane * kMaxM + q], __ATOMIC_RELAXED,
-                                                        __HIP_MEMORY_SCOPE_AGENT) == a.epoch;
-                    if (__all(mine)) break;
-                    __builtin_amdgcn_s_sleep(1);
-                    if (++spins == kSpinLimit) {
-                        if (lane == 0) raise_error(a.sync, 1u);
-                        break;
-                    }
-                }
-            }
-            __syncthreads();
-            for (int r = r_begin + tid; r < r_end; r += kThreads) a.y[r] = sum_partials(a.ypart, D, r, np);
-        }
-    } else {
-        // the last partition to finish this row chunk writes y
-        if (tid == 0) {
-            const unsigned done = bump_counter(&a.sync[kSyncChunk + q]);  // returns the coherent count
-            L.flag = done == (unsigned)np - 1;
-            if (L.flag) reset_counter(&a.sync[kSyncChunk + q]);
-        }
-        __syncthreads();
-        if (L.flag)
-            for (int r = r_begin + tid; r < r_end; r += kThreads) a.y[r] = sum_partials(a.ypart, D, r, np);
-    }
+    // ---- 5. workgroup q of partition q % np adds chunk q's partials into y
+    if (p == q % np)
+        for (int r = r_begin + tid; r < r_end; r += kThreads) a.y[r] = reduce_row(a.ypart, D, r, np, a.epoch, a.sync);
 }
 
 template <int LA, int GT, int UT, int DT>
@@ -919,7 +916,7 @@ static FusedGrid fused_grid(const MoeShape& s, int k, int capacity) {
 
 // The layout fits the kernel's fixed LDS and flag arrays.
 static bool fused_grid_ok(const MoeShape& s, int k, const FusedGrid& g) {
-    if (g.m <= 0 || g.m > kMaxChunks || g.m > kMaxM) return false;
+    if (g.m <= 0) return false;
     const int ep = k / g.np;
     if (g.rows_a > kMaxHW || g.rows_round <= 0) return false;
     return ep * g.stride_b <= kStageB && ep * g.rows_round * (s.FF / 64) <= kMaxPart;
@@ -991,10 +988,10 @@ hipError_t launch_moe_fused(const FusedArgsHost& h, hipStream_t st) {
     a.w_out = h.w_out;
     a.x = h.x;
     a.y = h.y;
-    a.h = h.h;
+    a.hx = h.hx;
     a.ypart = h.ypart;
     a.sync = h.sync;
-    if (!fused_supported(a.s, a.k, a.mode == 1 ? a.n_expert : 0) || !a.ypart || !a.h || !a.sync || !a.x)
+    if (!fused_supported(a.s, a.k, a.mode == 1 ? a.n_expert : 0) || !a.ypart || !a.hx || !a.sync || !a.x)
         return hipErrorInvalidValue;
     if (a.mode == 1 && (a.n_expert <= 0 || !a.logits || !a.table)) return hipErrorInvalidValue;
     FusedFn fn = pick_fused(a.s);

@@ -33,6 +33,14 @@ struct XSeg {
 
 __device__ __forceinline__ int sdot4(int a, int b, int c) { return __builtin_amdgcn_sdot4(a, b, c, false); }
 
+// Materialise v in a register here: the compiler may not move the arithmetic
+// that produced it past this point (it would otherwise sink a decode done
+// ahead of a barrier to the barrier's far side, where the codes are used).
+template <class T>
+__device__ __forceinline__ void pin(T& v) {
+    asm volatile("" : "+v"(v));
+}
+
 template <int T> struct RawSeg;
 template <int T> struct SegCodes;
 
@@ -43,6 +51,11 @@ struct SegCodesK {
     int32_t c[16];
     int sc0, sc1;
     float d, dm0, dm1;  // d, dmin*m0, dmin*m1
+    __device__ __forceinline__ void pin_all() {
+#pragma unroll
+        for (int i = 0; i < 16; i++) pin(c[i]);
+        pin(sc0); pin(sc1); pin(d); pin(dm0); pin(dm1);
+    }
     __device__ __forceinline__ float dot(const XSeg& x) const {
         float dot = 0.f;
 #pragma unroll
@@ -139,6 +152,13 @@ template <> struct SegCodes<kQ6_K> {
     int32_t c[16];
     int sc[4];  // the four signed 8-bit group scales
     float d4;   // d/4
+    __device__ __forceinline__ void pin_all() {
+#pragma unroll
+        for (int i = 0; i < 16; i++) pin(c[i]);
+#pragma unroll
+        for (int g = 0; g < 4; g++) pin(sc[g]);
+        pin(d4);
+    }
     __device__ __forceinline__ float dot(const XSeg& x) const {
         float dot = 0.f;
 #pragma unroll
@@ -194,6 +214,11 @@ template <> struct RawSeg<kQ6_K> {
 template <> struct SegCodes<kQ8_0> {
     int32_t c[16];  // the two blocks' int8 values
     float d0, d1;
+    __device__ __forceinline__ void pin_all() {
+#pragma unroll
+        for (int i = 0; i < 16; i++) pin(c[i]);
+        pin(d0); pin(d1);
+    }
     __device__ __forceinline__ float dot(const XSeg& x) const {
         float r0 = 0.f, r1 = 0.f;
 #pragma unroll
