@@ -40,15 +40,16 @@
 //      issued, DMA this workgroup's down rows (its output-row chunk of the
 //      partition's experts) into LDS; wave 4 renormalises the routing
 //      weights.
-//   3. once the down rows have landed every wave decodes its first NPD
-//      phase-B tasks into registers.
-//   4. all threads read the partition's h - polling until every word
-//      carries this launch's epoch - and turn it into int8 levels in LDS;
-//      every wave computes w_j * down_j[r].h_j per (row, 64-value segment)
-//      unit from the staged rows, and the units of each row are summed in a
-//      fixed order into this partition's partial ypart[p][r] (value and
-//      epoch again).  Chunks with more rows than the stage holds take
-//      several rounds.
+//   3. once the down rows have landed the B waves decode their first NPD
+//      phase-B tasks each into registers, while the A waves compute; the A
+//      waves, done with their passes, read the partition's h - polling until
+//      every word carries this launch's epoch - and turn it into int8 levels
+//      in LDS.
+//   4. every wave computes w_j * down_j[r].h_j per (row, 64-value segment)
+//      unit (the B waves from their decoded codes, the rest decoded from the
+//      staged rows), and the units of each row are summed in a fixed order
+//      into this partition's partial ypart[p][r] (value and epoch again).
+//      Chunks with more rows than the stage holds take several rounds.
 //   5. workgroup q of partition q % NP polls the NP partials of each row of
 //      chunk q until all carry this epoch and adds them in partition order
 //      (deterministic) into y.
@@ -72,7 +73,7 @@ constexpr int kMaxE = 256;
 constexpr int kMaxHP = 4096;     // values of h held per partition
 constexpr int kMaxPart = 2048;   // (row, segment) partials of one round
 constexpr int kMaxHW = 128;      // (expert, row) pairs one workgroup computes
-constexpr int NPD = 2;           // phase-B tasks each wave decodes before the barrier
+constexpr int NPD = 2;           // phase-B tasks each B wave decodes before the barrier
 constexpr int kSlotA = 20 * 1024;   // LDS ring of one A wave
 constexpr int kStageB = 40 * 1024;  // LDS for one round of down rows
 constexpr int kDmaB = kStageB / 1024 / (kWaves - kAWaves);  // round-0 down copies per B wave
@@ -87,9 +88,7 @@ struct PassA {
     static constexpr int bytes = 4096 * Fmt<T>::bytes / Fmt<T>::blck;
     static constexpr int nir = (bytes + 32 + 1023) / 1024;
     static constexpr int slot = 2 * nir * 1024;
-    // two passes in flight: more data in flight per CU only delays the first
-    // pass (the memory system interleaves every CU's outstanding copies)
-    static constexpr int n = kSlotA / slot < 2 ? kSlotA / slot : 2;
+    static constexpr int n = kSlotA / slot < 3 ? kSlotA / slot : 3;
     static_assert(n >= 1, "an A pass must fit the ring");
 };
 
@@ -214,7 +213,8 @@ struct alignas(16) FusedLds {
     const uint8_t* up[kMaxSlots];
     const uint8_t* down[kMaxSlots];
     float w[kMaxSlots];
-    unsigned a_issued;  // A waves whose passes are all issued (the down copies go out after them)
+    unsigned a_issued;  // A waves whose first passes are issued (the down copies go out after them)
+    unsigned xs_read;   // A waves that have read their activation levels
     unsigned b_landed;  // B waves whose round-0 down copies have landed
 };
 
@@ -549,6 +549,7 @@ __device__ void fused_body(const FusedArgs& a, FusedLds& L) {
     if (wave == 0) {
         if (lane == 0) {
             L.a_issued = 0u;
+            L.xs_read = 0u;
             L.b_landed = 0u;
         }
         if (a.mode == 1) {
@@ -633,8 +634,8 @@ __device__ void fused_body(const FusedArgs& a, FusedLds& L) {
     };
 
     // Phase-B tasks of a round: (expert e of the partition, 64-value segment
-    // sg, 64-row block); a lane is one row.  Every wave decodes its first NPD
-    // tasks of round 0 into registers before the barrier.
+    // sg, 64-row block); a lane is one row.  The B waves decode their first
+    // NPD tasks of round 0 into registers before the barrier.
     const int nrb0 = (rr0 + 63) / 64;
     const int n_tasks0 = ep * segB * nrb0;
     struct BTask {
@@ -676,6 +677,7 @@ __device__ void fused_body(const FusedArgs& a, FusedLds& L) {
         return r;
     };
 
+    SegCodes<DT> pre[NPD];  // B waves: their first phase-B tasks, decoded
     if (wave < kAWaves) {
         // ---- 2A. this wave's passes through its LDS ring.  Every load the
         // compiler issued is retired first: the copies below are invisible to
@@ -691,11 +693,10 @@ __device__ void fused_body(const FusedArgs& a, FusedLds& L) {
             dma_to_lds<PA::nir>(r.u, r.ok ? r.nr * urb : 16, sl + PA::nir * 1024, lane);
         };
         for (int pp = 0; pp < min(NPA, npass); pp++) issue(pp);
-        // the B waves copy the down rows once every pass of every A wave is issued
-        const int plast = max(-1, npass - 1 - NPA);  // iteration that issues the last pass (-1: none)
-        if (plast < 0 && lane == 0) __hip_atomic_fetch_add(&L.a_issued, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        if (lane == 0) __hip_atomic_fetch_add(&L.a_issued, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
         XSeg xs;  // read while the first pass is in flight
         load_xseg(xs, &L.a.xq[0][0], kMaxD, &L.a.xsc[0][0], kMaxD / 64, L.a.xs32, li);
+        if (lane == 0) __hip_atomic_fetch_add(&L.xs_read, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
         const int goff = gl * grb, uoff = PA::nir * 1024 + gl * urb;
         for (int pp = 0; pp < npass; pp++) {
             // passes pp+1 .. are still allowed in flight: 2 * nir instructions each
@@ -716,37 +717,34 @@ __device__ void fused_body(const FusedArgs& a, FusedLds& L) {
             }
             // every lane's reads of this slot have returned (their values are used above)
             if (pp + NPA < npass) issue(pp + NPA);
-            if (pp == plast && lane == 0)
-                __hip_atomic_fetch_add(&L.a_issued, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
         }
+        // ---- 4A. the partition's h as int8 levels, once every word carries
+        // this launch's epoch (it overwrites the activation levels: every A
+        // wave has read its own first)
+        wait_lds(&L.xs_read, (unsigned)kAWaves);
+        quantize_words(a.hx + p * ep * FF, ep * FF, a.epoch, a.sync, &L.b.hq[0][0], kMaxHP, &L.b.hsc[0][0],
+                       kMaxHP / 64, L.b.hs32, tid, kAThreads);
     } else {
         // ---- 2B. the round-0 down rows into LDS, queued behind the A waves'
-        // passes (h, the barrier and everything after it wait on gate/up first)
+        // first passes (h, the barrier and everything after it wait on
+        // gate/up first); once they land, the B waves decode their first NPD
+        // phase-B tasks into registers while the A waves compute
         wait_lds(&L.a_issued, (unsigned)kAWaves);
         stage_round0(wave - kAWaves);
         if (a.mode == 1 && wave == kAWaves) route_weights(a, L, lane);
         wait_vm();
         if (lane == 0) __hip_atomic_fetch_add(&L.b_landed, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
-    }
-
-    // ---- 3. every wave decodes its first NPD phase-B tasks once the down
-    // rows have landed
-    wait_lds(&L.b_landed, (unsigned)(kWaves - kAWaves));
-    SegCodes<DT> pre[NPD];
+        wait_lds(&L.b_landed, (unsigned)(kWaves - kAWaves));
 #pragma unroll
-    for (int i = 0; i < NPD; i++) {
-        const BTask t = btask(min(wave + kWaves * i, n_tasks0 - 1), rr0, 0);
-        RawSeg<DT> raw;
-        raw.template load<LdsLd>(t.row, t.sg);
-        pre[i] = raw.decode(t.sg);
-        pre[i].pin_all();  // decoded here, not after the barrier
+        for (int i = 0; i < NPD; i++) {
+            const BTask t = btask(min(wave - kAWaves + (kWaves - kAWaves) * i, n_tasks0 - 1), rr0, 0);
+            RawSeg<DT> raw;
+            raw.template load<LdsLd>(t.row, t.sg);
+            pre[i] = raw.decode(t.sg);
+            pre[i].pin_all();  // decoded here, not after the barrier
+        }
     }
-    __syncthreads();  // the activation levels are dead from here: the LDS union switches to h
-
-    // ---- 4. the partition's h as int8 levels, once every word is current
-    quantize_words(a.hx + p * ep * FF, ep * FF, a.epoch, a.sync, &L.b.hq[0][0], kMaxHP, &L.b.hsc[0][0], kMaxHP / 64,
-                   L.b.hs32, tid, kThreads);
-    __syncthreads();
+    __syncthreads();  // the h levels and the first phase-B codes are ready
 
     // Phase B rounds: every wave takes (expert, segment, 64-row block) tasks;
     // a lane is one row, so the h levels of the task are read by all lanes at
@@ -767,12 +765,14 @@ __device__ void fused_body(const FusedArgs& a, FusedLds& L) {
         };
         int first = 0;
         if (r0 == 0) {
+            if (wave >= kAWaves) {
 #pragma unroll
-            for (int i = 0; i < NPD; i++) {
-                const int task = wave + kWaves * i;
-                if (task < n_tasks0) finish(btask(task, rr, r0), pre[i]);
+                for (int i = 0; i < NPD; i++) {
+                    const int task = wave - kAWaves + (kWaves - kAWaves) * i;
+                    if (task < n_tasks0) finish(btask(task, rr, r0), pre[i]);
+                }
             }
-            first = kWaves * NPD;
+            first = (kWaves - kAWaves) * NPD;
         }
         for (int task = first + wave; task < ep * segB * ((rr + 63) / 64); task += kWaves) {
             const BTask t = btask(task, rr, r0);

@@ -44,6 +44,28 @@ __device__ __forceinline__ void pin(T& v) {
 template <int T> struct RawSeg;
 template <int T> struct SegCodes;
 
+// fp16 bits -> float by the hardware conversion.  Segment codes only feed dot
+// products, where a NaN scale gives a NaN whatever its payload.
+__device__ __forceinline__ float h2f(uint32_t h16) { return (float)__builtin_bit_cast(_Float16, (uint16_t)h16); }
+
+// 6-bit scales and mins of sub-blocks j0 and j0 + 1 (j0 even) from the 12
+// scale bytes in words s0..s2 (qwen3moe.cpp:133-141): sub-blocks 0-3 keep both
+// in the low six bits of bytes j and j+4; sub-blocks 4-7 keep the low four
+// bits in the nibbles of byte j+4 and the top two in bits 6-7 of bytes j-4
+// and j.  j0 and j0 + 1 share a form, so one set of selects serves both, and
+// each field is one or two bit-field extracts (a width of 0 extracts 0).
+__device__ __forceinline__ void scale_min_pair(int j0, uint32_t s0, uint32_t s1, uint32_t s2, int& sc0, int& m0,
+                                               int& sc1, int& m1) {
+    const bool lo = j0 < 4;
+    const uint32_t o = 8u * (uint32_t)(j0 & 3);
+    const uint32_t A = lo ? s0 : s2, B = lo ? s1 : s2;
+    const uint32_t w = lo ? 6u : 4u, wh = lo ? 0u : 2u, om = lo ? 0u : 4u;
+    sc0 = (int)(__builtin_amdgcn_ubfe(A, o, w) | (__builtin_amdgcn_ubfe(s0, o + 6u, wh) << 4));
+    m0 = (int)(__builtin_amdgcn_ubfe(B, o + om, w) | (__builtin_amdgcn_ubfe(s1, o + 6u, wh) << 4));
+    sc1 = (int)(__builtin_amdgcn_ubfe(A, o + 8u, w) | (__builtin_amdgcn_ubfe(s0, o + 14u, wh) << 4));
+    m1 = (int)(__builtin_amdgcn_ubfe(B, o + 8u + om, w) | (__builtin_amdgcn_ubfe(s1, o + 14u, wh) << 4));
+}
+
 // ---------------------------------------------------------------- Q4_K / Q5_K
 // Codes: dwords 0-7 the 32 values of sub-block 2g (values 0..31 of the
 // segment), dwords 8-15 those of sub-block 2g+1; value = d*sc*q - dmin*m.
@@ -66,7 +88,8 @@ struct SegCodesK {
                 lo = sdot4(c[i], x.q[L][i], lo);
                 hi = sdot4(c[8 + i], x.q[L][8 + i], hi);
             }
-            dot = __builtin_fmaf(x.s[L], (float)(sc0 * lo + sc1 * hi), dot);
+            // |lo|, |hi| <= 32 * 15 * 127 and scales < 64: 24-bit products suffice
+            dot = __builtin_fmaf(x.s[L], (float)(__mul24(sc0, lo) + __mul24(sc1, hi)), dot);
         }
         const float mt = __builtin_fmaf(dm0, x.sum32[0], dm1 * x.sum32[1]);
         return __builtin_fmaf(d, dot, -mt);
@@ -87,20 +110,16 @@ template <> struct RawSeg<kQ4_K> {
     }
     __device__ __forceinline__ SegCodes<kQ4_K> decode(int s) const {
         SegCodes<kQ4_K> k;
-        const float dmin = half_to_float(hdr.x >> 16);
-        const int j0 = 2 * (s & 3);
-        uint32_t sc0, m0, sc1, m1;
-        scale_min_k4(j0, hdr.y, hdr.z, hdr.w, sc0, m0);
-        scale_min_k4(j0 + 1, hdr.y, hdr.z, hdr.w, sc1, m1);
+        const float dmin = h2f(hdr.x >> 16);
+        int m0, m1;
+        scale_min_pair(2 * (s & 3), hdr.y, hdr.z, hdr.w, k.sc0, m0, k.sc1, m1);
         const uint32_t q[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
 #pragma unroll
         for (int i = 0; i < 8; i++) {
             k.c[i] = (int)(q[i] & 0x0F0F0F0Fu);
             k.c[8 + i] = (int)((q[i] >> 4) & 0x0F0F0F0Fu);
         }
-        k.sc0 = (int)sc0;
-        k.sc1 = (int)sc1;
-        k.d = half_to_float(hdr.x & 0xFFFFu);
+        k.d = h2f(hdr.x & 0xFFFFu);
         k.dm0 = dmin * (float)m0;
         k.dm1 = dmin * (float)m1;
         return k;
@@ -123,11 +142,10 @@ template <> struct RawSeg<kQ5_K> {
     }
     __device__ __forceinline__ SegCodes<kQ5_K> decode(int s) const {
         SegCodes<kQ5_K> k;
-        const float dmin = half_to_float(hdr.x >> 16);
+        const float dmin = h2f(hdr.x >> 16);
         const int j0 = 2 * (s & 3);
-        uint32_t sc0, m0, sc1, m1;
-        scale_min_k4(j0, hdr.y, hdr.z, hdr.w, sc0, m0);
-        scale_min_k4(j0 + 1, hdr.y, hdr.z, hdr.w, sc1, m1);
+        int m0, m1;
+        scale_min_pair(j0, hdr.y, hdr.z, hdr.w, k.sc0, m0, k.sc1, m1);
         const uint32_t q[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
         const uint32_t h[8] = {h0.x, h0.y, h0.z, h0.w, h1.x, h1.y, h1.z, h1.w};
 #pragma unroll
@@ -135,9 +153,7 @@ template <> struct RawSeg<kQ5_K> {
             k.c[i] = (int)((q[i] & 0x0F0F0F0Fu) | (((h[i] >> j0) & 0x01010101u) << 4));
             k.c[8 + i] = (int)(((q[i] >> 4) & 0x0F0F0F0Fu) | (((h[i] >> (j0 + 1)) & 0x01010101u) << 4));
         }
-        k.sc0 = (int)sc0;
-        k.sc1 = (int)sc1;
-        k.d = half_to_float(hdr.x & 0xFFFFu);
+        k.d = h2f(hdr.x & 0xFFFFu);
         k.dm0 = dmin * (float)m0;
         k.dm1 = dmin * (float)m1;
         return k;
@@ -166,7 +182,9 @@ template <> struct SegCodes<kQ6_K> {
             int acc[4] = {0, 0, 0, 0};
 #pragma unroll
             for (int i = 0; i < 16; i++) acc[i >> 2] = sdot4(c[i], x.q[L][i], acc[i >> 2]);
-            const int comb = sc[0] * acc[0] + sc[1] * acc[1] + sc[2] * acc[2] + sc[3] * acc[3];
+            // |acc| <= 16 * 128 * 127 and |sc| <= 128: 24-bit products suffice
+            const int comb = __mul24(sc[0], acc[0]) + __mul24(sc[1], acc[1]) + __mul24(sc[2], acc[2]) +
+                             __mul24(sc[3], acc[3]);
             dot = __builtin_fmaf(x.s[L], (float)comb, dot);
         }
         return d4 * dot;
@@ -204,7 +222,7 @@ template <> struct RawSeg<kQ6_K> {
         }
 #pragma unroll
         for (int g = 0; g < 4; g++) k.sc[g] = (int)(int8_t)((sc >> (8 * g)) & 0xFFu);
-        k.d4 = 0.25f * half_to_float(dbits);
+        k.d4 = 0.25f * h2f(dbits);
         return k;
     }
     __device__ __forceinline__ float dot_q8(int s, const XSeg& x) const { return decode(s).dot(x); }
@@ -254,8 +272,8 @@ template <> struct RawSeg<kQ8_0> {
             k.c[i] = (int)a.w[i];
             k.c[8 + i] = (int)b.w[i];
         }
-        k.d0 = half_to_float(d0);
-        k.d1 = half_to_float(d1);
+        k.d0 = h2f(d0);
+        k.d1 = h2f(d1);
         return k;
     }
     __device__ __forceinline__ float dot_q8(int s, const XSeg& x) const { return decode(s).dot(x); }
