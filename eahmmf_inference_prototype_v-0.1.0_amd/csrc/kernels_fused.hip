@@ -678,6 +678,7 @@ __device__ void fused_body(const FusedArgs& a, FusedLds& L) {
     };
 
     SegCodes<DT> pre[NPD];  // B waves: their first phase-B tasks, decoded
+    BTask tb[NPD];          // and where those tasks are
     if (wave < kAWaves) {
         // ---- 2A. this wave's passes through its LDS ring.  Every load the
         // compiler issued is retired first: the copies below are invisible to
@@ -737,14 +738,17 @@ __device__ void fused_body(const FusedArgs& a, FusedLds& L) {
         wait_lds(&L.b_landed, (unsigned)(kWaves - kAWaves));
 #pragma unroll
         for (int i = 0; i < NPD; i++) {
-            const BTask t = btask(min(wave - kAWaves + (kWaves - kAWaves) * i, n_tasks0 - 1), rr0, 0);
+            tb[i] = btask(min(wave - kAWaves + (kWaves - kAWaves) * i, n_tasks0 - 1), rr0, 0);
             RawSeg<DT> raw;
-            raw.template load<LdsLd>(t.row, t.sg);
-            pre[i] = raw.decode(t.sg);
+            raw.template load<LdsLd>(tb[i].row, tb[i].sg);
+            pre[i] = raw.decode(tb[i].sg);
             pre[i].pin_all();  // decoded here, not after the barrier
         }
     }
     __syncthreads();  // the h levels and the first phase-B codes are ready
+
+    // the router weight of each partition expert (0 for a slot without one)
+    const float wgt[2] = {dptr[0] ? L.w[p * ep] : 0.f, ep > 1 && dptr[1] ? L.w[p * ep + 1] : 0.f};
 
     // Phase B rounds: every wave takes (expert, segment, 64-row block) tasks;
     // a lane is one row, so the h levels of the task are read by all lanes at
@@ -761,16 +765,14 @@ __device__ void fused_body(const FusedArgs& a, FusedLds& L) {
             XSeg hs;  // the same address in every lane: one LDS broadcast per read
             load_xseg(hs, &L.b.hq[0][0], kMaxHP, &L.b.hsc[0][0], kMaxHP / 64, L.b.hs32, t.e * segB + t.sg);
             const float v = k.dot(hs);
-            if (t.r < rr) L.part[(t.e * rr + t.r) * segB + t.sg] = dptr[t.e] ? L.w[p * ep + t.e] * v : 0.f;
+            if (t.r < rr) L.part[__mul24(__mul24(t.e, rr) + t.r, segB) + t.sg] = wgt[t.e] * v;
         };
         int first = 0;
         if (r0 == 0) {
             if (wave >= kAWaves) {
 #pragma unroll
-                for (int i = 0; i < NPD; i++) {
-                    const int task = wave - kAWaves + (kWaves - kAWaves) * i;
-                    if (task < n_tasks0) finish(btask(task, rr, r0), pre[i]);
-                }
+                for (int i = 0; i < NPD; i++)
+                    if (wave - kAWaves + (kWaves - kAWaves) * i < n_tasks0) finish(tb[i], pre[i]);
             }
             first = (kWaves - kAWaves) * NPD;
         }
