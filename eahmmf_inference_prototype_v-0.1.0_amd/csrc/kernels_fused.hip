@@ -369,16 +369,18 @@ __device__ void route_keys(const FusedArgs& a, FusedLds& L, int lane) {
 }
 
 // acc + (key (hi, lo) > ki) for 64-bit keys, as the borrow out of ki - key:
-// three full-rate VALU instructions (a 64-bit compare is not full rate).
+// three full-rate VALU instructions (a 64-bit compare is not full rate).  The
+// borrow lives in an SGPR pair of its own, so independent accumulators are
+// independent chains.
 __device__ __forceinline__ int add_if_greater(int acc, uint32_t lo, uint32_t hi, uint64_t ki) {
     int r;
     uint32_t t;
-    asm("v_sub_co_u32 %1, vcc, %2, %3\n\t"
-        "v_subb_co_u32 %1, vcc, %4, %5, vcc\n\t"
-        "v_addc_co_u32 %0, vcc, 0, %6, vcc"
-        : "=v"(r), "=&v"(t)
-        : "v"((uint32_t)ki), "v"(lo), "v"((uint32_t)(ki >> 32)), "v"(hi), "v"(acc)
-        : "vcc");
+    uint64_t c;
+    asm("v_sub_co_u32 %1, %2, %3, %4\n\t"
+        "v_subb_co_u32 %1, %2, %5, %6, %2\n\t"
+        "v_addc_co_u32 %0, %2, 0, %7, %2"
+        : "=v"(r), "=&v"(t), "=&s"(c)
+        : "v"((uint32_t)ki), "v"(lo), "v"((uint32_t)(ki >> 32)), "v"(hi), "v"(acc));
     return r;
 }
 
@@ -400,16 +402,18 @@ __device__ void route_rank(const FusedArgs& a, FusedLds& L, int tid) {
             const uint64_t* kp = &L.rkey[2 * part];
             const int P = C / 2;
             int j = 0;
+            int acc[4] = {0, 0, 0, 0};  // four independent chains
             for (; j + 8 <= P; j += 8) {  // eight reads in flight before the first use
                 uint4 v[8];
 #pragma unroll
                 for (int u = 0; u < 8; u++) v[u] = *reinterpret_cast<const uint4*>(kp + 2 * T * (j + u));
 #pragma unroll
                 for (int u = 0; u < 8; u++) {
-                    ahead = add_if_greater(ahead, v[u].x, v[u].y, ki);
-                    ahead = add_if_greater(ahead, v[u].z, v[u].w, ki);
+                    acc[(2 * u) & 3] = add_if_greater(acc[(2 * u) & 3], v[u].x, v[u].y, ki);
+                    acc[(2 * u + 1) & 3] = add_if_greater(acc[(2 * u + 1) & 3], v[u].z, v[u].w, ki);
                 }
             }
+            ahead = (acc[0] + acc[1]) + (acc[2] + acc[3]);
             for (; j < P; j++) {
                 const uint4 v = *reinterpret_cast<const uint4*>(kp + 2 * T * j);
                 ahead = add_if_greater(ahead, v.x, v.y, ki);

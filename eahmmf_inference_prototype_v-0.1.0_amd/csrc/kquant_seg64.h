@@ -205,20 +205,22 @@ template <> struct RawSeg<kQ6_K> {
         sc = (uint32_t)LD::u16(sb + 192 + 8 * n + 4 * hi) | ((uint32_t)LD::u16(sb + 194 + 8 * n + 4 * hi) << 16);
         dbits = LD::u16(sb + 208);
     }
-    // 6-bit code bytes (0..63) of quarter u for ql dword i of one 32-byte half
-    __device__ __forceinline__ static uint32_t code(uint32_t ql, uint32_t h, int hi, int u) {
-        const uint32_t nib = hi ? ((ql >> 4) & 0x0F0F0F0Fu) : (ql & 0x0F0F0F0Fu);
-        return nib | (((h >> (2 * u)) & 0x03030303u) << 4);
-    }
     __device__ __forceinline__ SegCodes<kQ6_K> decode(int s) const {
         SegCodes<kQ6_K> k;
         const int hi = s & 1;
+        // Each byte becomes 4*(code-32) as a signed byte: the code's low nibble
+        // (ql, low or high half by hi) in bits 2-5, its two high bits (qh bits
+        // 2u, 2u+1 for quarter u = 2 hi + i/8) in bits 6-7, the top bit then
+        // flipped.  Both fields are moved with byte-wise-safe rotates (the bits
+        // that wrap are masked off).
+        const uint32_t rl = hi ? 2u : 30u;  // rotate right: nibble 1 -> bits 2-5, or nibble 0 -> bits 2-5
 #pragma unroll
         for (int i = 0; i < 16; i++) {
             const uint32_t ql = i < 8 ? l0.w[i] : l1.w[i - 8];
-            const int u = 2 * hi + (i >> 3);
-            // code*4 in the top six bits of each byte, as a signed byte 4*(code-32)
-            k.c[i] = (int)((code(ql, qh.w[i & 7], hi, u) << 2) ^ 0x80808080u);
+            const uint32_t u = 2u * (uint32_t)hi + (uint32_t)(i >> 3);
+            const uint32_t lo = __builtin_amdgcn_alignbit(ql, ql, rl) & 0x3C3C3C3Cu;
+            const uint32_t hb = __builtin_amdgcn_alignbit(qh.w[i & 7], qh.w[i & 7], (2u * u + 26u) & 31u);
+            k.c[i] = (int)(((hb & 0xC0C0C0C0u) | lo) ^ 0x80808080u);
         }
 #pragma unroll
         for (int g = 0; g < 4; g++) k.sc[g] = (int)(int8_t)((sc >> (8 * g)) & 0xFFu);
