@@ -18,7 +18,10 @@
  * Threading: like the reference's ABI, one caller thread per device is
  * assumed; each device has one internal stream and one set of scratch and
  * pinned staging buffers that grow on demand and are kept until
- * eahmmf_hip_shutdown().
+ * eahmmf_hip_shutdown().  The *_async entry points run on the caller's
+ * stream but use that same per-device scratch, so calls that may overlap in
+ * time on one device (streams without an order between them) race: order
+ * them on one stream.
  */
 #ifndef EAHMMF_HIP_H
 #define EAHMMF_HIP_H
