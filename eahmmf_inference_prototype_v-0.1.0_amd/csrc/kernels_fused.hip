@@ -189,6 +189,18 @@ __device__ __forceinline__ float group_sum(float v) {
     return v;
 }
 
+// The same for ints and a run-time group size T (uniform): the group's last
+// lane holds the total.
+__device__ __forceinline__ int group_sum_i(int v, int T) {
+    if (T >= 2) v += __builtin_amdgcn_update_dpp(0, v, 0xB1, 0xF, 0xF, false);
+    if (T >= 4) v += __builtin_amdgcn_update_dpp(0, v, 0x4E, 0xF, 0xF, false);
+    if (T >= 8) v += __builtin_amdgcn_update_dpp(0, v, 0x141, 0xF, 0xF, false);
+    if (T >= 16) v += __builtin_amdgcn_update_dpp(0, v, 0x140, 0xF, 0xF, false);
+    if (T >= 32) v += __builtin_amdgcn_update_dpp(0, v, 0x142, 0xA, 0xF, false);
+    if (T >= 64) v += __builtin_amdgcn_update_dpp(0, v, 0x143, 0xC, 0xF, false);
+    return v;
+}
+
 struct alignas(16) FusedLds {
     uint8_t stage_a[kAWaves][kSlotA];  // first members: 16-byte aligned
     uint8_t stage_b[kStageB];
@@ -384,58 +396,70 @@ __device__ __forceinline__ int add_if_greater(int acc, uint32_t lo, uint32_t hi,
     return r;
 }
 
+// The number of keys larger than ki among keys[0, T C) seen by thread part
+// of T: the pairs at 2 part + 2 T j (C even; N reads in flight, four
+// independent chains) or the keys at part + T j (C odd).  The T threads of a
+// candidate read adjacent banks and every candidate of a wave reads the same
+// words (broadcast).
+template <int N>
+__device__ __forceinline__ void count_pairs(const uint64_t* kp, int stride, int& j, int P, uint64_t ki,
+                                            int (&acc)[4]) {
+    for (; j + N <= P; j += N) {
+        uint4 v[N];
+#pragma unroll
+        for (int u = 0; u < N; u++) v[u] = *reinterpret_cast<const uint4*>(kp + stride * (j + u));
+#pragma unroll
+        for (int u = 0; u < N; u++) {
+            acc[(2 * u) & 3] = add_if_greater(acc[(2 * u) & 3], v[u].x, v[u].y, ki);
+            acc[(2 * u + 1) & 3] = add_if_greater(acc[(2 * u + 1) & 3], v[u].z, v[u].w, ki);
+        }
+    }
+}
+
+__device__ __forceinline__ int count_greater(const uint64_t* keys, int T, int part, int C, uint64_t ki) {
+    if ((C & 1) == 0) {
+        int acc[4] = {0, 0, 0, 0};
+        int j = 0;
+        count_pairs<8>(keys + 2 * part, 2 * T, j, C / 2, ki, acc);
+        count_pairs<4>(keys + 2 * part, 2 * T, j, C / 2, ki, acc);
+        count_pairs<2>(keys + 2 * part, 2 * T, j, C / 2, ki, acc);
+        count_pairs<1>(keys + 2 * part, 2 * T, j, C / 2, ki, acc);
+        return (acc[0] + acc[1]) + (acc[2] + acc[3]);
+    }
+    int ahead = 0;
+    for (int j = 0; j < C; j++) {
+        const uint64_t kj = keys[part + T * j];
+        ahead = add_if_greater(ahead, (uint32_t)kj, (uint32_t)(kj >> 32), ki);
+    }
+    return ahead;
+}
+
+// Slot r of the routing: the candidate's softmax numerator (its key's high
+// word less one) and id, or an empty slot for a NaN logit (high word 0).
+__device__ __forceinline__ void put_slot(FusedLds& L, int r, uint64_t key, int id) {
+    const uint32_t hi = (uint32_t)(key >> 32);
+    L.slot_key[r] = hi != 0u ? __builtin_bit_cast(float, hi - 1u) : -1.0f;
+    L.slot_id[r] = hi != 0u ? id : -1;
+}
+
 // Routing, step 2 (all threads): candidate i's rank in the reference's order
-// (qwen3moe.cpp:1016) is the number of larger keys.  T = 2^rank_shift
-// adjacent threads count over C = rank_c keys each: thread part reads the key
-// pairs 2 part + 2 T j (C even), so the T threads of a candidate read
-// adjacent banks and the wave's candidates share those reads (broadcast).
-// Ranks are distinct, so the top k fill slots 0..k-1.
+// (qwen3moe.cpp:1016) is the number of larger keys; ranks are distinct, so
+// the top k fill slots 0..k-1.  T = 2^rank_shift adjacent threads count over
+// C = rank_c keys each, and the group's last thread writes the slot.
 __device__ void route_rank(const FusedArgs& a, FusedLds& L, int tid) {
-    const int n = a.n_expert, C = a.rank_c;
-    const int i = tid >> a.rank_shift, part = tid & ((1 << a.rank_shift) - 1);
+    const int n = a.n_expert;
+    const int T = 1 << a.rank_shift;
+    const int i = tid >> a.rank_shift, part = tid & (T - 1);
     int ahead = 0;
     uint64_t ki = 0;
     if (i < n) {
         ki = L.rkey[i];
-        const int T = 1 << a.rank_shift;
-        if ((C & 1) == 0) {
-            const uint64_t* kp = &L.rkey[2 * part];
-            const int P = C / 2;
-            int j = 0;
-            int acc[4] = {0, 0, 0, 0};  // four independent chains
-            for (; j + 8 <= P; j += 8) {  // eight reads in flight before the first use
-                uint4 v[8];
-#pragma unroll
-                for (int u = 0; u < 8; u++) v[u] = *reinterpret_cast<const uint4*>(kp + 2 * T * (j + u));
-#pragma unroll
-                for (int u = 0; u < 8; u++) {
-                    acc[(2 * u) & 3] = add_if_greater(acc[(2 * u) & 3], v[u].x, v[u].y, ki);
-                    acc[(2 * u + 1) & 3] = add_if_greater(acc[(2 * u + 1) & 3], v[u].z, v[u].w, ki);
-                }
-            }
-            ahead = (acc[0] + acc[1]) + (acc[2] + acc[3]);
-            for (; j < P; j++) {
-                const uint4 v = *reinterpret_cast<const uint4*>(kp + 2 * T * j);
-                ahead = add_if_greater(ahead, v.x, v.y, ki);
-                ahead = add_if_greater(ahead, v.z, v.w, ki);
-            }
-        } else {
-            for (int j = 0; j < C; j++) {
-                const uint64_t kj = L.rkey[part + T * j];
-                ahead = add_if_greater(ahead, (uint32_t)kj, (uint32_t)(kj >> 32), ki);
-            }
-        }
+        ahead = count_greater(L.rkey, T, part, a.rank_c, ki);
     }
-    for (int off = (1 << a.rank_shift) / 2; off > 0; off >>= 1) ahead += __shfl_xor(ahead, off, 64);
-    if (i < n && part == 0 && ahead < a.k) {
-        const uint32_t hi = (uint32_t)(ki >> 32);
-        L.slot_key[ahead] = hi != 0u ? __builtin_bit_cast(float, hi - 1u) : -1.0f;
-        L.slot_id[ahead] = hi != 0u ? i : -1;
-    }
+    ahead = group_sum_i(ahead, T);
+    if (i < n && part == T - 1 && ahead < a.k) put_slot(L, ahead, ki, i);
 }
 
-// Routing, step 3 (one wave, lanes < k): renormalise the chosen e in rank
-// order, as the reference sums them.
 __device__ void route_weights(const FusedArgs& a, FusedLds& L, int lane) {
     const float kv = lane < a.k ? L.slot_key[lane] : -1.0f;
     const bool valid = kv >= 0.f;
@@ -1015,11 +1039,11 @@ hipError_t launch_moe_fused(const FusedArgsHost& h, hipStream_t st) {
     a.local_l2 = (a.np == 8 && xcd_round_robin(dev)) ? 1 : 0;
     a.epoch = h.epoch;
     // routing: n_expert rounded up to a power of two (at most 256) is split
-    // into t runs of rank_c keys, t threads per candidate
+    // into t runs of rank_c keys, t threads per candidate (t <= 16)
     int npow = 1;
     while (npow < a.n_expert) npow *= 2;
     int t = kThreads / npow;
-    if (t > 64) t = 64;
+    if (t > 16) t = 16;
     if (t > npow) t = npow;
     a.rank_shift = 0;
     while ((1 << a.rank_shift) < t) a.rank_shift++;
