@@ -435,11 +435,15 @@ __device__ __forceinline__ int count_greater(const uint64_t* keys, int T, int pa
 }
 
 // Slot r of the routing: the candidate's softmax numerator (its key's high
-// word less one) and id, or an empty slot for a NaN logit (high word 0).
-__device__ __forceinline__ void put_slot(FusedLds& L, int r, uint64_t key, int id) {
-    const uint32_t hi = (uint32_t)(key >> 32);
-    L.slot_key[r] = hi != 0u ? __builtin_bit_cast(float, hi - 1u) : -1.0f;
-    L.slot_id[r] = hi != 0u ? id : -1;
+// word less one), id and weight pointers, or an empty slot for a NaN logit
+// (high word 0).
+__device__ __forceinline__ void put_slot(FusedLds& L, int r, uint64_t key, int id, const ExpertEntry& ent) {
+    const bool ok = (uint32_t)(key >> 32) != 0u;
+    L.slot_key[r] = ok ? __builtin_bit_cast(float, (uint32_t)(key >> 32) - 1u) : -1.0f;
+    L.slot_id[r] = ok ? id : -1;
+    L.gate[r] = ok ? ent.gate : nullptr;
+    L.up[r] = ok ? ent.up : nullptr;
+    L.down[r] = ok ? ent.down : nullptr;
 }
 
 // Routing, step 2 (all threads): candidate i's rank in the reference's order
@@ -452,12 +456,14 @@ __device__ void route_rank(const FusedArgs& a, FusedLds& L, int tid) {
     const int i = tid >> a.rank_shift, part = tid & (T - 1);
     int ahead = 0;
     uint64_t ki = 0;
+    ExpertEntry ent{nullptr, nullptr, nullptr};
     if (i < n) {
         ki = L.rkey[i];
+        if (part == T - 1) ent = L.table[i];  // read with the keys, used by the slot's writer
         ahead = count_greater(L.rkey, T, part, a.rank_c, ki);
     }
     ahead = group_sum_i(ahead, T);
-    if (i < n && part == T - 1 && ahead < a.k) put_slot(L, ahead, ki, i);
+    if (i < n && part == T - 1 && ahead < a.k) put_slot(L, ahead, ki, i, ent);
 }
 
 __device__ void route_weights(const FusedArgs& a, FusedLds& L, int lane) {
@@ -476,16 +482,11 @@ __device__ void route_weights(const FusedArgs& a, FusedLds& L, int lane) {
     }
 }
 
-// Weight pointers of routed slot j (matrix c: 0 gate, 1 up, 2 down): from
-// the table row of the slot's expert id when the kernel routed, else as the
-// caller gave them; null for a slot without an expert.
-__device__ __forceinline__ const uint8_t* slot_ptr(const FusedArgs& a, const FusedLds& L, int j, int c) {
-    if (a.mode == 1) {
-        const int id = L.slot_id[j];
-        if (id < 0) return nullptr;
-        const ExpertEntry& t = L.table[id];
-        return c == 0 ? t.gate : (c == 1 ? t.up : t.down);
-    }
+// Weight pointers of slot j (matrix c: 0 gate, 1 up, 2 down), null for a
+// slot without an expert.  Every mode fills them before the routing barrier
+// (the routing writes them with the slot), so reading them is one LDS round
+// trip for all six.
+__device__ __forceinline__ const uint8_t* slot_ptr(const FusedLds& L, int j, int c) {
     return c == 0 ? L.gate[j] : (c == 1 ? L.up[j] : L.down[j]);
 }
 
@@ -586,6 +587,7 @@ __device__ void fused_body(const FusedArgs& a, FusedLds& L) {
             if (lane >= a.n_expert && lane < k) {
                 L.slot_key[lane] = -1.0f;
                 L.slot_id[lane] = -1;
+                L.gate[lane] = L.up[lane] = L.down[lane] = nullptr;
             }
         } else if (lane < k) {
             if (a.mode == 0) {
@@ -621,15 +623,23 @@ __device__ void fused_body(const FusedArgs& a, FusedLds& L) {
     }
 
     // weight pointers of the partition's (at most two) experts
-    const uint8_t* gptr[2] = {slot_ptr(a, L, p * ep, 0), ep > 1 ? slot_ptr(a, L, p * ep + 1, 0) : nullptr};
-    const uint8_t* uptr[2] = {slot_ptr(a, L, p * ep, 1), ep > 1 ? slot_ptr(a, L, p * ep + 1, 1) : nullptr};
-    const uint8_t* dptr[2] = {slot_ptr(a, L, p * ep, 2), ep > 1 ? slot_ptr(a, L, p * ep + 1, 2) : nullptr};
+    // (all six read at once: slot p ep + 1 < kMaxSlots exists even when unused)
+    const uint8_t* sp[6];
+#pragma unroll
+    for (int c = 0; c < 6; c++) sp[c] = slot_ptr(L, p * ep + (c & 1), c >> 1);
+    const uint8_t* gptr[2] = {sp[0], ep > 1 ? sp[1] : nullptr};
+    const uint8_t* uptr[2] = {sp[2], ep > 1 ? sp[3] : nullptr};
+    const uint8_t* dptr[2] = {sp[4], ep > 1 ? sp[5] : nullptr};
+    // the source of copies whose bytes are never used (x: valid, 16-byte
+    // aligned), held in registers rather than reloaded from the arguments
+    const uint8_t* xsrc = reinterpret_cast<const uint8_t*>(a.x);
+    asm volatile("" : "+s"(xsrc));
 
     // phase-B stage: rows [r0, r0 + rr) of the chunk, expert e of the
     // partition at stage_b + e * stride_b + (its source & 15)
     auto down_src = [&](int e, int r0) -> const uint8_t* {
         const uint8_t* dw = dptr[e];
-        return dw ? dw + (size_t)(r_begin + r0) * drb : reinterpret_cast<const uint8_t*>(a.x);
+        return dw ? dw + (size_t)(r_begin + r0) * drb : xsrc;
     };
     // global source of 1 KB stage instruction ii of expert e (lanes past the
     // end re-read the last 16 bytes)
@@ -700,8 +710,8 @@ __device__ void fused_body(const FusedArgs& a, FusedLds& L) {
         const uint8_t* uw = uptr[r.e];
         r.ok = (r.nr > 0) & (gw != nullptr) & (uw != nullptr);
         // a pass without weights copies 16 bytes of x instead; nothing of it is used
-        r.g = r.ok ? gw + (size_t)r.f0 * grb : reinterpret_cast<const uint8_t*>(a.x);
-        r.u = r.ok ? uw + (size_t)r.f0 * urb : reinterpret_cast<const uint8_t*>(a.x);
+        r.g = r.ok ? gw + (size_t)r.f0 * grb : xsrc;
+        r.u = r.ok ? uw + (size_t)r.f0 * urb : xsrc;
         return r;
     };
 
