@@ -566,6 +566,15 @@ int eahmmf_hip_route_topk_async(const float* dev_logits, int nb, int n_expert, i
     return hip_ok(e, "route launch") ? 0 : -3;
 }
 
+int eahmmf_hip_stream_read_async(const void* dev_buf, size_t bytes, uint32_t* dev_sink, void* stream) {
+    if (bytes == 0) return 0;
+    if (!dev_buf || !dev_sink) return set_error("null argument"), -1;
+    const hipError_t e = launch_stream_read(dev_buf, bytes, dev_sink, (hipStream_t)stream);
+    if (e == hipErrorInvalidValue)
+        return set_error("stream read needs a 16-byte aligned buffer and a multiple of 16 bytes (got %zu)", bytes), -1;
+    return hip_ok(e, "stream read launch") ? 0 : -3;
+}
+
 int eahmmf_hip_dequantize(const uint8_t* dev_w, int type, int64_t ne0, int64_t nrows, size_t row_bytes,
                           float* dev_out, void* stream) {
     if (!dev_w || !dev_out || nrows < 0) return set_error("null argument"), -1;

@@ -23,7 +23,7 @@ EXPORTS = (
     "eahmmf_hip_free", "eahmmf_hip_h2d", "eahmmf_hip_d2h", "eahmmf_hip_sync", "eahmmf_hip_mem_info",
     "eahmmf_hip_last_error", "eahmmf_hip_device_count", "eahmmf_hip_shutdown", "eahmmf_hip_moe_layer_decode_async",
     "eahmmf_hip_set_fused", "eahmmf_hip_device_flags", "eahmmf_hip_fused_exchange", "eahmmf_hip_moe_grouped",
-    "eahmmf_hip_moe_grouped_async", "eahmmf_hip_set_grouped_mfma",
+    "eahmmf_hip_moe_grouped_async", "eahmmf_hip_set_grouped_mfma", "eahmmf_hip_stream_read_async",
 )
 
 
@@ -93,6 +93,7 @@ def load(path=LIB_PATH):
                                                  vp]),
         "eahmmf_hip_route_topk": (c_bool, [vp, c_int, c_int, c_int, vp, vp]),
         "eahmmf_hip_route_topk_async": (c_int, [vp, c_int, c_int, c_int, vp, vp, vp]),
+        "eahmmf_hip_stream_read_async": (c_int, [vp, ctypes.c_size_t, vp, vp]),
         "eahmmf_hip_dequantize": (c_int, [vp, c_int, c_i64, c_i64, c_sz, vp, vp]),
         "eahmmf_hip_row_bytes": (c_sz, [c_int, c_i64]),
         "eahmmf_hip_quantize_rows": (c_i64, [c_int, vp, c_i64, c_i64, vp]),

@@ -41,6 +41,13 @@ def test_invalid_arguments_fail_without_touching_the_device(hip):
     ids = np.zeros(8, dtype=np.int32)
     assert not hip.eahmmf_hip_route_topk(x.ctypes.data, 1, 128, 17, ids.ctypes.data, out.ctypes.data)
     assert not hip.eahmmf_hip_route_topk(x.ctypes.data, 1, 1024, 8, ids.ctypes.data, out.ctypes.data)
+    # streaming read: nothing to do for 0 bytes; null, unaligned or ragged sizes rejected up front
+    assert hip.eahmmf_hip_stream_read_async(None, 0, None, None) == 0
+    assert hip.eahmmf_hip_stream_read_async(None, 16, fake, None) == -1
+    assert "null" in hip.eahmmf_hip_last_error().decode()
+    assert hip.eahmmf_hip_stream_read_async(fake + 8, 16, fake, None) == -1
+    assert hip.eahmmf_hip_stream_read_async(fake, 24, fake, None) == -1
+    assert "multiple of 16" in hip.eahmmf_hip_last_error().decode()
 
 
 @pytest.mark.parametrize("t,ne0", [(0, 64), (8, 96), (12, 2048), (13, 768), (14, 768), (14, 1536)])
