@@ -208,7 +208,7 @@ def stream_rates(torch, hip, steps=2000):
     W, R = 24_477_696, 16
     buf = torch.empty(W * R, dtype=torch.uint8, device="cuda").random_(0, 256)
     big = torch.empty(1 << 30, dtype=torch.uint8, device="cuda").random_(0, 256)
-    sink = torch.zeros(1, dtype=torch.int32, device="cuda")
+    sink = torch.zeros(4096, dtype=torch.int32, device="cuda")
     stream = torch.cuda.current_stream()
     sp, vp = ctypes.c_void_p(stream.cuda_stream), ctypes.c_void_p
 

@@ -101,8 +101,9 @@ int set_grouped_mfma(int enable);
 
 // softmax -> top-k (e desc, index asc) -> renormalise; logits [nb][n_expert].
 hipError_t launch_route_topk(const float* logits, int nb, int n_expert, int k, int* ids, float* w, hipStream_t st);
-// Streaming read of bytes (a multiple of 16, 16-byte aligned buffer) with
-// *sink ^= the XOR of every 32-bit word; hipErrorInvalidValue on bad arguments.
+// Streaming read of bytes (a multiple of 16, 16-byte aligned buffer); the
+// XOR of sink[0..4096) becomes the XOR of every 32-bit word read.
+// hipErrorInvalidValue on bad arguments.
 hipError_t launch_stream_read(const void* buf, size_t bytes, uint32_t* sink, hipStream_t st);
 
 bool moe_shape_ok(const MoeShape& s);

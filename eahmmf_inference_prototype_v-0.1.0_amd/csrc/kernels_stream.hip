@@ -3,9 +3,9 @@
 //
 // Workgroup g of G reads the contiguous chunk [g per, (g+1) per) of the buffer
 // (16-byte units) with nontemporal 16-byte loads, eight per thread in flight,
-// and XORs every 32-bit word it reads into one value; the G values are XORed
-// into *sink with one vector atomic per workgroup, so no load can be dropped
-// and the result does not depend on the order the workgroups finish in.
+// and XORs every 32-bit word it reads into one value, stored to sink[g]; the
+// other words of the kStreamMaxGroups-word sink are set to 0, so the XOR of
+// the whole sink is the XOR of the buffer and no load can be dropped.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -43,8 +43,13 @@ __global__ __launch_bounds__(kStreamThreads) void stream_read_kernel(const v4u* 
     if (threadIdx.x == 0) {
         uint32_t t = 0;
         for (int w = 0; w < kStreamThreads / 64; w++) t ^= wv[w];
-        __hip_atomic_fetch_xor(sink, t, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        sink[blockIdx.x] = t;
     }
+    // the sink words past the grid read as 0 (plain stores: no atomics on
+    // one address, which would serialise across the XCDs)
+    for (unsigned w = blockIdx.x + gridDim.x * (threadIdx.x + 1u); w < (unsigned)kStreamMaxGroups;
+         w += gridDim.x * kStreamThreads)
+        sink[w] = 0u;
 }
 
 // Workgroups: one full batch per thread at least, rounded up to a multiple of

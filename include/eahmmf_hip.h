@@ -145,11 +145,14 @@ int eahmmf_hip_route_topk_async(const float* dev_logits, int nb, int n_expert, i
 /* ---- measurement ------------------------------------------------------ */
 
 /* Streaming read of bytes from dev_buf (16-byte aligned, bytes a multiple of
- * 16): *dev_sink ^= the XOR of every 32-bit word read.  No counterpart in the
- * reference: it measures the achievable HBM read rate that the decode
- * kernels are compared with (nontemporal 16-byte loads, eight per thread in
- * flight, at most 4096 workgroups of 512 threads).  Asynchronous on stream;
- * 0 on success, -1 on bad arguments, -3 on a launch error. */
+ * 16).  dev_sink holds EAHMMF_HIP_STREAM_SINK_WORDS words; afterwards their
+ * XOR is the XOR of every 32-bit word read.  No counterpart in the reference:
+ * it measures the achievable HBM read rate that the decode kernels are
+ * compared with (nontemporal 16-byte loads, eight per thread in flight, at
+ * most 4096 workgroups of 512 threads, no atomics).  Asynchronous on stream;
+ * 0 on success (also for 0 bytes, which writes nothing), -1 on bad arguments,
+ * -3 on a launch error. */
+#define EAHMMF_HIP_STREAM_SINK_WORDS 4096
 int eahmmf_hip_stream_read_async(const void* dev_buf, size_t bytes, uint32_t* dev_sink, void* stream);
 
 /* ---- format utilities ------------------------------------------------- */

@@ -201,20 +201,20 @@ def test_moe_decode_vs_oracle(torch_dev, binding, hip, path, name, types, D, FF,
 
 @pytest.mark.parametrize("nbytes", [16, 4096 + 48, 3 * (1 << 20) + 16 * 37, 24_477_696, (1 << 28) + 4096 + 48])
 def test_stream_read_checksum(torch_dev, hip, nbytes):
-    """The streaming-read kernel reads every byte once: the sink word becomes
-    its old value XOR the XOR of all 32-bit words (sizes cover one partial
-    batch, a ragged tail, the C2 expert bytes and more than 4096 full chunks)."""
+    """The streaming-read kernel reads every byte once: the XOR of the 4096
+    sink words (pre-filled with garbage) is the XOR of all 32-bit words of
+    the buffer (sizes cover one partial batch, a ragged tail, the C2 expert
+    bytes and more than 4096 full chunks)."""
     torch = torch_dev
     rng = np.random.default_rng(nbytes % 100003)
     host = rng.integers(0, 2**32, nbytes // 4, dtype=np.uint32)
     dbuf = to_dev(torch, host.view(np.int32))
-    v0 = np.uint32(0x9E3779B9)
-    dsink = to_dev(torch, np.array([v0], dtype=np.uint32).view(np.int32))
+    dsink = to_dev(torch, rng.integers(0, 2**32, 4096, dtype=np.uint32).view(np.int32))
     stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
     assert hip.eahmmf_hip_stream_read_async(ptr(dbuf), nbytes, ptr(dsink), stream) == 0, hip.eahmmf_hip_last_error()
     torch.cuda.synchronize()
-    got = dsink.cpu().numpy().view(np.uint32)[0]
-    assert got == v0 ^ np.bitwise_xor.reduce(host)
+    got = np.bitwise_xor.reduce(dsink.cpu().numpy().view(np.uint32))
+    assert got == np.bitwise_xor.reduce(host)
 
 
 def test_route_topk_vs_oracle(torch_dev, hip):
