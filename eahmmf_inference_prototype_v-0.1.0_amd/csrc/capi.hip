@@ -17,6 +17,7 @@
 #include <string>
 #include <vector>
 #include <algorithm>
+#include <thread>
 
 #include "../../include/eahmmf_hip.h"
 #include "internal.h"
@@ -48,12 +49,21 @@ struct DeviceBuf {
     size_t cap = 0;
 };
 
+// Bulk staging ring: kRingSlots pinned slots of kRingChunk bytes each.
+constexpr int kRingSlots = 4;
+constexpr size_t kRingChunk = (size_t)32 << 20;
+
 struct DevCtx {
     hipStream_t stream = nullptr;
     DeviceBuf dx, dy, dy2, dh, dids, dw, dyp, dhx, dgs, dtab;  // device scratch
     DeviceBuf px, py, py2;                // pinned host staging
     unsigned* dsync = nullptr;            // fused-launch counters and flags (zeroed once)
     unsigned epoch = 0;                   // fused launches issued on dsync
+    // bulk host-to-device staging (eahmmf_hip_h2d_batch), created on first use
+    hipStream_t copy_stream[kRingSlots] = {};  // one per slot: slots drain on parallel DMA engines
+    uint8_t* ring[kRingSlots] = {};
+    hipEvent_t ring_done[kRingSlots] = {};  // recorded after the copies out of each slot
+    bool ring_ready = false;
 };
 
 // 1: single fused launch where the shape allows it; 0: route + two-kernel path.
@@ -169,6 +179,63 @@ bool grow_fused(DevCtx* c, const MoeShape& s, int k) {
 }
 
 bool weight_ok(const eahmmf_hip_weight& w) { return w.dev && type_supported(w.type) && w.ne0 > 0 && w.ne1 > 0; }
+
+bool ensure_ring(DevCtx* c) {
+    if (c->ring_ready) return true;
+    for (int s = 0; s < kRingSlots; s++) {
+        if (!c->copy_stream[s] &&
+            !hip_ok(hipStreamCreateWithFlags(&c->copy_stream[s], hipStreamNonBlocking), "hipStreamCreate(staging)"))
+            return false;
+        if (!c->ring[s]) {
+            void* p = nullptr;
+            if (!hip_ok(hipHostMalloc(&p, kRingChunk, hipHostMallocDefault), "hipHostMalloc(staging ring)")) return false;
+            c->ring[s] = (uint8_t*)p;
+        }
+        if (!c->ring_done[s] &&
+            !hip_ok(hipEventCreateWithFlags(&c->ring_done[s], hipEventDisableTiming), "hipEventCreate(staging)"))
+            return false;
+    }
+    c->ring_ready = true;
+    return true;
+}
+
+// One piece of a staging slot: n bytes from src to dst, at offset at in the slot.
+struct Piece {
+    uint8_t* dst;
+    const uint8_t* src;
+    size_t n, at;
+};
+
+// Threads that fill a slot (pageable -> pinned copies run on the CPU).
+int stage_threads() {
+    static const int n = [] {
+        const char* e = getenv("EAHMMF_HIP_STAGE_THREADS");
+        int v = e && *e ? atoi(e) : (int)std::thread::hardware_concurrency() / 2;
+        return v < 1 ? 1 : (v > 16 ? 16 : v);
+    }();
+    return n;
+}
+
+// Copies the pieces into the slot, splitting the slot's bytes [0, total)
+// evenly over nt threads (small slots on the calling thread alone).
+void fill_slot(uint8_t* slot, const std::vector<Piece>& ps, size_t total, int nt) {
+    auto range = [&](size_t lo, size_t hi) {
+        for (const Piece& q : ps) {
+            const size_t a = std::max(lo, q.at), b = std::min(hi, q.at + q.n);
+            if (a < b) memcpy(slot + a, q.src + (a - q.at), b - a);
+        }
+    };
+    if (nt <= 1 || total < ((size_t)4 << 20)) {
+        range(0, total);
+        return;
+    }
+    const size_t per = ((total + nt - 1) / nt + 4095) & ~(size_t)4095;
+    std::vector<std::thread> th;
+    for (int t = 1; t < nt && (size_t)t * per < total; t++)
+        th.emplace_back(range, (size_t)t * per, std::min(total, (size_t)(t + 1) * per));
+    range(0, std::min(total, per));
+    for (std::thread& x : th) x.join();
+}
 
 }  // namespace
 
@@ -621,6 +688,57 @@ int eahmmf_hip_mem_info(size_t* free_bytes, size_t* total_bytes) {
     return 0;
 }
 
+int eahmmf_hip_h2d_batch(const eahmmf_hip_copy* copies, int n) {
+    if (n < 0 || (n > 0 && !copies)) return set_error("null argument"), -1;
+    for (int i = 0; i < n; i++)
+        if (copies[i].bytes && (!copies[i].dev_dst || !copies[i].host_src))
+            return set_error("copy %d: null pointer", i), -1;
+    if (n == 0) return 0;
+    DevCtx* c = ctx_for_current_device();
+    if (!c || !ensure_ring(c)) return -2;
+    // work already queued on the library's stream finishes first
+    if (!drain(c, true)) return -2;
+    const int nt = stage_threads();
+    bool ok = true;
+    int slot = 0;
+    std::vector<Piece> ps;
+    size_t fill = 0;
+    // slot: wait until its previous copies have left it, fill it on the CPU,
+    // then one DMA per piece on the staging stream and an event behind them
+    auto flush = [&]() -> bool {
+        if (ps.empty()) return true;
+        if (!hip_ok(hipEventSynchronize(c->ring_done[slot]), "staging wait")) return false;
+        fill_slot(c->ring[slot], ps, fill, nt);
+        for (const Piece& q : ps)
+            if (!hip_ok(hipMemcpyAsync(q.dst, c->ring[slot] + q.at, q.n, hipMemcpyHostToDevice,
+                                       c->copy_stream[slot]),
+                        "staging copy"))
+                return false;
+        if (!hip_ok(hipEventRecord(c->ring_done[slot], c->copy_stream[slot]), "staging record")) return false;
+        slot = (slot + 1) % kRingSlots;
+        ps.clear();
+        fill = 0;
+        return true;
+    };
+    for (int i = 0; ok && i < n; i++) {
+        uint8_t* dst = (uint8_t*)copies[i].dev_dst;
+        const uint8_t* src = (const uint8_t*)copies[i].host_src;
+        for (size_t off = 0; ok && off < copies[i].bytes;) {
+            const size_t m = std::min(copies[i].bytes - off, kRingChunk - fill);
+            ps.push_back(Piece{dst + off, src + off, m, fill});
+            off += m;
+            fill = std::min(kRingChunk, (fill + m + 255) & ~(size_t)255);  // pieces start 256-byte aligned
+            if (fill == kRingChunk) ok = flush();
+        }
+    }
+    if (ok) ok = flush();
+    for (int s = 0; s < kRingSlots; s++) {  // drained on every path
+        const hipError_t e = hipStreamSynchronize(c->copy_stream[s]);
+        if (ok && e != hipSuccess) ok = hip_ok(e, "staging drain");
+    }
+    return ok ? 0 : -2;
+}
+
 void eahmmf_hip_shutdown(void) {
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess) return;
@@ -634,6 +752,12 @@ void eahmmf_hip_shutdown(void) {
     for (DeviceBuf* b : {&c.px, &c.py, &c.py2})
         if (b->p) (void)hipHostFree(b->p);
     if (c.dsync) (void)hipFree(c.dsync);
+    for (int s = 0; s < kRingSlots; s++) {
+        if (c.copy_stream[s]) (void)hipStreamSynchronize(c.copy_stream[s]);
+        if (c.ring[s]) (void)hipHostFree(c.ring[s]);
+        if (c.ring_done[s]) (void)hipEventDestroy(c.ring_done[s]);
+        if (c.copy_stream[s]) (void)hipStreamDestroy(c.copy_stream[s]);
+    }
     if (c.stream) (void)hipStreamDestroy(c.stream);
     g_ctx.erase(it);
 }

@@ -24,6 +24,7 @@ EXPORTS = (
     "eahmmf_hip_last_error", "eahmmf_hip_device_count", "eahmmf_hip_shutdown", "eahmmf_hip_moe_layer_decode_async",
     "eahmmf_hip_set_fused", "eahmmf_hip_device_flags", "eahmmf_hip_fused_exchange", "eahmmf_hip_moe_grouped",
     "eahmmf_hip_moe_grouped_async", "eahmmf_hip_set_grouped_mfma", "eahmmf_hip_stream_read_async",
+    "eahmmf_hip_h2d_batch",
 )
 
 
@@ -38,6 +39,10 @@ class Expert(ctypes.Structure):
 
 class ExpertPtrs(ctypes.Structure):
     _fields_ = [("gate", ctypes.c_void_p), ("up", ctypes.c_void_p), ("down", ctypes.c_void_p)]
+
+
+class Copy(ctypes.Structure):
+    _fields_ = [("dev_dst", ctypes.c_void_p), ("host_src", ctypes.c_void_p), ("bytes", ctypes.c_size_t)]
 
 
 class MoeShape(ctypes.Structure):
@@ -94,6 +99,7 @@ def load(path=LIB_PATH):
         "eahmmf_hip_route_topk": (c_bool, [vp, c_int, c_int, c_int, vp, vp]),
         "eahmmf_hip_route_topk_async": (c_int, [vp, c_int, c_int, c_int, vp, vp, vp]),
         "eahmmf_hip_stream_read_async": (c_int, [vp, ctypes.c_size_t, vp, vp]),
+        "eahmmf_hip_h2d_batch": (c_int, [ctypes.POINTER(Copy), c_int]),
         "eahmmf_hip_dequantize": (c_int, [vp, c_int, c_i64, c_i64, c_sz, vp, vp]),
         "eahmmf_hip_row_bytes": (c_sz, [c_int, c_i64]),
         "eahmmf_hip_quantize_rows": (c_i64, [c_int, vp, c_i64, c_i64, vp]),

@@ -67,6 +67,10 @@ struct HipDeviceOn : Base {
     bool h2d(void* d, const void* s, size_t n) override { return eahmmf_hip_h2d(d, s, n) == 0; }
     bool d2h(void* d, const void* s, size_t n) override { return eahmmf_hip_d2h(d, s, n) == 0; }
     bool sync() override { return eahmmf_hip_sync() == 0; }
+    // Not in the reference's interface: many host-to-device copies in one
+    // call through the library's pinned staging ring (valid for compute when
+    // it returns), for preloading experts instead of one h2d() + sync() each.
+    bool h2d_batch(const eahmmf_hip_copy* copies, int n) { return eahmmf_hip_h2d_batch(copies, n) == 0; }
     bool cpu_readable() const override { return false; }
     size_t total_memory() const override { return total; }
     size_t free_memory() const override {

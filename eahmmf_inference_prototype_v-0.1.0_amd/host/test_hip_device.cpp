@@ -113,6 +113,40 @@ static void check_expert_block(eahmmf_hip::HipDevice& dev, int D, int FF, int k,
     for (void* p : owned) dev.release(p, 0);
 }
 
+// Bulk staging (h2d_batch): copies of assorted sizes - one byte, unaligned,
+// exactly one 32 MiB ring slot, more than one slot, empty, and the C2 expert
+// components - land byte for byte; a second batch reuses the ring.
+static void check_batch(eahmmf_hip::HipDevice& dev) {
+    std::mt19937 rng(99u);
+    const size_t sizes[] = {1, 4097, (size_t)32 << 20, ((size_t)40 << 20) + 123, 0, 884736, 1290240, 884736};
+    const int n = (int)(sizeof sizes / sizeof sizes[0]);
+    std::vector<std::vector<uint8_t>> host(n);
+    std::vector<void*> ptrs(n, nullptr);
+    std::vector<eahmmf_hip_copy> cp(n);
+    for (int round = 0; round < 2; round++) {
+        for (int i = 0; i < n; i++) {
+            host[i].resize(sizes[i]);
+            for (auto& b : host[i]) b = (uint8_t)rng();
+            if (round == 0 && sizes[i]) {
+                ptrs[i] = dev.alloc(sizes[i]);
+                CHECK(ptrs[i] != nullptr);
+            }
+            cp[i] = eahmmf_hip_copy{ptrs[i], host[i].data(), sizes[i]};
+        }
+        CHECK(dev.h2d_batch(cp.data(), n));
+        for (int i = 0; i < n; i++) {
+            if (!sizes[i] || !ptrs[i]) continue;
+            std::vector<uint8_t> back(sizes[i]);
+            CHECK(dev.d2h(back.data(), ptrs[i], sizes[i]));
+            CHECK(back == host[i]);
+        }
+    }
+    CHECK(eahmmf_hip_h2d_batch(nullptr, 1) == -1);
+    CHECK(eahmmf_hip_h2d_batch(cp.data(), 0) == 0);
+    for (void* p : ptrs)
+        if (p) dev.release(p, 0);
+}
+
 int main() {
     if (eahmmf_hip_device_count() < 1) {
         fprintf(stderr, "no HIP device\n");
@@ -126,6 +160,7 @@ int main() {
     check_expert_block(dev, 512, 256, 2, 12, 14);    // Q4_K gate/up, Q6_K down
     check_expert_block(dev, 2048, 768, 8, 12, 14);   // Qwen3-30B-A3B expert shape, top-8
     check_expert_block(dev, 1024, 512, 4, 8, 8);     // Q8_0 throughout
+    check_batch(dev);
     eahmmf_hip_shutdown();
     if (g_fail) {
         fprintf(stderr, "%d check(s) failed\n", g_fail);

@@ -180,6 +180,27 @@ int eahmmf_hip_d2h(void* host_dst, const void* dev_src, size_t n);
 int eahmmf_hip_sync(void);
 int eahmmf_hip_mem_info(size_t* free_bytes, size_t* total_bytes);
 
+/* One host-to-device copy of a batch. */
+typedef struct {
+    void* dev_dst;
+    const void* host_src; /* pageable host memory */
+    size_t bytes;
+} eahmmf_hip_copy;
+
+/* Bulk staging: performs n host-to-device copies through a ring of four
+ * 32 MiB pinned buffers, so that CPU threads fill one buffer while the DMA
+ * engine drains the others (EAHMMF_HIP_STAGE_THREADS threads, default half
+ * the host's hardware threads, at most 16).  Small copies share a buffer.
+ * Work already queued on the library stream finishes first; the call returns
+ * when every byte is on the device (copies are then valid for compute, as
+ * after h2d() + sync()).  The reference moves an expert with three h2d()
+ * calls and a sync() (ExpertPager::stage_to_vram, eahmmf.h:959-1031, the
+ * copies at :1009-1013) and lists asynchronous prefetch as not implemented
+ * (README.md:379); this is the batch form its store can use to make many
+ * experts resident at once.  Single-threaded caller per device.  0 on
+ * success, -1 on bad arguments, -2 on a HIP error. */
+int eahmmf_hip_h2d_batch(const eahmmf_hip_copy* copies, int n);
+
 /* ---- diagnostics / lifetime ------------------------------------------- */
 /* Selects the single-launch fused expert block (1, the default) or the
  * routing + two-kernel path (0); a negative argument only queries.  Returns

@@ -23,7 +23,7 @@ def test_every_declared_symbol_is_exported(binding, hip):
     assert set(syms) == set(binding.EXPORTS)
 
 
-def test_invalid_arguments_fail_without_touching_the_device(hip):
+def test_invalid_arguments_fail_without_touching_the_device(binding, hip):
     x = np.zeros(256, dtype=np.float32)
     out = np.zeros(8, dtype=np.float32)
     # null weights, unsupported type, bad ldx, row_bytes mismatch: all rejected up front
@@ -48,6 +48,13 @@ def test_invalid_arguments_fail_without_touching_the_device(hip):
     assert hip.eahmmf_hip_stream_read_async(fake + 8, 16, fake, None) == -1
     assert hip.eahmmf_hip_stream_read_async(fake, 24, fake, None) == -1
     assert "multiple of 16" in hip.eahmmf_hip_last_error().decode()
+    # bulk staging: negative counts and null copies rejected up front, an empty batch is a no-op
+    assert hip.eahmmf_hip_h2d_batch(None, 0) == 0
+    assert hip.eahmmf_hip_h2d_batch(None, 1) == -1
+    assert hip.eahmmf_hip_h2d_batch(None, -1) == -1
+    bad = (binding.Copy * 1)(binding.Copy(None, x.ctypes.data, 16))
+    assert hip.eahmmf_hip_h2d_batch(bad, 1) == -1
+    assert "null pointer" in hip.eahmmf_hip_last_error().decode()
 
 
 @pytest.mark.parametrize("t,ne0", [(0, 64), (8, 96), (12, 2048), (13, 768), (14, 768), (14, 1536)])

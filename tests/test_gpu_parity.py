@@ -217,6 +217,23 @@ def test_stream_read_checksum(torch_dev, hip, nbytes):
     assert got == np.bitwise_xor.reduce(host)
 
 
+def test_h2d_batch_round_trip(torch_dev, binding, hip):
+    """Bulk staging through the pinned ring: copies from pageable numpy arrays
+    (a C2 layer's worth of expert components plus odd sizes spanning and
+    filling ring slots) land byte for byte."""
+    torch = torch_dev
+    rng = np.random.default_rng(11)
+    sizes = [884736, 884736, 1290240] * 8 + [1, 4097, 32 << 20, (40 << 20) + 123, 0]
+    host = [rng.integers(0, 256, n, dtype=np.uint8) for n in sizes]
+    dev = [torch.empty(max(n, 1), dtype=torch.uint8, device="cuda") for n in sizes]
+    copies = (binding.Copy * len(sizes))()
+    for i, n in enumerate(sizes):
+        copies[i] = binding.Copy(dev[i].data_ptr(), host[i].ctypes.data, n)
+    assert hip.eahmmf_hip_h2d_batch(copies, len(sizes)) == 0, hip.eahmmf_hip_last_error()
+    for h, d, n in zip(host, dev, sizes):
+        assert np.array_equal(d[:n].cpu().numpy(), h)
+
+
 def test_route_topk_vs_oracle(torch_dev, hip):
     rng = np.random.default_rng(3)
     nb, E, k = 257, 128, 8
