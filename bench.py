@@ -149,6 +149,85 @@ def bench_c4(args, torch, b, hip):
         "tflops": round(flop * steps / el / 1e12, 3)}), flush=True)
 
 
+def bench_c5_batch(args, torch, b, hip):
+    """The 16-sequence ragged decode batch at the Qwen3-235B-A22B expert shape:
+    16 decode tokens (one per sequence) through one MoE layer per step, routing
+    on the device from fresh ~N(0,1) logits, then eahmmf_hip_moe_grouped_async
+    (which runs a batch this small as one single-launch block per token).  Also
+    timed: the same step with the grouped kernels forced (fused launches off),
+    matrix-core and vector-ALU."""
+    D_, FF_, E_, K_, NB = 4096, 1536, 128, 8, 16
+    rng = np.random.default_rng(6)
+    uniq, grb, drb = build_layer_replicated(b, rng, D_, FF_, E_, 16)
+    R = args.replicas if args.replicas else 4
+    comps, tables = upload_layers(torch, uniq, E_, R)
+    shape = b.MoeShape(Q4_K, Q4_K, Q6_K, D_, FF_, grb, grb, drb)
+    NS = 16
+    dl = torch.from_numpy(rng.normal(0, 1, (NS, NB, E_)).astype(np.float32)).cuda()
+    dx = torch.from_numpy(rng.normal(0, 1, (NS, NB, D_)).astype(np.float32)).cuda()
+    dids = torch.empty((NS, NB, K_), dtype=torch.int32, device="cuda")
+    dw = torch.empty((NS, NB, K_), dtype=torch.float32, device="cuda")
+    dy = torch.empty((NS, NB, D_), dtype=torch.float32, device="cuda")
+    stream = torch.cuda.current_stream()
+    sp, vp = ctypes.c_void_p(stream.cuda_stream), ctypes.c_void_p
+    for i in range(NS):
+        assert hip.eahmmf_hip_route_topk_async(vp(dl[i].data_ptr()), NB, E_, K_, vp(dids[i].data_ptr()),
+                                               vp(dw[i].data_ptr()), sp) == 0
+    torch.cuda.synchronize()
+    ids = dids.cpu().numpy()
+    exp_bytes = 2 * FF_ * grb + D_ * drb
+    distinct = [len(np.unique(ids[i])) for i in range(NS)]
+
+    def step(i):  # routing + the batch's expert block, as a serving step runs it
+        s_ = i % NS
+        assert hip.eahmmf_hip_route_topk_async(vp(dl[s_].data_ptr()), NB, E_, K_, vp(dids[s_].data_ptr()),
+                                               vp(dw[s_].data_ptr()), sp) == 0
+        rc = hip.eahmmf_hip_moe_grouped_async(ctypes.byref(shape), vp(tables[i % R].data_ptr()), E_,
+                                              vp(dids[s_].data_ptr()), vp(dw[s_].data_ptr()), NB, K_,
+                                              vp(dx[s_].data_ptr()), vp(dy[s_].data_ptr()), sp)
+        assert rc == 0, b.last_error()
+
+    def timed(steps, warm):
+        for i in range(warm):
+            step(i)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for i in range(steps):
+            step(i)
+        e1.record(stream)
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) * 1e-3 / steps
+
+    steps = args.steps if args.steps else 100
+    t_api = timed(steps, args.warmup if args.warmup else 5)
+    fused_prev = hip.eahmmf_hip_set_fused(0)
+    t_mfma = timed(max(10, steps // 4), 2)
+    mfma_prev = hip.eahmmf_hip_set_grouped_mfma(0)
+    t_valu = timed(max(10, steps // 4), 2)
+    hip.eahmmf_hip_set_grouped_mfma(mfma_prev)
+    hip.eahmmf_hip_set_fused(fused_prev)
+    assert hip.eahmmf_hip_device_flags() == 0
+    read_bytes = NB * K_ * exp_bytes  # each token's experts, read per token
+    distinct_bytes = float(np.mean([d * exp_bytes for d in distinct]))
+    gbs = distinct_bytes / t_api / 1e9  # algorithmic: each distinct routed expert once
+    print(json.dumps({
+        "metric": "16-sequence decode batch expert-FFN HBM GB/s (% of peak), Qwen3-235B-A22B shape",
+        "value": round(gbs, 2), "unit": "GB/s", "n_gpus": 1, "steps": steps, "ms_per_step": round(t_api * 1e3, 4),
+        "higher_is_better": True, "dtype": "f32", "data": "synthetic",
+        "config": {"workload": "16 decode tokens (one per sequence) through one MoE layer, D=4096 FF=1536 "
+                               "128 experts top-8, Q4_K gate/up + Q6_K down, routing on device, "
+                               "eahmmf_hip_moe_grouped_async", "layer_replicas": R,
+                   "bytes_read_per_step": read_bytes, "distinct_experts_mean": round(float(np.mean(distinct)), 1),
+                   "distinct_expert_bytes_per_step": int(distinct_bytes)},
+        "pct_of_hbm_peak": round(100 * gbs / HBM_PEAK_GBS, 2),
+        "bytes_read_GB_s": round(read_bytes / t_api / 1e9, 2),
+        "expert_only_batch_tokens_per_s_94_layers": round(NB / (94 * t_api), 1),
+        "grouped_kernels_forced": {"matrix_core_ms": round(t_mfma * 1e3, 4), "vector_alu_ms": round(t_valu * 1e3, 4),
+                                   "what": "the same step with eahmmf_hip_set_fused(0) (grouping on the device, "
+                                           "each distinct expert read once)"}}), flush=True)
+
+
 def bench_c5(args, torch, b, hip):
     """Single decode token through one MoE layer at the Qwen3-235B-A22B expert
     shape (D=4096, FF=1536, 128 experts, top-8, Q4_K/Q6_K), routing on device."""
@@ -491,9 +570,10 @@ def main():
     ap.add_argument("--replicas", type=int, default=None, help="layer copies in HBM (c2 16, c4 4, c5 4)")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--workload", choices=("c2", "c3", "c4", "c5", "stream", "staging"), default="c2",
+    ap.add_argument("--workload", choices=("c2", "c3", "c4", "c5", "c5b16", "stream", "staging"), default="c2",
                     help="c2 (default): the headline single-token layer; c3: one token through 48 layers; "
                          "c4: ragged grouped prefill; c5: single-token layer at the 235B shape; "
+                         "c5b16: a 16-sequence decode batch at the 235B shape; "
                          "stream: the achievable HBM read rate (streaming-read kernel); "
                          "staging: making one layer's experts resident from host memory")
     ap.add_argument("--calibrate-copy", action="store_true",
@@ -516,7 +596,7 @@ def main():
     if args.workload != "c2":
         hip_ = b.lib()
         torch.cuda.set_device(0)
-        {"c3": bench_c3, "c4": bench_c4, "c5": bench_c5, "stream": bench_stream,
+        {"c3": bench_c3, "c4": bench_c4, "c5": bench_c5, "c5b16": bench_c5_batch, "stream": bench_stream,
          "staging": bench_staging}[args.workload](args, torch, b, hip_)
         return
     hip = b.lib()

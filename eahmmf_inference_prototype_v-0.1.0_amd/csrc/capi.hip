@@ -49,6 +49,9 @@ struct DeviceBuf {
     size_t cap = 0;
 };
 
+// Largest batch eahmmf_hip_moe_grouped_async runs as per-token fused launches.
+constexpr int kFusedBatchMax = 32;
+
 // Bulk staging ring: kRingSlots pinned slots of kRingChunk bytes each.
 constexpr int kRingSlots = 4;
 constexpr size_t kRingChunk = (size_t)32 << 20;
@@ -497,6 +500,33 @@ int eahmmf_hip_moe_grouped_async(const eahmmf_hip_moe_shape* shape, const eahmmf
                -1;
     DevCtx* c = ctx_for_current_device();
     if (!c) return -2;
+    // A decode batch of a few sequences runs as one fused launch per token
+    // (ids and weights as given): at one or two tokens per routed expert the
+    // grouped kernels' per-expert pipeline costs more than reading each
+    // token's experts on its own.  Measured for 1..32 tokens at D=2048/FF=768
+    // and D=4096/FF=1536 (top-8 of 128): per token 12.0 / 39.8 us each, the
+    // grouped block 433 / 1521 us at 32 tokens against 373 / 1268 us.
+    if (nb <= kFusedBatchMax && fused_enabled() && fused_supported(s, k, 0)) {
+        if (!grow_fused(c, s, k)) return -2;
+        for (int t = 0; t < nb; t++) {
+            FusedArgsHost f;
+            f.shape = s;
+            f.k = k;
+            f.n_expert = n_expert;
+            f.mode = 2;
+            f.table = (const ExpertEntry*)dev_table;
+            f.ids_in = dev_ids + (size_t)t * k;
+            f.w_in = dev_w + (size_t)t * k;
+            f.x = dev_x + (size_t)t * s.D;
+            f.y = dev_y + (size_t)t * s.D;
+            f.hx = (uint64_t*)c->dhx.p;
+            f.sync = c->dsync;
+            f.ypart = (uint64_t*)c->dyp.p;
+            f.epoch = ++c->epoch;
+            if (!hip_ok(launch_moe_fused(f, (hipStream_t)stream), "fused batch-decode launch")) return -3;
+        }
+        return 0;
+    }
     if (!grow_device(c->dgs, grouped_scratch_bytes(s, nb, k, n_expert))) return -2;
     return hip_ok(launch_moe_grouped(s, (const ExpertEntry*)dev_table, n_expert, dev_ids, dev_w, nb, k, dev_x, s.D,
                                      dev_y, s.D, c->dgs.p, (hipStream_t)stream),

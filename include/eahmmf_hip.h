@@ -128,9 +128,12 @@ bool eahmmf_hip_moe_grouped(const eahmmf_hip_expert* experts, int n_groups, cons
 /* Same with the routing on the device: dev_ids/dev_w [nb][k] (e.g. from
  * eahmmf_hip_route_topk_async; ids outside 0..n_expert-1 are skipped) over
  * the device table [n_expert <= 256]; dev_x/dev_y [nb][D], asynchronous on
- * `stream`.  The (token, expert) pairs are grouped on the device (stable, in
- * token order) and each token's results are added in ascending expert id,
- * as qwen3moe.cpp:1009-1067 does. */
+ * `stream`.  Above 32 tokens the (token, expert) pairs are grouped on the
+ * device (stable, in token order) and each token's results are added in
+ * ascending expert id, as qwen3moe.cpp:1009-1067 does.  A batch of up to 32
+ * tokens (a decode step of a few sequences) where the single-launch kernel
+ * covers the shape runs as one such launch per token instead, its results
+ * added in the routing's rank order (the same output tolerance). */
 int eahmmf_hip_moe_grouped_async(const eahmmf_hip_moe_shape* shape, const eahmmf_hip_expert_ptrs* dev_table,
                                  int n_expert, const int* dev_ids, const float* dev_w, int nb, int k,
                                  const float* dev_x, float* dev_y, void* stream);

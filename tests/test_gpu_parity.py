@@ -430,10 +430,13 @@ def test_grouped_vs_oracle(torch_dev, binding, hip, grouped_mode, name, types, D
     close(y, want)
 
 
-@pytest.mark.parametrize("nb,E,k,skew", [(64, 32, 8, 0.0), (200, 128, 8, 1.1), (1, 16, 4, 0.0), (129, 64, 6, 2.0)])
+@pytest.mark.parametrize("nb,E,k,skew", [(64, 32, 8, 0.0), (200, 128, 8, 1.1), (1, 16, 4, 0.0), (129, 64, 6, 2.0),
+                                         (16, 128, 8, 0.0), (32, 64, 8, 1.1), (33, 128, 8, 0.0)])
 def test_grouped_async_device_routing(torch_dev, binding, hip, grouped_mode, nb, E, k, skew):
     """Routing on the device (route_topk), grouping on the device, Zipf-skewed
-    expert popularity: y of every token matches the oracle on the same ids."""
+    expert popularity: y of every token matches the oracle on the same ids
+    (up to 32 tokens as per-token single-launch blocks, above as the grouped
+    block)."""
     torch = torch_dev
     D, FF = 512, 256
     types = (Q4_K, Q4_K, Q6_K)
