@@ -28,7 +28,7 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 PKG_DIR = os.path.join(ROOT, "eahmmf_inference_prototype_v-0.1.0_amd")
 HBM_PEAK_GBS = 8000.0
 D, FF, E, K = 2048, 768, 128, 8
-Q4_K, Q5_K, Q6_K = 12, 13, 14
+Q8_0, Q4_K, Q5_K, Q6_K = 8, 12, 13, 14
 COPY_BYTES = 256 << 20
 
 
@@ -391,14 +391,14 @@ def bench_c3(args, torch, b, hip):
     """Expert-only decode of one token through all 48 MoE layers of the
     Qwen3-30B-A3B shape (D=2048, FF=768, 128 experts, top-8), every layer
     resident at its own HBM addresses; one step = 48 layer launches (routing on
-    device).  Runs the Q4_K_M variant (Q4_K gate/up, Q6_K down) and the Q5_K
-    variant (all three components Q5_K)."""
+    device).  Runs the Q4_K_M variant (Q4_K gate/up, Q6_K down) and the
+    config's two variants, all three components Q5_K and all Q8_0."""
     D_, FF_, E_, K_, NL = 2048, 768, 128, 8, 48
     rng = np.random.default_rng(3)
     stream = torch.cuda.current_stream()
     sp, vp = ctypes.c_void_p(stream.cuda_stream), ctypes.c_void_p
     results = {}
-    for name, gt, dt in (("q4_k_m", Q4_K, Q6_K), ("q5_k", Q5_K, Q5_K)):
+    for name, gt, dt in (("q4_k_m", Q4_K, Q6_K), ("q5_k", Q5_K, Q5_K), ("q8_0", Q8_0, Q8_0)):
         uniq, grb, drb = build_layer_replicated(b, rng, D_, FF_, E_, 16, gt, dt)
         comps, tables = upload_layers(torch, uniq, E_, NL)  # 48 distinct layers in HBM
         shape = b.MoeShape(gt, gt, dt, D_, FF_, grb, grb, drb)
