@@ -534,6 +534,15 @@ struct PassRows {
     const uint8_t* u;
 };
 
+// Workgroup barrier that waits for this wave's LDS operations only
+// (lgkmcnt 0; vmcnt 63 and expcnt 7 leave copies in flight).
+__device__ __forceinline__ void barrier_lds() {
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __builtin_amdgcn_s_waitcnt(0xC07F);
+    __builtin_amdgcn_s_barrier();
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+
 // LDS flag or counter of the workgroup reaching v (acquire; bounded: the
 // waves it waits for always progress).
 __device__ __forceinline__ void wait_lds(const unsigned* c, unsigned v) {
@@ -650,11 +659,19 @@ __device__ void fused_body(const FusedArgs& a, FusedLds& L) {
         const int n16 = (int)(((((uintptr_t)src + (uintptr_t)n + 15) & ~(uintptr_t)15) - base) / 16);
         return base + (uintptr_t)min(ii * 64 + lane, n16 - 1) * 16;
     };
+    // Phase-B rounds alternate between two stages: round i's rows sit in
+    // stage_b (i even) or in the A waves' rings (i odd; free once every A
+    // wave has passed the barrier after its passes), so the next round's
+    // copies run while a round computes.
+    auto stage_of = [&](int r0) -> uint8_t* {
+        return (r0 / a.rows_round) & 1 ? &L.stage_a[0][0] : L.stage_b;
+    };
     // rounds after the first: all waves copy, one 1 KB instruction each in turn
     auto stage_round = [&](int r0, int rr) {
         const int ni = a.stride_b / 1024;
+        uint8_t* st = stage_of(r0);
         for (int e = 0; e < ep; e++)
-            for (int i = wave; i < ni; i += kWaves) lds_dma16(stage_src(e, i, r0, rr), L.stage_b + e * a.stride_b + i * 1024);
+            for (int i = wave; i < ni; i += kWaves) lds_dma16(stage_src(e, i, r0, rr), st + e * a.stride_b + i * 1024);
     };
     // round 0, B wave wb: exactly kDmaB instructions f = wb + 4i over the
     // experts' stage instructions in order (expert e's instruction ii lands at
@@ -674,21 +691,37 @@ __device__ void fused_body(const FusedArgs& a, FusedLds& L) {
     // Phase-B tasks of a round: (expert e of the partition, 64-value segment
     // sg, 64-row block); a lane is one row.  The B waves decode their first
     // NPD tasks of round 0 into registers before the barrier.
-    const int nrb0 = (rr0 + 63) / 64;
-    const int n_tasks0 = ep * segB * nrb0;
+    // When a round holds at most 32 rows (long down rows, e.g. 1260 B at
+    // FF=1536), a task is (expert, segment pair, the round's rows) instead:
+    // lanes 32..63 take the pair's second segment of the same rows, so no
+    // lane idles.  A lane past an odd segment count writes nothing.
+    const bool half = a.rows_round <= 32;
+    const int nsg = half ? (segB + 1) / 2 : segB;
+    auto n_tasks = [&](int rr) { return ep * nsg * (half ? 1 : (rr + 63) / 64); };
+    const int n_tasks0 = n_tasks(rr0);
     struct BTask {
         int e, sg, r;
         const uint8_t* row;
     };
     auto btask = [&](int task, int rr, int r0) {
-        const int nrb = (rr + 63) / 64;
+        const int nrb = half ? 1 : (rr + 63) / 64;
         BTask t;
-        t.e = task / (segB * nrb);
-        const int rest = task - t.e * (segB * nrb);
-        t.sg = rest / nrb;
-        t.r = (rest - t.sg * nrb) * 64 + lane;
+        t.e = task / (nsg * nrb);
+        const int rest = task - t.e * (nsg * nrb);
+        const int g = rest / nrb;
+        if (half) {
+            t.sg = 2 * g + (lane >> 5);
+            t.r = lane & 31;
+            if (t.sg >= segB) {
+                t.sg = segB - 1;
+                t.r = kThreads;  // beyond every round: no partial is written
+            }
+        } else {
+            t.sg = g;
+            t.r = (rest - g * nrb) * 64 + lane;
+        }
         const uint8_t* src = down_src(t.e, r0);  // rows [r0, r0 + rr) of the chunk are staged
-        t.row = L.stage_b + t.e * a.stride_b + ((uintptr_t)src & 15) + min(t.r, rr - 1) * drb;
+        t.row = stage_of(r0) + t.e * a.stride_b + ((uintptr_t)src & 15) + min(t.r, rr - 1) * drb;
         return t;
     };
 
@@ -791,13 +824,21 @@ __device__ void fused_body(const FusedArgs& a, FusedLds& L) {
     // Phase B rounds: every wave takes (expert, segment, 64-row block) tasks;
     // a lane is one row, so the h levels of the task are read by all lanes at
     // one address.
-    for (int r0 = 0; r0 < r_end - r_begin; r0 += a.rows_round) {
-        const int rr = min(a.rows_round, r_end - r_begin - r0);
+    const int nrows = r_end - r_begin;
+    for (int r0 = 0; r0 < nrows; r0 += a.rows_round) {
+        const int rr = min(a.rows_round, nrows - r0);
         if (r0 > 0) {
-            __syncthreads();  // the previous round's rows and partials are consumed
-            stage_round(r0, rr);
+            // this wave's copies of the round (issued a round ago) have
+            // landed; after the barrier everyone's have, and the previous
+            // round's rows and partials are consumed
             wait_vm();
             __syncthreads();
+        }
+        {
+            // the next round's copies go out now, into the stage the previous
+            // round has finished with (round 1: the A rings)
+            const int r1 = r0 + a.rows_round;
+            if (r1 < nrows) stage_round(r1, min(a.rows_round, nrows - r1));
         }
         auto finish = [&](const BTask& t, const SegCodes<DT>& k) {
             XSeg hs;  // the same address in every lane: one LDS broadcast per read
@@ -814,13 +855,15 @@ __device__ void fused_body(const FusedArgs& a, FusedLds& L) {
             }
             first = (kWaves - kAWaves) * NPD;
         }
-        for (int task = first + wave; task < ep * segB * ((rr + 63) / 64); task += kWaves) {
+        for (int task = first + wave; task < n_tasks(rr); task += kWaves) {
             const BTask t = btask(task, rr, r0);
             RawSeg<DT> raw;
             raw.template load<LdsLd>(t.row, t.sg);
             finish(t, raw.decode(t.sg));
         }
-        __syncthreads();
+        // the partials are in LDS; an LDS-only barrier leaves the next
+        // round's copies in flight (__syncthreads would wait for them)
+        barrier_lds();
         // fixed-order sum over the partition's (expert, segment) units, one
         // thread per row (float4 reads when segB is a multiple of 4)
         for (int r = tid; r < rr; r += kThreads) {

@@ -165,6 +165,7 @@ DECODE_CASES = [
     ("c3_q5_k", (Q5_K, Q5_K, Q5_K), 2048, 768, 8, 8),
     ("c3_q8_0", (Q8_0, Q8_0, Q8_0), 2048, 768, 8, 8),
     ("c5_q4_k_m", (Q4_K, Q4_K, Q6_K), 4096, 1536, 8, 8),
+    ("ff192_q8_0_odd_segments", (Q8_0, Q8_0, Q8_0), 512, 192, 8, 8),
 ]
 
 
