@@ -992,6 +992,9 @@ static FusedGrid fused_grid(const MoeShape& s, int k, int capacity) {
     int rr = g.rows_b;
     auto stride = [&](int rows) { return (rows * drb + 32 + 1023) / 1024 * 1024; };
     while (rr > 1 && (ep * stride(rr) > kStageB || ep * rr * (s.FF / 64) > kMaxPart)) rr--;
+    // more than one round: 32-row rounds, where a task's 64 lanes cover two
+    // segments of the rows and none idles
+    if (rr < g.rows_b && rr > 32) rr = 32;
     g.rows_round = rr;
     g.stride_b = stride(rr);
     return g;
