@@ -504,8 +504,8 @@ int eahmmf_hip_moe_grouped_async(const eahmmf_hip_moe_shape* shape, const eahmmf
     // (ids and weights as given): at one or two tokens per routed expert the
     // grouped kernels' per-expert pipeline costs more than reading each
     // token's experts on its own.  Measured for 1..32 tokens at D=2048/FF=768
-    // and D=4096/FF=1536 (top-8 of 128): per token 12.0 / 39.8 us each, the
-    // grouped block 433 / 1521 us at 32 tokens against 373 / 1268 us.
+    // and D=4096/FF=1536 (top-8 of 128): per token 12.2 / 30.4 us each; at 32
+    // tokens 374 / 971 us against 433 / 1520 us for the grouped block.
     if (nb <= kFusedBatchMax && fused_enabled() && fused_supported(s, k, 0)) {
         if (!grow_fused(c, s, k)) return -2;
         for (int t = 0; t < nb; t++) {
