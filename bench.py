@@ -584,8 +584,8 @@ def main():
         args.warmup = 100 if args.warmup is None else args.warmup
         args.replicas = 16 if args.replicas is None else args.replicas
     if args.gpus != 1:
-        print(f"bench.py runs on one GPU only (asked for --gpus {args.gpus}); the expert path shards by expert "
-              "across GPUs, which this build does not run", file=sys.stderr)
+        print(f"bench.py runs on one GPU only (asked for --gpus {args.gpus}); the expert path would shard by "
+              "expert across GPUs, and no multi-GPU run is made here", file=sys.stderr)
         sys.exit(2)
 
     import torch

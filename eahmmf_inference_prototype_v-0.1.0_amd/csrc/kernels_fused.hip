@@ -836,7 +836,7 @@ __device__ void fused_body(const FusedArgs& a, FusedLds& L) {
         }
         {
             // the next round's copies go out now, into the stage the previous
-            // round has finished with (round 1: the A rings)
+            // round has finished with (the second round's: the A rings)
             const int r1 = r0 + a.rows_round;
             if (r1 < nrows) stage_round(r1, min(a.rows_round, nrows - r1));
         }

@@ -1,6 +1,6 @@
 """HIP path vs the oracle, through the C ABI (MI355X).
 
-Bars (from the north star): dequantized weights and top-k expert ids
+Bars: dequantized weights and top-k expert ids
 bit-exact; outputs within 1e-3 relative / 1e-4 absolute of the oracle's fp32
 result: |gpu - oracle| <= 1e-4 + 1e-3 * |oracle| elementwise.
 """
