@@ -234,9 +234,18 @@ void fill_slot(uint8_t* slot, const std::vector<Piece>& ps, size_t total, int nt
     }
     const size_t per = ((total + nt - 1) / nt + 4095) & ~(size_t)4095;
     std::vector<std::thread> th;
-    for (int t = 1; t < nt && (size_t)t * per < total; t++)
-        th.emplace_back(range, (size_t)t * per, std::min(total, (size_t)(t + 1) * per));
+    size_t done = per;  // [0, done) is this thread's; the rest is handed out below
+    try {
+        for (int t = 1; t < nt && (size_t)t * per < total; t++) {
+            th.emplace_back(range, (size_t)t * per, std::min(total, (size_t)(t + 1) * per));
+            done = std::min(total, (size_t)(t + 1) * per);
+        }
+    } catch (...) {
+        // no thread could be started: the rest is copied here (no exception
+        // leaves the C ABI)
+    }
     range(0, std::min(total, per));
+    if (done < total) range(done, total);
     for (std::thread& x : th) x.join();
 }
 
