@@ -387,6 +387,57 @@ def bench_staging(args, torch, b, hip):
         "speedup": round(t_ref / t_batch, 2)}), flush=True)
 
 
+def bench_dropin(args, torch, b, hip):
+    """One C2 layer-token through the drop-in entry points, exactly as the
+    reference's host loop calls them (qwen3moe.cpp:1024-1067): per routed
+    expert eahmmf_hip_matmul_pair (gate/up, host x in, host g/u out), SiLU on
+    the host, eahmmf_hip_matmul (down), the weighted sum on the host; every
+    call synchronous with pageable host buffers.  Routing is taken as given."""
+    D_, FF_, E_, K_ = 2048, 768, 128, 8
+    rng = np.random.default_rng(7)
+    uniq, grb, drb = build_layer_replicated(b, rng, D_, FF_, E_, 16)
+    R = args.replicas if args.replicas else 4
+    comps, tables = upload_layers(torch, uniq, E_, R)
+    tab = [t.cpu().numpy().view(np.uint64) for t in tables]
+    NS = 16
+    xs = rng.normal(0, 1, (NS, D_)).astype(np.float32)
+    ids = np.stack([rng.choice(E_, K_, replace=False) for _ in range(NS)])
+    w = rng.uniform(0.05, 0.2, (NS, K_)).astype(np.float32)
+    g = np.empty(FF_, np.float32)
+    u = np.empty(FF_, np.float32)
+    yd = np.empty(D_, np.float32)
+
+    def token(i):
+        s_, r = i % NS, i % R
+        x = xs[s_]
+        y = np.zeros(D_, np.float32)
+        for j in sorted(range(K_), key=lambda jj: ids[s_, jj]):  # ascending expert id, as by_exp
+            gp, up, dp = (int(v) for v in tab[r][ids[s_, j]])
+            assert hip.eahmmf_hip_matmul_pair(gp, Q4_K, D_, FF_, grb, up, Q4_K, D_, FF_, grb, x.ctypes.data, 1, D_,
+                                              g.ctypes.data, FF_, u.ctypes.data, FF_), b.last_error()
+            h = (g / (1.0 + np.exp(-g)) * u).astype(np.float32)
+            assert hip.eahmmf_hip_matmul(dp, Q6_K, FF_, D_, drb, h.ctypes.data, 1, FF_, yd.ctypes.data, D_), \
+                b.last_error()
+            y += w[s_, j] * yd
+
+    steps = args.steps if args.steps else 300
+    for i in range(10):
+        token(i)
+    t0 = time.perf_counter()
+    for i in range(steps):
+        token(i)
+    el = (time.perf_counter() - t0) / steps
+    bytes_step = K_ * (2 * FF_ * grb + D_ * drb)
+    print(json.dumps({
+        "metric": "expert-FFN HBM GB/s through the drop-in matmul entry points (reference calling pattern)",
+        "value": round(bytes_step / el / 1e9, 2), "unit": "GB/s", "n_gpus": 1, "steps": steps,
+        "ms_per_step": round(el * 1e3, 4), "higher_is_better": True, "dtype": "f32", "data": "synthetic",
+        "config": {"workload": "one C2 layer-token (D=2048 FF=768, 8 routed experts, Q4_K gate/up + Q6_K down) as "
+                               "8 x (eahmmf_hip_matmul_pair + host SiLU + eahmmf_hip_matmul), synchronous, pageable "
+                               "host buffers", "bytes_per_step": bytes_step, "calls_per_step": 2 * K_},
+        "us_per_call": round(el * 1e6 / (2 * K_), 2)}), flush=True)
+
+
 def bench_c3(args, torch, b, hip):
     """Expert-only decode of one token through all 48 MoE layers of the
     Qwen3-30B-A3B shape (D=2048, FF=768, 128 experts, top-8), every layer
@@ -570,12 +621,13 @@ def main():
     ap.add_argument("--replicas", type=int, default=None, help="layer copies in HBM (c2 16, c4 4, c5 4)")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--workload", choices=("c2", "c3", "c4", "c5", "c5b16", "stream", "staging"), default="c2",
+    ap.add_argument("--workload", choices=("c2", "c3", "c4", "c5", "c5b16", "stream", "staging", "dropin"), default="c2",
                     help="c2 (default): the headline single-token layer; c3: one token through 48 layers; "
                          "c4: ragged grouped prefill; c5: single-token layer at the 235B shape; "
                          "c5b16: a 16-sequence decode batch at the 235B shape; "
                          "stream: the achievable HBM read rate (streaming-read kernel); "
-                         "staging: making one layer's experts resident from host memory")
+                         "staging: making one layer's experts resident from host memory; "
+                         "dropin: a C2 layer-token through the drop-in matmul calls")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a plain 256 MiB device copy (the reference kernel for scaling HBM counters)")
     args = ap.parse_args()
@@ -597,7 +649,7 @@ def main():
         hip_ = b.lib()
         torch.cuda.set_device(0)
         {"c3": bench_c3, "c4": bench_c4, "c5": bench_c5, "c5b16": bench_c5_batch, "stream": bench_stream,
-         "staging": bench_staging}[args.workload](args, torch, b, hip_)
+         "staging": bench_staging, "dropin": bench_dropin}[args.workload](args, torch, b, hip_)
         return
     hip = b.lib()
     torch.cuda.set_device(0)
