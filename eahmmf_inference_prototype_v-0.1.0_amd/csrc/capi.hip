@@ -60,8 +60,8 @@ struct DevCtx {
     hipStream_t stream = nullptr;
     DeviceBuf dx, dy, dy2, dh, dids, dw, dyp, dhx, dgs, dtab;  // device scratch
     DeviceBuf px, py, py2;                // pinned host staging
-    unsigned* dsync = nullptr;            // fused-launch counters and flags (zeroed once)
-    unsigned epoch = 0;                   // fused launches issued on dsync
+    unsigned* dsync = nullptr;            // fused-launch error word and ticket counters (zeroed once)
+    FusedState fused;                     // the fused kernel's scratch set (dhx, dyp, dsync) and epochs
     // bulk host-to-device staging (eahmmf_hip_h2d_batch), created on first use
     hipStream_t copy_stream[kRingSlots] = {};  // one per slot: slots drain on parallel DMA engines
     uint8_t* ring[kRingSlots] = {};
@@ -98,6 +98,7 @@ DevCtx* ctx_for_current_device() {
             return nullptr;
         }
         c.dsync = (unsigned*)p;
+        c.fused.sync = c.dsync;
     }
     return &c;
 }
@@ -177,8 +178,37 @@ static bool grow_zeroed(DeviceBuf& b, size_t need) {
 }
 
 bool grow_fused(DevCtx* c, const MoeShape& s, int k) {
-    return grow_zeroed(c->dyp, (size_t)8 * s.D * sizeof(uint64_t)) &&
-           grow_zeroed(c->dhx, (size_t)k * s.FF * sizeof(uint64_t));
+    if (!grow_zeroed(c->dyp, (size_t)8 * s.D * sizeof(uint64_t)) ||
+        !grow_zeroed(c->dhx, (size_t)k * s.FF * sizeof(uint64_t)))
+        return false;
+    c->fused.hx = (uint64_t*)c->dhx.p;
+    c->fused.hx_words = c->dhx.cap / sizeof(uint64_t);
+    c->fused.ypart = (uint64_t*)c->dyp.p;
+    c->fused.ypart_words = c->dyp.cap / sizeof(uint64_t);
+    return true;
+}
+
+// Synchronous entry points read the fused kernel's error word with their
+// output: one 4-byte copy queued behind the output's, into pinned staging
+// next to it, so no extra synchronisation is needed.
+bool queue_flag_read(DevCtx* c, void* host_slot) {
+    return hip_ok(hipMemcpyAsync(host_slot, c->dsync + kSyncFlagWord, sizeof(unsigned), hipMemcpyDeviceToHost,
+                                 c->stream),
+                  "hipMemcpyAsync(error word)");
+}
+
+// After the drain: an error word equal to the call's own launch epoch means
+// that launch gave up a wait and its output is invalid (NaN where words were
+// missing).  The call then fails, as the reference's ABI does on any GPU
+// error (expert_cuda.cu:332-335), and the ticket counters are reset for the
+// next launch.  The word itself stays set for eahmmf_hip_device_flags(); a
+// later launch compares it with its own epoch, so it does not fail them.
+bool flag_ok(DevCtx* c, unsigned v, unsigned epoch) {
+    if (v != epoch) return true;
+    set_error("fused expert block: a bounded wait gave up (launch %u); output invalid", v);
+    (void)reset_fused_sync(c->fused, c->stream, false);
+    (void)hipStreamSynchronize(c->stream);
+    return false;
 }
 
 bool weight_ok(const eahmmf_hip_weight& w) { return w.dev && type_supported(w.type) && w.ne0 > 0 && w.ne1 > 0; }
@@ -338,8 +368,10 @@ bool eahmmf_hip_moe_decode(const eahmmf_hip_expert* experts, const float* w, int
     DevCtx* c = ctx_for_current_device();
     if (!c) return false;
     const size_t ybytes = (size_t)s.D * sizeof(float);
-    bool ok = grow_device(c->dy, ybytes) && grow_pinned(c->py, ybytes) &&
+    const size_t flag_at = (ybytes + 255) & ~(size_t)255;  // the error word's pinned slot
+    bool ok = grow_device(c->dy, ybytes) && grow_pinned(c->py, flag_at + 256) &&
               grow_device(c->dh, (size_t)k * s.FF * sizeof(float)) && stage_x(c, host_x, 1, s.D, s.D);
+    bool fused = false;
     if (ok) {
         if (fused_enabled() && fused_supported(s, k, 0) && grow_fused(c, s, k)) {
             FusedArgsHost f;
@@ -349,20 +381,25 @@ bool eahmmf_hip_moe_decode(const eahmmf_hip_expert* experts, const float* w, int
             f.direct = slots;
             f.x = (const float*)c->dx.p;
             f.y = (float*)c->dy.p;
-            f.hx = (uint64_t*)c->dhx.p;
-            f.sync = c->dsync;
-            f.ypart = (uint64_t*)c->dyp.p;
-            f.epoch = ++c->epoch;
-            ok = hip_ok(launch_moe_fused(f, c->stream), "fused moe decode launch");
+            fused = true;
+            ok = hip_ok(launch_moe_fused(f, c->fused, c->stream), "fused moe decode launch");
         } else {
             ok = hip_ok(launch_moe_decode(s, slots, (const float*)c->dx.p, (float*)c->dh.p, (float*)c->dy.p,
                                           c->stream), "moe decode launch");
         }
     }
+    unsigned* flag = (unsigned*)((uint8_t*)c->py.p + flag_at);
     if (ok) ok = hip_ok(hipMemcpyAsync(c->py.p, c->dy.p, ybytes, hipMemcpyDeviceToHost, c->stream), "copy y");
+    if (ok && fused) {
+        *flag = 0;
+        ok = queue_flag_read(c, flag);
+    }
     ok = drain(c, ok);
-    if (ok) memcpy(host_y, c->py.p, ybytes);
-    return ok;
+    if (!ok) return false;
+    // also after a wait gave up: y then holds NaN where it is invalid, so a
+    // caller that ignores the return value still cannot take it for a result
+    memcpy(host_y, c->py.p, ybytes);
+    return fused ? flag_ok(c, *flag, c->fused.epoch) : true;
 }
 
 static bool shape_from_abi(const eahmmf_hip_moe_shape* sh, MoeShape& s) {
@@ -406,11 +443,7 @@ int eahmmf_hip_moe_decode_async(const eahmmf_hip_moe_shape* shape, const eahmmf_
         f.direct = slots;
         f.x = dev_x;
         f.y = dev_y;
-        f.hx = (uint64_t*)c->dhx.p;
-        f.sync = c->dsync;
-        f.ypart = (uint64_t*)c->dyp.p;
-        f.epoch = ++c->epoch;
-        return hip_ok(launch_moe_fused(f, (hipStream_t)stream), "fused moe decode launch") ? 0 : -3;
+        return hip_ok(launch_moe_fused(f, c->fused, (hipStream_t)stream), "fused moe decode launch") ? 0 : -3;
     }
     if (!hip_ok(launch_moe_decode(s, slots, dev_x, (float*)c->dh.p, dev_y, (hipStream_t)stream), "moe decode launch"))
         return -3;
@@ -439,11 +472,7 @@ int eahmmf_hip_moe_decode_routed_async(const eahmmf_hip_moe_shape* shape, const 
         f.w_in = dev_w;
         f.x = dev_x;
         f.y = dev_y;
-        f.hx = (uint64_t*)c->dhx.p;
-        f.sync = c->dsync;
-        f.ypart = (uint64_t*)c->dyp.p;
-        f.epoch = ++c->epoch;
-        return hip_ok(launch_moe_fused(f, (hipStream_t)stream), "fused routed moe decode launch") ? 0 : -3;
+        return hip_ok(launch_moe_fused(f, c->fused, (hipStream_t)stream), "fused routed moe decode launch") ? 0 : -3;
     }
     if (!hip_ok(launch_moe_decode_routed(s, (const ExpertEntry*)dev_table, n_expert, dev_ids, dev_w, k, dev_x,
                                          (float*)c->dh.p, dev_y, (hipStream_t)stream),
@@ -476,11 +505,7 @@ int eahmmf_hip_moe_layer_decode_async(const eahmmf_hip_moe_shape* shape, const e
         f.w_out = dev_w_out;
         f.x = dev_x;
         f.y = dev_y;
-        f.hx = (uint64_t*)c->dhx.p;
-        f.sync = c->dsync;
-        f.ypart = (uint64_t*)c->dyp.p;
-        f.epoch = ++c->epoch;
-        return hip_ok(launch_moe_fused(f, st), "fused moe layer launch") ? 0 : -3;
+        return hip_ok(launch_moe_fused(f, c->fused, st), "fused moe layer launch") ? 0 : -3;
     }
     // two-step path: routing kernel into scratch (or the caller's buffers), then the expert block
     int* ids = dev_ids_out;
@@ -528,11 +553,7 @@ int eahmmf_hip_moe_grouped_async(const eahmmf_hip_moe_shape* shape, const eahmmf
             f.w_in = dev_w + (size_t)t * k;
             f.x = dev_x + (size_t)t * s.D;
             f.y = dev_y + (size_t)t * s.D;
-            f.hx = (uint64_t*)c->dhx.p;
-            f.sync = c->dsync;
-            f.ypart = (uint64_t*)c->dyp.p;
-            f.epoch = ++c->epoch;
-            if (!hip_ok(launch_moe_fused(f, (hipStream_t)stream), "fused batch-decode launch")) return -3;
+            if (!hip_ok(launch_moe_fused(f, c->fused, (hipStream_t)stream), "fused batch-decode launch")) return -3;
         }
         return 0;
     }
@@ -636,10 +657,25 @@ int eahmmf_hip_device_flags(void) {
     if (!hip_ok(hipMemcpy(&v, c->dsync + kSyncFlagWord, sizeof v, hipMemcpyDeviceToHost), "read device flags"))
         return -2;
     if (v) {
-        const unsigned zero = 0;
-        (void)hipMemcpy(c->dsync + kSyncFlagWord, &zero, sizeof zero, hipMemcpyHostToDevice);
+        (void)reset_fused_sync(c->fused, c->stream, true);
+        (void)hipStreamSynchronize(c->stream);
     }
-    return (int)v;
+    return v ? 1 : 0;
+}
+
+int eahmmf_hip_fused_status_async(unsigned* dst, void* stream) {
+    if (!dst) return set_error("null argument"), -1;
+    DevCtx* c = ctx_for_current_device();
+    if (!c) return -2;
+    return hip_ok(hipMemcpyAsync(dst, c->dsync + kSyncFlagWord, sizeof(unsigned), hipMemcpyDefault,
+                                 (hipStream_t)stream),
+                  "hipMemcpyAsync(error word)")
+               ? 0
+               : -3;
+}
+
+void eahmmf_hip_set_fault_injection(unsigned spin_limit, int drop_partition) {
+    set_fused_fault_injection(spin_limit, drop_partition);
 }
 
 bool eahmmf_hip_route_topk(const float* host_logits, int nb, int n_expert, int k, int* host_ids, float* host_w) {

@@ -62,19 +62,50 @@ struct FusedArgsHost {
     float* w_out = nullptr;
     const float* x = nullptr;
     float* y = nullptr;
-    uint64_t* hx = nullptr;       // k * FF exchange words (h value | epoch << 32), zeroed when allocated
-    uint64_t* ypart = nullptr;    // 8 * D exchange words: per-partition partial outputs, zeroed when allocated
-    unsigned* sync = nullptr;     // kSyncWords words, zero before the first launch (error flag)
-    unsigned epoch = 0;           // launch number on these buffers, starting at 1
 };
+
+// Sync buffer of a fused scratch set: kSyncWords words, zero before the first
+// launch.  Word kSyncFlagWord is the error word (the epoch of the last launch
+// whose bounded wait gave up, 0 if none); the eight per-XCD ticket counters
+// sit kTicketStride words apart (one 128-byte line each) from kTicketWord.
 constexpr int kSyncWords = 4096;
-constexpr int kSyncFlagWord = 1020;  // error flag word inside the sync buffer
+constexpr int kSyncFlagWord = 1020;
+constexpr int kTicketWord = 1024;
+constexpr int kTicketStride = 32;
+
+// One set of the fused kernel's scratch and its launch bookkeeping.  The
+// exchange words (h and the per-partition partials) carry the epoch of the
+// launch that wrote them, so they are zeroed once, when allocated, and never
+// again; every launch on the set gets a new epoch.
+struct FusedState {
+    uint64_t* hx = nullptr;     // hx_words words: h value bits | epoch << 32
+    size_t hx_words = 0;
+    uint64_t* ypart = nullptr;  // ypart_words words: 8 partitions x D partials, same form
+    size_t ypart_words = 0;
+    unsigned* sync = nullptr;   // kSyncWords words
+    unsigned epoch = 0;         // epoch of the last launch (0: none yet; launches skip 0 when it wraps)
+    unsigned ticket_base = 0;   // tickets each XCD counter handed out so far
+};
+
 bool fused_supported(const MoeShape& s, int k, int n_expert_for_routing);
 // 1 if the fused kernel's partitions exchange h through their own XCD's L2 on
-// this device (workgroup b runs on XCD b % 8), 0 if it uses the
+// this device (eight XCDs, a launch spread evenly over them), 0 if it uses the
 // device-coherent protocol.
 int fused_exchange_mode(int device);
-hipError_t launch_moe_fused(const FusedArgsHost& h, hipStream_t st);
+// The same, running the one-time placement probe (first call per device) with
+// probe_buf (4 KiB of device memory) instead of a buffer of its own.
+int fused_exchange_probe(int device, int* probe_buf);
+// Enqueues one fused launch on st with the next epoch of `fs`; its scratch
+// must hold k * FF h words and 8 * D partials.
+hipError_t launch_moe_fused(const FusedArgsHost& h, FusedState& fs, hipStream_t st);
+// Enqueues the reset of fs's ticket counters, and of its error word when
+// clear_error (a fill kernel, no memset node), and restarts the host's ticket
+// count; after a launch whose wait gave up.
+hipError_t reset_fused_sync(FusedState& fs, hipStream_t st, bool clear_error);
+// Test knobs of the fused kernel (0 / -1 restore the defaults): the polls
+// before a wait gives up, and one partition whose h words are never stored,
+// so that the kernel's own bounded waits give up.
+void set_fused_fault_injection(unsigned spin_limit, int drop_partition);
 
 // Ragged grouped expert block (kernels_grouped.hip): nb tokens routed by
 // ids/w [nb][k] over table [n_expert]; x [nb][ldx] -> y [nb][ldy].  scratch
@@ -107,6 +138,7 @@ hipError_t launch_route_topk(const float* logits, int nb, int n_expert, int k, i
 hipError_t launch_stream_read(const void* buf, size_t bytes, uint32_t* sink, hipStream_t st);
 
 bool moe_shape_ok(const MoeShape& s);
+
 bool type_supported(int t);
 
 }  // namespace eahmmf

@@ -14,14 +14,14 @@
 // with the arithmetic done from LDS as the bytes land.
 //
 // Layout of the work.  The routed experts are split into NP partitions (one
-// expert each for k <= 8, k/8 each for k = 16); workgroup b is rank q = b / NP
-// inside its partition.  With NP = 8 the partition is the XCD the workgroup
-// runs on (hardware XCC id): the dispatcher hands consecutive workgroups to
-// the eight XCDs in turn, starting wherever the previous launch stopped, so
-// workgroups b, b+8, b+16, ... share one XCD (checked once per device) and a
-// partition's h is exchanged through that XCD's L2.  Otherwise workgroup b
-// belongs to partition b % NP and h travels with device-coherent stores and
-// loads.
+// expert each for k <= 8, k/8 each for k = 16); each workgroup is rank q
+// inside its partition p.  With NP = 8 on a device whose dispatcher hands
+// consecutive workgroups to its eight XCDs in turn (checked once per device),
+// the partition is the XCD the workgroup runs on (hardware XCC id) and q is
+// b / 8, or optionally a ticket (the workgroup's position in its XCD's
+// arrival order, one atomic add on a per-XCD counter), so a partition's h is
+// exchanged through that XCD's L2.  Otherwise workgroup b is rank b / NP of
+// partition b % NP and h travels with device-coherent stores and loads.
 //
 // Per workgroup (waves 0-3 "A", waves 4-7 "B"):
 //   1. routing: wave 0 reads the logits and the expert table and forms the
@@ -55,8 +55,17 @@
 //      (deterministic) into y.
 // Nothing is reset between launches: a word is current exactly when it
 // carries this launch's epoch (launches are numbered from 1 and the exchange
-// buffers are zeroed when allocated).  Every wait is bounded; if a bound is
-// ever hit an error flag is raised and the kernel still exits.
+// buffers are zeroed when allocated).
+//
+// Failure is loud.  Every wait is bounded (spin_limit polls) and also ends as
+// soon as the launch's error word holds this launch's epoch.  A workgroup
+// whose wait gave up stores NaN in place of everything that depended on the
+// missing words (its partials; y rows whose partials never came), and the
+// error word records the epoch, so the host's synchronous entry points
+// return false and the caller falls back (the reference's contract for a
+// failed GPU call).  The kernel still exits normally.
+#include <stdlib.h>
+
 #include <mutex>
 
 #include "internal.h"
@@ -77,7 +86,6 @@ constexpr int NPD = 2;           // phase-B tasks each B wave decodes before the
 constexpr int kSlotA = 20 * 1024;   // LDS ring of one A wave
 constexpr int kStageB = 40 * 1024;  // LDS for one round of down rows
 constexpr int kDmaB = kStageB / 1024 / (kWaves - kAWaves);  // round-0 down copies per B wave
-constexpr unsigned kSpinLimit = 1u << 22;
 
 // One A pass: GW rows of gate and GW rows of up, GW * row bytes =
 // 4096 * (bytes per value) whatever D is.  NIR DMA instructions per matrix
@@ -92,19 +100,27 @@ struct PassA {
     static_assert(n >= 1, "an A pass must fit the ring");
 };
 
-constexpr int kSyncErr = kSyncFlagWord;  // the only word of the sync buffer this kernel uses
+constexpr int kSyncErr = kSyncFlagWord;  // error word: epoch of the last launch whose wait gave up
 
+// Kernel arguments.  The kernel rereads fields from the argument block where
+// it uses them, so the fields every launch uses are packed into the first
+// three 64-byte lines: the shape as ints, the knobs in one flags word.
 struct FusedArgs {
-    MoeShape s;
-    int k, n_expert, mode;  // mode 0: direct slots, 1: logits + table, 2: ids/w + table
-    int np, m;              // partitions and workgroups per partition
-    int rows_b;             // output rows per workgroup (chunk)
-    int rows_a;             // (expert, row) pairs of gate/up per workgroup, a multiple of the A lane groups
-    int rows_round;         // output rows staged per phase-B round
-    int stride_b;           // LDS bytes per expert in the phase-B stage (multiple of 1024)
-    int rank_shift, rank_c;  // routing: log2 of the threads per candidate, keys each of them compares
-    int local_l2;            // 1: partition p runs on XCD p, so h is exchanged through that XCD's L2
-    unsigned epoch;          // launch number (>= 1): the high word of this launch's exchange words
+    int D, FF, grb, urb, drb;  // shape: model width, expert FF, gate/up/down row bytes
+    int k, n_expert, mode;     // mode 0: direct slots, 1: logits + table, 2: ids/w + table
+    int np, m;                 // partitions and workgroups per partition
+    int rows_b;                // output rows per workgroup (chunk)
+    int rows_a;                // (expert, row) pairs of gate/up per workgroup, a multiple of the A lane groups
+    int rows_round;            // output rows staged per phase-B round
+    int stride_b;              // LDS bytes per expert in the phase-B stage (multiple of 1024)
+    int rank_shift, rank_c;    // routing: log2 of the threads per candidate, keys each of them compares
+    int local_l2;              // 1: partition p runs on XCD p, so h is exchanged through that XCD's L2
+    // bits 0-3: 1 + the partition whose h words are never stored (test knob, 0: none); bit 4: rank by
+    // ticket (else by b / np); bit 5: h words device-coherent also within an XCD; bits 8-31: polls
+    // before a wait gives up (0: kDefaultSpinLimit)
+    unsigned flags;
+    unsigned epoch;        // launch number (>= 1): the high word of this launch's exchange words
+    unsigned ticket_base;  // local_l2: tickets every XCD's counter handed out before this launch
     const ExpertEntry* table;
     const float* logits;
     const int* ids_in;
@@ -116,10 +132,15 @@ struct FusedArgs {
     uint64_t* hx;     // k * FF words: h value bits | epoch << 32
     uint64_t* ypart;  // np * D words: partial value bits | epoch << 32
     unsigned* sync;
-    // last: read only in mode 0, so the fields above share the first few
-    // cache lines of the argument block (the kernel rereads them as it goes)
+    // last: read only in mode 0
     DecodeSlots direct;
 };
+constexpr unsigned kDefaultSpinLimit = 1u << 18;  // polls: a wait gives up after about 0.1-0.3 s
+constexpr unsigned kFlagTicket = 1u << 4, kFlagHAgent = 1u << 5, kFlagTicketL2 = 1u << 6;
+__device__ __forceinline__ unsigned spin_limit_of(unsigned flags) {
+    const unsigned v = flags >> 8;
+    return v ? v : kDefaultSpinLimit;
+}
 
 template <int CTRL, int ROWS>
 __device__ __forceinline__ float dpp_fmax_step(float a, float fill) {
@@ -160,8 +181,16 @@ __device__ __forceinline__ uint64_t load_word(const uint64_t* p) {
     return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-__device__ __forceinline__ void raise_error(unsigned* sync, unsigned code) {
-    __hip_atomic_store(&sync[kSyncErr], code, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+__device__ __forceinline__ void raise_error(unsigned* sync, unsigned epoch) {
+    __hip_atomic_store(&sync[kSyncErr], epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// The error word is read on every (kErrPoll + 1)-th poll of a wait only: a
+// load of it on every poll lengthened each poll (a line nobody else touches,
+// read device-coherent), and a launch whose wait gave up still ends within
+// kErrPoll + 1 polls of every other wait.
+constexpr unsigned kErrPoll = 31;
+__device__ __forceinline__ unsigned load_error(const unsigned* sync) {
+    return __hip_atomic_load(&sync[kSyncErr], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // XCD (XCC) the calling wave runs on: hardware register HW_REG_XCC_ID (20),
@@ -228,6 +257,8 @@ struct alignas(16) FusedLds {
     unsigned a_issued;  // A waves whose first passes are issued (the down copies go out after them)
     unsigned xs_read;   // A waves that have read their activation levels
     unsigned b_landed;  // B waves whose round-0 down copies have landed
+    unsigned ticket;    // local_l2: this workgroup's rank in its XCD's arrival order
+    unsigned bad;       // a wait of this workgroup gave up: its results are NaN
 };
 
 // Activation levels.  n fp32 values (n % 64 == 0) become 3 int8 levels per
@@ -250,24 +281,27 @@ __device__ __forceinline__ void load8(const float* src, int seg, int part, bool 
 }
 
 // The same from exchange words, polled until all eight carry this launch's
-// epoch (bounded: on a timeout the error flag is raised and the values are
-// used as they are).
-__device__ __forceinline__ void load8_words(const uint64_t* src, int seg, int part, bool active, unsigned epoch,
-                                            unsigned* sync, float (&v)[8]) {
+// epoch.  Bounded: after spin_limit polls, or once the error word holds this
+// epoch, it gives up (raising the error) and returns false.
+__device__ __forceinline__ bool load8_words(const uint64_t* src, int seg, int part, bool active, unsigned epoch,
+                                            unsigned* sync, unsigned spin_limit, float (&v)[8]) {
     uint64_t w[8];
 #pragma unroll
     for (int i = 0; i < 8; i++) w[i] = 0;
+    bool good = true;
     if (active) {
         const uint64_t* sp = src + seg * 64 + part * 8;
         for (unsigned spins = 0;; spins++) {
 #pragma unroll
             for (int i = 0; i < 8; i++) w[i] = load_word(sp + i);
+            const unsigned err = (spins & kErrPoll) == kErrPoll ? load_error(sync) : 0u;
             bool ok = true;
 #pragma unroll
             for (int i = 0; i < 8; i++) ok &= (unsigned)(w[i] >> 32) == epoch;
             if (ok) break;
-            if (spins == kSpinLimit) {
-                raise_error(sync, 1u);
+            if (err == epoch || spins >= spin_limit) {
+                raise_error(sync, epoch);
+                good = false;
                 break;
             }
             __builtin_amdgcn_s_sleep(1);
@@ -275,6 +309,7 @@ __device__ __forceinline__ void load8_words(const uint64_t* src, int seg, int pa
     }
 #pragma unroll
     for (int i = 0; i < 8; i++) v[i] = __builtin_bit_cast(float, (uint32_t)w[i]);
+    return good;
 }
 
 // Levels of the eight values v of segment seg; every lane of the wave calls it
@@ -322,16 +357,18 @@ __device__ __forceinline__ void quantize8(const float (&v)[8], int seg, int part
 }
 
 // Levels of n values held as exchange words, by threads t in [0, nthr) (nthr
-// a multiple of 64).
-__device__ void quantize_words(const uint64_t* src, int n, unsigned epoch, unsigned* sync, int8_t* q, int qstride,
-                               float* sc, int scstride, float* s32, int t, int nthr) {
+// a multiple of 64).  False if a wait gave up.
+__device__ bool quantize_words(const uint64_t* src, int n, unsigned epoch, unsigned* sync, unsigned spin_limit,
+                               int8_t* q, int qstride, float* sc, int scstride, float* s32, int t, int nthr) {
     const int nseg = n / 64;
+    bool good = true;
     for (int base = 0; base < nseg; base += nthr / 8) {
         const int seg = base + t / 8, part = t % 8;
         float v[8];
-        load8_words(src, seg, part, seg < nseg, epoch, sync, v);
+        good &= load8_words(src, seg, part, seg < nseg, epoch, sync, spin_limit, v);
         quantize8(v, seg, part, seg < nseg, q, qstride, sc, scstride, s32);
     }
+    return good;
 }
 
 // The activation levels of segment g (64 values) held by one lane.
@@ -357,7 +394,8 @@ __device__ __forceinline__ void load_xseg(XSeg& xs, const int8_t* q, int qstride
 // e_i's bits + 1 in the high word (non-negative floats order as their bits;
 // 0 for a NaN e_i and for ids past n_expert up to 256) and ~i in the low
 // word, so keys are distinct and order exactly as (e desc, id asc).
-__device__ void route_keys(const FusedArgs& a, FusedLds& L, int lane) {
+template <class After>
+__device__ void route_keys(const FusedArgs& a, FusedLds& L, int lane, After after_loads) {
     const int n = a.n_expert;
     // every global load of this step goes out before the first use
     float l[4];
@@ -368,6 +406,7 @@ __device__ void route_keys(const FusedArgs& a, FusedLds& L, int lane) {
         l[c] = id < n ? a.logits[id] : -INFINITY;
         ent[c] = id < n ? a.table[id] : ExpertEntry{nullptr, nullptr, nullptr};
     }
+    after_loads();
     float mx = fmaxf(fmaxf(l[0], l[1]), fmaxf(l[2], l[3]));
     mx = dpp_max(mx);
 #pragma unroll
@@ -492,20 +531,21 @@ __device__ __forceinline__ const uint8_t* slot_ptr(const FusedLds& L, int j, int
 
 // ypart[0][r] + ... + ypart[np-1][r] (np <= 8) in partition order, once
 // every partial carries this launch's epoch (all loads of a poll in flight
-// together; bounded like every wait).
+// together).  Bounded like every wait: NaN when it gives up.
 __device__ __forceinline__ float reduce_row(const uint64_t* ypart, int D, int r, int np, unsigned epoch,
-                                            unsigned* sync) {
+                                            unsigned* sync, unsigned spin_limit) {
     uint64_t v[8];
     for (unsigned spins = 0;; spins++) {
 #pragma unroll
         for (int pp = 0; pp < 8; pp++) v[pp] = pp < np ? load_word(&ypart[pp * D + r]) : ((uint64_t)epoch << 32);
+        const unsigned err = (spins & kErrPoll) == kErrPoll ? load_error(sync) : 0u;
         bool ok = true;
 #pragma unroll
         for (int pp = 0; pp < 8; pp++) ok &= (unsigned)(v[pp] >> 32) == epoch;
         if (ok) break;
-        if (spins == kSpinLimit) {
-            raise_error(sync, 1u);
-            break;
+        if (err == epoch || spins >= spin_limit) {
+            raise_error(sync, epoch);
+            return __builtin_nanf("");
         }
         __builtin_amdgcn_s_sleep(1);
     }
@@ -561,19 +601,32 @@ __device__ void fused_body(const FusedArgs& a, FusedLds& L) {
     constexpr int NPA = PA::n;
     const int tid = threadIdx.x;
     const int wave = __builtin_amdgcn_readfirstlane(tid / 64), lane = tid % 64;
-    const MoeShape& s = a.s;
-    const int D = s.D, FF = s.FF, k = a.k;
+    const int D = a.D, FF = a.FF, k = a.k;
     const int np = a.np;
     const int xcc = a.local_l2 ? xcc_id() : 0;
-    const bool xcc_bad = xcc >= np;  // never on a device that passed the host's placement check
-    const int p = a.local_l2 ? (xcc_bad ? 0 : xcc) : (int)blockIdx.x % np, q = blockIdx.x / np;
+    const int p = a.local_l2 ? xcc : (int)blockIdx.x % np;
     const int ep = k / np;  // experts per partition (1 or 2)
     const int segB = FF / 64;
-    const int drb = (int)s.down_rb;
-    const bool device_words = !a.local_l2;  // h words are read in other XCDs
-    // output rows of this workgroup's chunk (the host gives every workgroup at least one)
-    const int r_begin = q * a.rows_b;
-    const int r_end = min(D, r_begin + a.rows_b);
+    const int drb = a.drb;
+    // h words read in other XCDs, or forced coherent
+    const bool device_words = !a.local_l2 || (a.flags & kFlagHAgent);
+    // the XCD-local rank by ticket: lane 0 of wave 0 takes it after the
+    // routing's loads are issued (memory operations complete in order, so a
+    // wait for those loads does not wait for it) and publishes it after the
+    // rank, keeping its latency off the routing's path
+    const bool use_ticket = a.local_l2 && (a.flags & kFlagTicket) && xcc < np;
+    unsigned ticket = 0;
+    auto take_ticket = [&]() {
+        if (use_ticket && tid == 0) {
+            if (a.flags & kFlagTicketL2)
+                ticket = __hip_atomic_fetch_add(&a.sync[kTicketWord + kTicketStride * xcc], 1u, __ATOMIC_RELAXED,
+                                                __HIP_MEMORY_SCOPE_WORKGROUP);
+            else
+                ticket = __hip_atomic_fetch_add(&a.sync[kTicketWord + kTicketStride * xcc], 1u, __ATOMIC_RELAXED,
+                                                __HIP_MEMORY_SCOPE_AGENT);
+        }
+    };
+    if (a.mode != 1) take_ticket();
 
     // ---- 1. routing / slots and activation levels
     // x in parts of eight values, loaded first so that their latency overlaps
@@ -589,6 +642,7 @@ __device__ void fused_body(const FusedArgs& a, FusedLds& L) {
             L.a_issued = 0u;
             L.xs_read = 0u;
             L.b_landed = 0u;
+            L.bad = 0u;
         }
         if (a.mode == 1) {
             // ranks are a permutation of 0..n_expert-1, so the routing
@@ -615,7 +669,8 @@ __device__ void fused_body(const FusedArgs& a, FusedLds& L) {
             }
         }
     }
-    if (wave == 0 && a.mode == 1) route_keys(a, L, lane);
+    if (wave == 0 && a.mode == 1) route_keys(a, L, lane, take_ticket);
+    if (tid == 0 && a.mode != 1) L.ticket = ticket - a.ticket_base;
     if (xp >= 0) {  // wave-uniform
         quantize8(xv, xp / 8, xp % 8, xp < nxp, &L.a.xq[0][0], kMaxD, &L.a.xsc[0][0], kMaxD / 64, L.a.xs32);
         const int xp2 = xp + xnt;
@@ -625,11 +680,25 @@ __device__ void fused_body(const FusedArgs& a, FusedLds& L) {
             quantize8(xv2, xp2 / 8, xp2 % 8, xp2 < nxp, &L.a.xq[0][0], kMaxD, &L.a.xsc[0][0], kMaxD / 64, L.a.xs32);
         }
     }
-    __syncthreads();
     if (a.mode == 1) {
+        // LDS only: keys, x levels (__syncthreads would also wait for the ticket)
+        barrier_lds();
         route_rank(a, L, tid);
-        __syncthreads();
+        if (tid == 0) L.ticket = ticket - a.ticket_base;
     }
+    __syncthreads();
+    // rank inside the partition; a workgroup outside the launch's layout (an
+    // XCD that received more than its share, or an XCC id past the
+    // partitions) raises the error and leaves: the share it would have
+    // computed is missing elsewhere, and those waits give up
+    const int q = use_ticket ? (int)__builtin_amdgcn_readfirstlane(L.ticket) : (int)blockIdx.x / np;
+    if (p >= np || q >= a.m) {
+        if (tid == 0) raise_error(a.sync, a.epoch);
+        return;
+    }
+    // output rows of this workgroup's chunk (the host gives every workgroup at least one)
+    const int r_begin = q * a.rows_b;
+    const int r_end = min(D, r_begin + a.rows_b);
 
     // weight pointers of the partition's (at most two) experts
     // (all six read at once: slot p ep + 1 < kMaxSlots exists even when unused)
@@ -731,7 +800,7 @@ __device__ void fused_body(const FusedArgs& a, FusedLds& L) {
     const int rows_a = ep * FF;
     const int ra0 = min(rows_a, q * a.rows_a), ra1 = min(rows_a, ra0 + a.rows_a);
     const int npass = (ra1 - ra0 + GA - 1) / GA;
-    const int grb = (int)s.gate_rb, urb = (int)s.up_rb;
+    const int grb = a.grb, urb = a.urb;
     auto rows_of = [&](int pp) {
         PassRows r;
         r.t0 = ra0 + pp * GA + wave * GW;
@@ -783,7 +852,7 @@ __device__ void fused_body(const FusedArgs& a, FusedLds& L) {
             const float dg = group_sum<LA>(g.dot_q8(li, xs));
             const float du = group_sum<LA>(u.dot_q8(li, xs));
             // every pair of the workgroup gets a word, 0 for a slot without an expert
-            if (li == LA - 1 && gl < r.nr) {
+            if (li == LA - 1 && gl < r.nr && p + 1 != (int)(a.flags & 15u)) {
                 const float hv = r.ok ? dg / (1.0f + expf(-dg)) * du : 0.f;
                 store_word(&a.hx[(p * ep + r.e) * FF + r.f0 + gl], epoch_word(hv, a.epoch), device_words);
             }
@@ -794,8 +863,9 @@ __device__ void fused_body(const FusedArgs& a, FusedLds& L) {
         // this launch's epoch (it overwrites the activation levels: every A
         // wave has read its own first)
         wait_lds(&L.xs_read, (unsigned)kAWaves);
-        quantize_words(a.hx + p * ep * FF, ep * FF, a.epoch, a.sync, &L.b.hq[0][0], kMaxHP, &L.b.hsc[0][0],
-                       kMaxHP / 64, L.b.hs32, tid, kAThreads);
+        if (!quantize_words(a.hx + p * ep * FF, ep * FF, a.epoch, a.sync, spin_limit_of(a.flags), &L.b.hq[0][0], kMaxHP,
+                            &L.b.hsc[0][0], kMaxHP / 64, L.b.hs32, tid, kAThreads))
+            L.bad = 1u;
     } else {
         // ---- 2B. the round-0 down rows into LDS, queued behind the A waves'
         // first passes (h, the barrier and everything after it wait on
@@ -820,6 +890,8 @@ __device__ void fused_body(const FusedArgs& a, FusedLds& L) {
 
     // the router weight of each partition expert (0 for a slot without one)
     const float wgt[2] = {dptr[0] ? L.w[p * ep] : 0.f, ep > 1 && dptr[1] ? L.w[p * ep + 1] : 0.f};
+    // a wait for h gave up: the partials would be computed from stale words
+    const bool poisoned = L.bad != 0u;
 
     // Phase B rounds: every wave takes (expert, segment, 64-row block) tasks;
     // a lane is one row, so the h levels of the task are read by all lanes at
@@ -882,13 +954,14 @@ __device__ void fused_body(const FusedArgs& a, FusedLds& L) {
                     for (int u = 0; u < segB; u++) v += pr[u];
                 }
             }
-            store_word(&a.ypart[p * D + r_begin + r0 + r], epoch_word(v, a.epoch), true);
+            store_word(&a.ypart[p * D + r_begin + r0 + r], epoch_word(poisoned ? __builtin_nanf("") : v, a.epoch),
+                       true);
         }
     }
 
     // ---- 5. workgroup q of partition q % np adds chunk q's partials into y
     if (p == q % np)
-        for (int r = r_begin + tid; r < r_end; r += kThreads) a.y[r] = reduce_row(a.ypart, D, r, np, a.epoch, a.sync);
+        for (int r = r_begin + tid; r < r_end; r += kThreads) a.y[r] = reduce_row(a.ypart, D, r, np, a.epoch, a.sync, spin_limit_of(a.flags));
 }
 
 template <int LA, int GT, int UT, int DT>
@@ -1027,41 +1100,120 @@ bool fused_supported(const MoeShape& s, int k, int n_expert_for_routing) {
     return fused_grid_ok(s, k, fused_grid(s, k, current_capacity(s)));
 }
 
+constexpr int kXccProbe = 1024;
+
 __global__ void xcc_probe_kernel(int* out) {
     if (threadIdx.x == 0) out[blockIdx.x] = xcc_id();
 }
 
-// One-time check per device that a plain launch places workgroup b on XCD
-// (b + s) % 8 for one start s (the round-robin dispatch the XCD-local exchange
-// relies on; s depends on the launches before).
-static bool xcd_round_robin(int device) {
+// One-time check per device that a launch is spread round-robin over eight
+// XCDs: workgroup b on XCD (b + s) % 8 for one start s.  The XCD-local
+// exchange relies only on what follows from it, that every XCD receives an
+// equal share of a grid that is a multiple of 8 (the kernel ranks workgroups
+// by tickets, not by their index, and raises its error word if a share is
+// off).
+// probe_buf: kXccProbe ints of device memory to use, or null to allocate them.
+static bool xcd_round_robin(int device, int* probe_buf = nullptr) {
     static int state[64];  // 0 unknown, 1 yes, 2 no
     static std::mutex mu;
     std::lock_guard<std::mutex> lk(mu);
     if (device < 0 || device >= 64) return false;
     if (state[device]) return state[device] == 1;
-    state[device] = 2;
-    constexpr int kProbe = 1024;
-    int* d = nullptr;
+    int* d = probe_buf;
     clear_stale_error();  // an earlier, unrelated failure must not read as the probe's
-    if (hipMalloc(&d, kProbe * sizeof(int)) != hipSuccess) return false;
-    hipLaunchKernelGGL(xcc_probe_kernel, dim3(kProbe), dim3(64), 0, nullptr, d);
-    int hbuf[kProbe];
+    if (!d && hipMalloc(&d, kXccProbe * sizeof(int)) != hipSuccess) {
+        state[device] = 2;
+        return false;
+    }
+    hipLaunchKernelGGL(xcc_probe_kernel, dim3(kXccProbe), dim3(64), 0, nullptr, d);
+    int hbuf[kXccProbe];
     bool ok = hipGetLastError() == hipSuccess &&
               hipMemcpy(hbuf, d, sizeof hbuf, hipMemcpyDeviceToHost) == hipSuccess;
-    (void)hipFree(d);
+    if (!probe_buf) (void)hipFree(d);
     const int s = ok ? hbuf[0] : -1;
     ok = ok && s >= 0 && s < 8;
-    for (int b = 0; ok && b < kProbe; b++) ok = hbuf[b] == (b + s) % 8;
-    if (ok) state[device] = 1;
+    for (int b = 0; ok && b < kXccProbe; b++) ok = hbuf[b] == (b + s) % 8;
+    state[device] = ok ? 1 : 2;
     return ok;
 }
 
+int fused_exchange_probe(int device, int* probe_buf) { return xcd_round_robin(device, probe_buf) ? 1 : 0; }
+
 int fused_exchange_mode(int device) { return xcd_round_robin(device) ? 1 : 0; }
 
-hipError_t launch_moe_fused(const FusedArgsHost& h, hipStream_t st) {
+// Test knobs (set_fused_fault_injection): 0 / -1 mean the defaults.
+static unsigned g_spin_limit = 0;
+static int g_drop_part = -1;
+
+void set_fused_fault_injection(unsigned spin_limit, int drop_partition) {
+    g_spin_limit = spin_limit;
+    g_drop_part = drop_partition < 0 || drop_partition > 7 ? -1 : drop_partition;
+}
+
+// Launch options read once from the environment: EAHMMF_HIP_FUSED_COOP=1
+// launches cooperatively (the runtime then guarantees that every workgroup is
+// resident, at a measured cost of about 19 us per launch on MI355X, more
+// than the kernel itself at the Qwen3-30B-A3B shape); EAHMMF_HIP_H_AGENT=1
+// stores h device-coherent also within an XCD.
+static int env_flag(const char* name, int dflt) {
+    const char* e = getenv(name);
+    return e && *e ? (*e != '0') : dflt;
+}
+static bool coop_launch() {
+    static const bool v = env_flag("EAHMMF_HIP_FUSED_COOP", 0) != 0;
+    return v;
+}
+// Devices on which a cooperative launch was refused in this process.
+static bool g_coop_refused[64];
+static bool coop_ok(int dev) { return dev < 0 || dev >= 64 || !__atomic_load_n(&g_coop_refused[dev], __ATOMIC_RELAXED); }
+static void coop_refused(int dev) {
+    if (dev >= 0 && dev < 64) __atomic_store_n(&g_coop_refused[dev], true, __ATOMIC_RELAXED);
+}
+// EAHMMF_HIP_TICKET=1 ranks the workgroups of an XCD by an atomic ticket
+// (agent scope; 2: workgroup scope, executed in the XCD's L2) instead of by
+// b / 8.  Measured at the Qwen3-30B-A3B shape: +0.45 us per launch either
+// way (32 workgroups per XCD add to one counter at the same moment), so the
+// default ranks by b / 8, which the once-per-device placement check
+// validates; a launch placed otherwise shows up as waits that give up.
+static int ticket_mode() {
+    static const int v = [] {
+        const char* e = getenv("EAHMMF_HIP_TICKET");
+        return e && *e ? atoi(e) : 0;
+    }();
+    return v;
+}
+static int h_agent() {
+    static const int v = env_flag("EAHMMF_HIP_H_AGENT", 0);
+    return v;
+}
+
+__global__ void reset_sync_kernel(unsigned* sync, int clear_error) {
+    const int i = threadIdx.x;
+    if (i == 0 && clear_error) sync[kSyncFlagWord] = 0u;
+    if (i < 8) sync[kTicketWord + kTicketStride * i] = 0u;
+}
+
+hipError_t reset_fused_sync(FusedState& fs, hipStream_t st, bool clear_error) {
+    if (!fs.sync) return hipErrorInvalidValue;
+    clear_stale_error();
+    hipLaunchKernelGGL(reset_sync_kernel, dim3(1), dim3(64), 0, st, fs.sync, clear_error ? 1 : 0);
+    const hipError_t e = hipGetLastError();
+    if (e == hipSuccess) fs.ticket_base = 0;
+    return e;
+}
+
+hipError_t launch_moe_fused(const FusedArgsHost& h, FusedState& fs, hipStream_t st) {
+    const MoeShape& sh = h.shape;
+    if (!fused_supported(sh, h.k, h.mode == 1 ? h.n_expert : 0) || !fs.ypart || !fs.hx || !fs.sync || !h.x)
+        return hipErrorInvalidValue;
+    if (fs.hx_words < (size_t)h.k * sh.FF || fs.ypart_words < (size_t)8 * sh.D) return hipErrorInvalidValue;
+    if (h.mode == 1 && (h.n_expert <= 0 || !h.logits || !h.table)) return hipErrorInvalidValue;
     FusedArgs a{};
-    a.s = h.shape;
+    a.D = sh.D;
+    a.FF = sh.FF;
+    a.grb = (int)sh.gate_rb;
+    a.urb = (int)sh.up_rb;
+    a.drb = (int)sh.down_rb;
     a.k = h.k;
     a.n_expert = h.n_expert;
     a.mode = h.mode;
@@ -1074,18 +1226,15 @@ hipError_t launch_moe_fused(const FusedArgsHost& h, hipStream_t st) {
     a.w_out = h.w_out;
     a.x = h.x;
     a.y = h.y;
-    a.hx = h.hx;
-    a.ypart = h.ypart;
-    a.sync = h.sync;
-    if (!fused_supported(a.s, a.k, a.mode == 1 ? a.n_expert : 0) || !a.ypart || !a.hx || !a.sync || !a.x)
-        return hipErrorInvalidValue;
-    if (a.mode == 1 && (a.n_expert <= 0 || !a.logits || !a.table)) return hipErrorInvalidValue;
-    FusedFn fn = pick_fused(a.s);
+    a.hx = fs.hx;
+    a.ypart = fs.ypart;
+    a.sync = fs.sync;
+    FusedFn fn = pick_fused(sh);
     int dev = 0;
     hipError_t e = hipGetDevice(&dev);
     if (e != hipSuccess) return e;
-    const FusedGrid g = fused_grid(a.s, a.k, fused_capacity(fn, dev));
-    if (!fused_grid_ok(a.s, a.k, g) || h.epoch == 0) return hipErrorInvalidConfiguration;
+    const FusedGrid g = fused_grid(sh, a.k, fused_capacity(fn, dev));
+    if (!fused_grid_ok(sh, a.k, g)) return hipErrorInvalidConfiguration;
     a.np = g.np;
     a.m = g.m;
     a.rows_b = g.rows_b;
@@ -1093,7 +1242,11 @@ hipError_t launch_moe_fused(const FusedArgsHost& h, hipStream_t st) {
     a.rows_round = g.rows_round;
     a.stride_b = g.stride_b;
     a.local_l2 = (a.np == 8 && xcd_round_robin(dev)) ? 1 : 0;
-    a.epoch = h.epoch;
+    a.epoch = fs.epoch + 1 == 0 ? 1 : fs.epoch + 1;
+    a.ticket_base = fs.ticket_base;
+    const unsigned lim = g_spin_limit > 0xFFFFFFu ? 0xFFFFFFu : g_spin_limit;
+    a.flags = (unsigned)(g_drop_part + 1) | (ticket_mode() ? kFlagTicket : 0u) | (h_agent() ? kFlagHAgent : 0u) |
+              (ticket_mode() == 2 ? kFlagTicketL2 : 0u) | (lim << 8);
     // routing: n_expert rounded up to a power of two (at most 256) is split
     // into t runs of rank_c keys, t threads per candidate (t <= 16)
     int npow = 1;
@@ -1105,10 +1258,34 @@ hipError_t launch_moe_fused(const FusedArgsHost& h, hipStream_t st) {
     while ((1 << a.rank_shift) < t) a.rank_shift++;
     a.rank_c = npow / t;
     clear_stale_error();
-    // A plain launch: the grid never exceeds what is resident at once, and the
-    // stream runs nothing else concurrently, so every workgroup is live.
-    hipLaunchKernelGGL(fn, dim3(a.np * a.m), dim3(kThreads), 0, st, a);
-    return hipGetLastError();
+    // Workgroups wait for each other, so all of them must be resident at
+    // once.  The grid is at most one workgroup per CU, which the occupancy
+    // check above admits, and a plain launch of it on an idle device makes
+    // every workgroup resident.  When something else holds CUs, a workgroup
+    // that is not resident in time shows up as waits that give up: NaN in y
+    // and the error word, never a silent result.  A cooperative launch
+    // (EAHMMF_HIP_FUSED_COOP=1) guarantees residency instead, at the cost
+    // above.  The runtime can refuse it while another process on the GPU
+    // holds the device's cooperative-launch resource; the launch is then a
+    // plain one, and this process keeps to plain launches on the device.
+    if (coop_launch() && coop_ok(dev)) {
+        void* args[] = {&a};
+        e = hipLaunchCooperativeKernel(reinterpret_cast<const void*>(fn), dim3(a.np * a.m), dim3(kThreads), args, 0,
+                                       st);
+        if (e != hipSuccess) {
+            coop_refused(dev);
+            clear_stale_error();
+        }
+    }
+    if (!(coop_launch() && coop_ok(dev))) {
+        hipLaunchKernelGGL(fn, dim3(a.np * a.m), dim3(kThreads), 0, st, a);
+        e = hipGetLastError();
+    }
+    if (e == hipSuccess) {
+        fs.epoch = a.epoch;
+        if (a.local_l2 && (a.flags & kFlagTicket)) fs.ticket_base += (unsigned)a.m;
+    }
+    return e;
 }
 
 }  // namespace eahmmf

@@ -196,10 +196,18 @@ extern "C" int64_t eahmmf_hip_quantize_rows(int type, const float* src, int64_t 
     } else {
         std::vector<std::thread> th;
         const int64_t per = (nrows + nthr - 1) / nthr;
-        for (int64_t t = 0; t < nthr; t++) {
-            const int64_t a = t * per, z = std::min(nrows, a + per);
-            if (a < z) th.emplace_back(work, a, z);
+        int64_t started = 0;  // rows [0, started) are handed to threads
+        try {
+            for (int64_t t = 0; t < nthr; t++) {
+                const int64_t a = t * per, z = std::min(nrows, a + per);
+                if (a < z) th.emplace_back(work, a, z);
+                started = std::max(started, z);
+            }
+        } catch (...) {
+            // a thread could not be started: the remaining rows are quantized
+            // on this thread (no exception leaves the C ABI)
         }
+        if (started < nrows) work(started, nrows);
         for (auto& t : th) t.join();
     }
     return (int64_t)(rb * (size_t)nrows);

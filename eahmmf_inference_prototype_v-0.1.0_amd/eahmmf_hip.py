@@ -24,7 +24,7 @@ EXPORTS = (
     "eahmmf_hip_last_error", "eahmmf_hip_device_count", "eahmmf_hip_shutdown", "eahmmf_hip_moe_layer_decode_async",
     "eahmmf_hip_set_fused", "eahmmf_hip_device_flags", "eahmmf_hip_fused_exchange", "eahmmf_hip_moe_grouped",
     "eahmmf_hip_moe_grouped_async", "eahmmf_hip_set_grouped_mfma", "eahmmf_hip_stream_read_async",
-    "eahmmf_hip_h2d_batch",
+    "eahmmf_hip_h2d_batch", "eahmmf_hip_fused_status_async", "eahmmf_hip_set_fault_injection",
 )
 
 
@@ -91,6 +91,8 @@ def load(path=LIB_PATH):
                                                       vp, vp]),
         "eahmmf_hip_set_fused": (c_int, [c_int]),
         "eahmmf_hip_device_flags": (c_int, []),
+        "eahmmf_hip_fused_status_async": (c_int, [vp, vp]),
+        "eahmmf_hip_set_fault_injection": (None, [ctypes.c_uint, c_int]),
         "eahmmf_hip_fused_exchange": (c_int, []),
         "eahmmf_hip_set_grouped_mfma": (c_int, [c_int]),
         "eahmmf_hip_moe_grouped": (c_bool, [ctypes.POINTER(Expert), c_int, vp, vp, vp, c_int, vp, vp]),

@@ -96,7 +96,10 @@ static void check_expert_block(eahmmf_hip::HipDevice& dev, int D, int FF, int k,
     float tot = 0.f;
     for (int j = 0; j < k; j++) tot += (w[j] = 1.0f + (float)j);
     for (auto& v : w) v /= tot;
-    CHECK(eahmmf_hip_moe_decode(ex.data(), w.data(), k, x.data(), y.data()));
+    if (!eahmmf_hip_moe_decode(ex.data(), w.data(), k, x.data(), y.data())) {
+        fprintf(stderr, "FAILED eahmmf_hip_moe_decode D=%d FF=%d k=%d: %s\n", D, FF, k, eahmmf_hip_last_error());
+        g_fail++;
+    }
     // the reference's sequence of calls, through the drop-in entry points
     std::vector<float> g(FF), u(FF), yd(D);
     for (int j = 0; j < k; j++) {

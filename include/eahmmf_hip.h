@@ -211,18 +211,40 @@ int eahmmf_hip_h2d_batch(const eahmmf_hip_copy* copies, int n);
  * reference's EAHMMF_OLD_KERNEL switch, expert_cuda.cu:307-308). */
 int eahmmf_hip_set_fused(int enable);
 /* How the fused kernel's partitions exchange their gate/up results on the
- * current device: 1 through each XCD's own L2 (the dispatch places workgroup b
- * on XCD b % 8, checked once per device), 0 through device-coherent memory,
- * -1 on error. */
+ * current device: 1 through each XCD's own L2 (eight XCDs that each receive
+ * an equal share of a launch, checked once per device; workgroups then rank
+ * themselves per XCD with an atomic ticket), 0 through device-coherent
+ * memory, -1 on error. */
 int eahmmf_hip_fused_exchange(void);
 /* Selects matrix-core (MFMA) matmuls in the grouped block where the formats
  * allow (1, the default: Q4_K/Q5_K gate/up, Q6_K down) or the vector-ALU
  * kernels only (0); a negative argument only queries.  Returns the previous
  * setting. */
 int eahmmf_hip_set_grouped_mfma(int enable);
-/* Nonzero if a fused launch on the current device hit its bounded wait since
- * the last call (its output is then not valid); clears the flag. */
+/* The single-launch expert block's workgroups wait for each other's words
+ * (h, per-partition partials).  Every wait is bounded; when one gives up the
+ * launch writes NaN where the missing words were needed and records its
+ * epoch in a per-device error word, and the kernel still exits.  The
+ * synchronous entry points read that word with their output and then return
+ * false (as on any HIP error, expert_cuda.cu:332-335, so the caller falls back
+ * to the CPU, qwen3moe.cpp:515-521).  For the *_async entry points:
+ *
+ * eahmmf_hip_device_flags: 1 if a fused launch on the current device gave up
+ * a wait since the last call (its output is then not valid), else 0; -2 on a
+ * HIP error.  Synchronises the device and clears the word. */
 int eahmmf_hip_device_flags(void);
+/* Cheap check for *_async callers: enqueues on `stream` a copy of the error
+ * word (0: no launch gave up a wait since the word was last cleared) into
+ * dst, device or pinned host memory, valid once the stream reaches it.  Does
+ * not clear the word (eahmmf_hip_device_flags does).  0 on success, -1 on a
+ * null dst, -3 on a HIP error. */
+int eahmmf_hip_fused_status_async(unsigned* dst, void* stream);
+/* Test knob, no counterpart in the reference: the number of polls after which
+ * a fused-kernel wait gives up (0: the default, 2^18), and one partition
+ * (0-7) whose h words are never stored (-1: none), so that tests can make the
+ * kernel's own bounded waits give up while every kernel still exits
+ * normally.  Not for production use. */
+void eahmmf_hip_set_fault_injection(unsigned spin_limit, int drop_partition);
 const char* eahmmf_hip_last_error(void);
 int eahmmf_hip_device_count(void);
 /* Frees the calling device's scratch, staging buffers and stream. */

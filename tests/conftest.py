@@ -38,3 +38,11 @@ def binding():
 @pytest.fixture(scope="session")
 def hip(binding):
     return binding.lib()
+
+
+@pytest.fixture(scope="session")
+def torch_dev():
+    """torch with a visible GPU (for tests marked gpu)."""
+    import torch
+    assert torch.cuda.is_available()
+    return torch
