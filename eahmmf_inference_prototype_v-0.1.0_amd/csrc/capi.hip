@@ -281,6 +281,9 @@ void fill_slot(uint8_t* slot, const std::vector<Piece>& ps, size_t total, int nt
 
 }  // namespace
 
+void eahmmf::set_last_error(const char* msg) { set_error("%s", msg); }
+bool eahmmf::fused_path_enabled() { return fused_enabled(); }
+
 extern "C" {
 
 const char* eahmmf_hip_last_error(void) { return g_last_error.c_str(); }
@@ -660,7 +663,9 @@ int eahmmf_hip_device_flags(void) {
         (void)reset_fused_sync(c->fused, c->stream, true);
         (void)hipStreamSynchronize(c->stream);
     }
-    return v ? 1 : 0;
+    const int na = noalloc_device_flags();
+    if (na < 0) return set_error("reading the no-allocation scratch's error word failed"), -2;
+    return (v || na) ? 1 : 0;
 }
 
 int eahmmf_hip_fused_status_async(unsigned* dst, void* stream) {

@@ -139,6 +139,14 @@ hipError_t launch_stream_read(const void* buf, size_t bytes, uint32_t* sink, hip
 
 bool moe_shape_ok(const MoeShape& s);
 
+// Sets the message eahmmf_hip_last_error() returns on this thread (capi.hip).
+void set_last_error(const char* msg);
+// The eahmmf_hip_set_fused() setting (capi.hip).
+bool fused_path_enabled();
+// Error word of the no-allocation entry point's scratch on the current device
+// (noalloc.hip): 1 if a launch gave up a wait since the last call, then
+// cleared; 0 if not or never set up; -2 on a HIP error.
+int noalloc_device_flags();
 bool type_supported(int t);
 
 }  // namespace eahmmf

@@ -25,6 +25,7 @@ EXPORTS = (
     "eahmmf_hip_set_fused", "eahmmf_hip_device_flags", "eahmmf_hip_fused_exchange", "eahmmf_hip_moe_grouped",
     "eahmmf_hip_moe_grouped_async", "eahmmf_hip_set_grouped_mfma", "eahmmf_hip_stream_read_async",
     "eahmmf_hip_h2d_batch", "eahmmf_hip_fused_status_async", "eahmmf_hip_set_fault_injection",
+    "eahmmf_hip_moe_layer_decode_noalloc",
 )
 
 
@@ -89,6 +90,8 @@ def load(path=LIB_PATH):
                                                        vp]),
         "eahmmf_hip_moe_layer_decode_async": (c_int, [ctypes.POINTER(MoeShape), vp, c_int, vp, c_int, vp, vp, vp,
                                                       vp, vp]),
+        "eahmmf_hip_moe_layer_decode_noalloc": (c_int, [ctypes.POINTER(MoeShape), vp, c_int, vp, c_int, vp, vp, vp,
+                                                        vp, vp]),
         "eahmmf_hip_set_fused": (c_int, [c_int]),
         "eahmmf_hip_device_flags": (c_int, []),
         "eahmmf_hip_fused_status_async": (c_int, [vp, vp]),

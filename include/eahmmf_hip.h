@@ -113,6 +113,24 @@ int eahmmf_hip_moe_layer_decode_async(const eahmmf_hip_moe_shape* shape, const e
                                       int n_expert, const float* dev_logits, int k, const float* dev_x, float* dev_y,
                                       int* dev_ids_out, float* dev_w_out, void* stream);
 
+/* No counterpart in the reference.  For callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc): eahmmf_hip_moe_layer_decode_async with the same
+ * arguments and results, calling no hipMalloc/hipFree.  Its scratch (the
+ * single-launch kernel's exchange and sync words, or the two-kernel path's h
+ * and routing results) is one file-scope device array of about 1 MiB that
+ * every GPU the library runs on holds until the process ends.  Limits:
+ * k * FF <= 65536 and D <= 4096 (else -1 and a message).  All calls on one
+ * GPU share the array, which keeps the last call's contents: calls that
+ * overlap in time on one device race (order them on one stream).  The first
+ * call on a device sets the array up (its address, one fill kernel and a
+ * synchronisation of `stream`), so make it outside graph capture.  A launch
+ * whose bounded wait gave up writes NaN to dev_y and is reported by
+ * eahmmf_hip_device_flags(). */
+int eahmmf_hip_moe_layer_decode_noalloc(const eahmmf_hip_moe_shape* shape, const eahmmf_hip_expert_ptrs* dev_table,
+                                        int n_expert, const float* dev_logits, int k, const float* dev_x,
+                                        float* dev_y, int* dev_ids_out, float* dev_w_out, void* stream);
+
 /* Ragged grouped expert block for a batch of nb tokens (prefill, batched
  * decode), in the reference's by_exp form: group g (ascending expert id) is
  * experts[g] applied to tokens[group_offsets[g] .. group_offsets[g+1]) with
