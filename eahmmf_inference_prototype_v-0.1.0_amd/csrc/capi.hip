@@ -713,6 +713,12 @@ int eahmmf_hip_route_topk_async(const float* dev_logits, int nb, int n_expert, i
     return hip_ok(e, "route launch") ? 0 : -3;
 }
 
+int eahmmf_hip_expf_ref_async(const float* dev_x, float* dev_y, int64_t n, void* stream) {
+    const hipError_t e = launch_expf_ref(dev_x, dev_y, n, (hipStream_t)stream);
+    if (e == hipErrorInvalidValue) return set_error("null buffer or negative n"), -1;
+    return hip_ok(e, "expf launch") ? 0 : -3;
+}
+
 int eahmmf_hip_stream_read_async(const void* dev_buf, size_t bytes, uint32_t* dev_sink, void* stream) {
     if (bytes == 0) return 0;
     if (!dev_buf || !dev_sink) return set_error("null argument"), -1;

@@ -130,6 +130,8 @@ hipError_t launch_down_mfma(const MoeShape& s, const ExpertEntry* table, int E, 
 // allow; 0: the vector-ALU kernels only.  A negative argument only queries.
 int set_grouped_mfma(int enable);
 
+// y[i] = expf(x[i]) bit for bit as glibc's (expf_ref.h), i < n.
+hipError_t launch_expf_ref(const float* x, float* y, int64_t n, hipStream_t st);
 // softmax -> top-k (e desc, index asc) -> renormalise; logits [nb][n_expert].
 hipError_t launch_route_topk(const float* logits, int nb, int n_expert, int k, int* ids, float* w, hipStream_t st);
 // Streaming read of bytes (a multiple of 16, 16-byte aligned buffer); the

@@ -68,6 +68,7 @@
 
 #include <mutex>
 
+#include "expf_ref.h"
 #include "internal.h"
 #include "kquant_seg64.h"
 
@@ -390,10 +391,11 @@ __device__ __forceinline__ void load_xseg(XSeg& xs, const int8_t* q, int qstride
 }
 
 // Routing, step 1 (wave 0): the expert table into LDS and every candidate's
-// order key.  e_i = expf(l_i - max) as the reference forms it; the key holds
-// e_i's bits + 1 in the high word (non-negative floats order as their bits;
-// 0 for a NaN e_i and for ids past n_expert up to 256) and ~i in the low
-// word, so keys are distinct and order exactly as (e desc, id asc).
+// order key.  e_i = expf(l_i - max) bit for bit as the reference's libm forms
+// it (expf_ref.h; the table entry 2^(k/32) comes from the lane holding it);
+// the key holds e_i's bits + 1 in the high word (non-negative floats order as
+// their bits; 0 for a NaN e_i and for ids past n_expert up to 256) and ~i in
+// the low word, so keys are distinct and order exactly as (e desc, id asc).
 template <class After>
 __device__ void route_keys(const FusedArgs& a, FusedLds& L, int lane, After after_loads) {
     const int n = a.n_expert;
@@ -406,13 +408,21 @@ __device__ void route_keys(const FusedArgs& a, FusedLds& L, int lane, After afte
         l[c] = id < n ? a.logits[id] : -INFINITY;
         ent[c] = id < n ? a.table[id] : ExpertEntry{nullptr, nullptr, nullptr};
     }
+    const uint64_t tab = exp2_tab((uint32_t)lane);  // lanes 32-63 repeat lanes 0-31
     after_loads();
     float mx = fmaxf(fmaxf(l[0], l[1]), fmaxf(l[2], l[3]));
     mx = dpp_max(mx);
 #pragma unroll
     for (int c = 0; c < 4; c++) {
         const int id = lane + 64 * c;
-        const float e = expf(l[c] - mx);
+        double rr;
+        uint64_t ki;
+        float sp;
+        const bool special = expf_ref_reduce(l[c] - mx, &rr, &ki, &sp);
+        const int src = (int)(ki & 31u);  // every lane takes part in the exchange
+        const uint32_t tlo = (uint32_t)__shfl((int)(uint32_t)tab, src, 64);
+        const uint32_t thi = (uint32_t)__shfl((int)(uint32_t)(tab >> 32), src, 64);
+        const float e = special ? sp : expf_ref_finish(rr, ki, ((uint64_t)thi << 32) | tlo);
         const uint32_t hi = (id < n && e == e) ? __builtin_bit_cast(uint32_t, e) + 1u : 0u;
         L.rkey[id] = ((uint64_t)hi << 32) | (uint32_t)~id;
         if (id < n) L.table[id] = ent[c];

@@ -10,6 +10,7 @@
 //            LDS; the k experts of one output row are reduced inside one wave,
 //            so no atomics and the result is deterministic.
 // route_topk_kernel does softmax -> top-k -> renormalise (qwen3moe.cpp:1011-1023).
+#include "expf_ref.h"
 #include "internal.h"
 #include "kquant.h"
 
@@ -112,8 +113,9 @@ __global__ __launch_bounds__(256) void moe_down_kernel(MoeShape s, SlotSource sr
 
 // ---------------------------------------------------------------------------
 // Routing: one wave per token.  Ranking uses the same key as the reference,
-// e_i = expf(l_i - max) (desc) with the lower index winning ties; the chosen
-// e are summed in rank order and divided (qwen3moe.cpp:1011-1023).
+// e_i = expf(l_i - max) (desc, bit for bit as the reference's libm forms it:
+// expf_ref.h) with the lower index winning ties; the chosen e are summed in
+// rank order and divided (qwen3moe.cpp:1011-1023).
 __global__ __launch_bounds__(256) void route_topk_kernel(const float* __restrict__ logits, int nb, int n_expert, int k,
                                                          int* __restrict__ ids, float* __restrict__ w) {
     const int lane = threadIdx.x & 63;
@@ -133,7 +135,7 @@ __global__ __launch_bounds__(256) void route_topk_kernel(const float* __restrict
 #pragma unroll
     for (int i = 0; i < kMaxPerLane; i++) {
         const int id = lane + 64 * i;
-        e[i] = id < n_expert ? expf(l[id] - mx) : -1.0f;
+        e[i] = id < n_expert ? expf_ref(l[id] - mx) : -1.0f;
     }
     float tot = 0.f;
     float chosen_e[kMaxSlots];
@@ -166,6 +168,21 @@ __global__ __launch_bounds__(256) void route_topk_kernel(const float* __restrict
             w[(size_t)t * k + r] = chosen_e[r] / tot;
         }
     }
+}
+
+// The routing's exp on its own (glibc's expf, bit for bit): y[i] = e^x[i].
+__global__ __launch_bounds__(256) void expf_ref_kernel(const float* __restrict__ x, float* __restrict__ y, int64_t n) {
+    for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x)
+        y[i] = expf_ref(x[i]);
+}
+
+hipError_t launch_expf_ref(const float* x, float* y, int64_t n, hipStream_t st) {
+    if (n < 0 || (n > 0 && (!x || !y))) return hipErrorInvalidValue;
+    if (n == 0) return hipSuccess;
+    const int64_t blocks = (n + 255) / 256;
+    clear_stale_error();
+    hipLaunchKernelGGL(expf_ref_kernel, dim3((unsigned)(blocks < 4096 ? blocks : 4096)), dim3(256), 0, st, x, y, n);
+    return hipGetLastError();
 }
 
 // ---------------------------------------------------------------------------

@@ -163,6 +163,14 @@ bool eahmmf_hip_route_topk(const float* host_logits, int nb, int n_expert, int k
 int eahmmf_hip_route_topk_async(const float* dev_logits, int nb, int n_expert, int k, int* dev_ids, float* dev_w,
                                 void* stream);
 
+/* The routing's exponential on the device: dev_y[i] = expf(dev_x[i]) with
+ * the bits glibc's expf gives (the method of expf_ref.h), so routing keys
+ * e = expf(l - max) and their ties match the reference host's
+ * (qwen3moe.cpp:1013-1016).  No counterpart in the reference; for callers
+ * that form routing keys in their own kernels.  Asynchronous on stream; 0 on
+ * success, -1 on bad arguments, -3 on a launch error. */
+int eahmmf_hip_expf_ref_async(const float* dev_x, float* dev_y, int64_t n, void* stream);
+
 /* ---- measurement ------------------------------------------------------ */
 
 /* Streaming read of bytes from dev_buf (16-byte aligned, bytes a multiple of

@@ -71,6 +71,7 @@ def lib():
                                  ctypes.c_int, ctypes.c_int, vp, ctypes.c_int]
         L.orc_rmsnorm.argtypes = [vp, vp, vp, ctypes.c_int, ctypes.c_float]
         L.orc_route_topk.argtypes = [vp, ctypes.c_int, ctypes.c_int, ctypes.c_int, vp, vp]
+        L.orc_expf_array.argtypes = [vp, vp, ctypes.c_int64]
         L.orc_moe_layer.argtypes = [ctypes.POINTER(Experts), vp, ctypes.c_int, ctypes.c_int, vp, vp, vp]
         L.orc_state_new.restype = vp
         L.orc_state_new.argtypes = [ctypes.POINTER(Model)]
@@ -119,6 +120,14 @@ def route_topk(logits, k):
     w = np.empty((nb, k), dtype=np.float32)
     lib().orc_route_topk(_ptr(logits), nb, E, k, _ptr(ids), _ptr(w))
     return ids, w
+
+
+def expf(x):
+    """Elementwise expf of float32 x with the host libm (the routing keys' exp)."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    y = np.empty_like(x)
+    lib().orc_expf_array(_ptr(x), _ptr(y), x.size)
+    return y
 
 
 def make_view(t, w, ne0):

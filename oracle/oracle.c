@@ -238,6 +238,10 @@ void orc_route_topk(const float* logits, int nb, int n_expert, int k, int* ids, 
     free(e);
 }
 
+void orc_expf_array(const float* x, float* y, int64_t n) {
+    for (int64_t i = 0; i < n; i++) y[i] = expf(x[i]);
+}
+
 static float silu_mul(float g, float u) { return g / (1.0f + expf(-g)) * u; }
 
 /* qwen3moe.cpp:1024-1067 */

@@ -54,6 +54,9 @@ void orc_rmsnorm(const float* x, const float* w, float* out, int n, float eps);
 /* softmax -> top-k (e desc, index asc) -> renorm in rank order.
  * logits[nb][n_expert] (not modified); ids/wts [nb][k] in rank order. */
 void orc_route_topk(const float* logits, int nb, int n_expert, int k, int* ids, float* wts);
+/* y[i] = expf(x[i]) with the host libm's expf, the function the routing
+ * keys use (qwen3moe.cpp:1013). */
+void orc_expf_array(const float* x, float* y, int64_t n);
 
 /* One quantized component view (a WeightView without the device pointer). */
 typedef struct {

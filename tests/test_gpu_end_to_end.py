@@ -144,4 +144,11 @@ def test_config0_with_gpu_experts(torch_dev, binding, hip):
         gen.append(t)
         lg = m.forward([t], pos)
         pos += 1
+        # every one of the 32 decode steps' logits, not only the prompt's
+        np.testing.assert_allclose(lg, ref["step_logits"][i + 1], rtol=0, atol=1e-4)
     assert gen == list(ref["gen"])
+    # the routing trace of every layer, prompt token and generated token
+    ids, wts = m.trace()
+    assert np.array_equal(ids, ref["trace_ids"])
+    np.testing.assert_allclose(wts, ref["trace_w"], rtol=5e-5, atol=0)  # the oracle's own bar vs the reference
+    assert gpu.calls["decode"] == spec.n_layer * len(ref["gen"])
