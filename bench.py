@@ -27,6 +27,7 @@ import numpy as np
 ROOT = os.path.dirname(os.path.abspath(__file__))
 PKG_DIR = os.path.join(ROOT, "eahmmf_inference_prototype_v-0.1.0_amd")
 HBM_PEAK_GBS = 8000.0
+MFMA_F16_PEAK_TFLOPS = 2500.0  # MI355X dense fp16/bf16 matrix-core peak
 D, FF, E, K = 2048, 768, 128, 8
 Q8_0, Q4_K, Q5_K, Q6_K = 8, 12, 13, 14
 COPY_BYTES = 256 << 20
@@ -146,7 +147,12 @@ def bench_c4(args, torch, b, hip):
                    "distinct_experts_per_step": [len(np.unique(ids[i])) for i in range(NS)],
                    "bytes_per_step_avg": int(np.mean(step_bytes))},
         "pct_of_hbm_peak": round(100 * gbs / HBM_PEAK_GBS, 2),
-        "tflops": round(flop * steps / el / 1e12, 3)}), flush=True)
+        "tflops": round(flop * steps / el / 1e12, 3),
+        # useful expert FLOP over the step time against the dense fp16 matrix-core peak (the
+        # grouped matmuls run v_mfma_f32_16x16x32_f16); the busy-cycle counters behind it are in
+        # profiles/moe_grouped_c4_counters.md
+        "mfma_util": round(flop * steps / el / 1e12 / MFMA_F16_PEAK_TFLOPS, 4),
+        "mfma_peak_tflops": MFMA_F16_PEAK_TFLOPS}), flush=True)
 
 
 def bench_c5_batch(args, torch, b, hip):

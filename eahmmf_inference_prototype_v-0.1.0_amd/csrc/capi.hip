@@ -135,13 +135,22 @@ bool drain(DevCtx* c, bool ok) {
     return ok;
 }
 
+// The reference's checks (expert_cuda.cu:263-267) plus two of the layout:
+// ne0 a whole number of blocks (every GGUF row is), and a row stride that
+// holds the row's blocks, a multiple of 16 for Q4_K/Q5_K and of 2 for
+// Q6_K/Q8_0 (the block loads' alignment).  Rows may be padded: row r starts
+// at w + r * row_bytes, as in the reference.
 bool matmul_args_ok(const uint8_t* w, int type, int ne0, int ne1, size_t row_bytes, int ldx, int ldo) {
     if (!w) return set_error("null weight pointer"), false;
     if (!type_supported(type)) return set_error("unsupported ggml type %d", type), false;
     if (ne0 <= 0 || ne1 <= 0) return set_error("bad shape %d x %d", ne1, ne0), false;
     if (ne0 % type_blck(type)) return set_error("ne0 %d not a multiple of the block size", ne0), false;
-    if (row_bytes != (size_t)(ne0 / type_blck(type)) * type_bytes(type))
-        return set_error("row_bytes %zu does not match type %d, ne0 %d", row_bytes, type, ne0), false;
+    const size_t packed = (size_t)(ne0 / type_blck(type)) * type_bytes(type);
+    const size_t align = (type == kQ4_K || type == kQ5_K) ? 16 : 2;
+    if (row_bytes < packed || row_bytes % align)
+        return set_error("row_bytes %zu: type %d, ne0 %d needs at least %zu, a multiple of %zu", row_bytes, type, ne0,
+                         packed, align),
+               false;
     if (ldx < ne0 || ldo < ne1) return set_error("ldx/ldo smaller than the row length"), false;
     return true;
 }
@@ -403,6 +412,32 @@ bool eahmmf_hip_moe_decode(const eahmmf_hip_expert* experts, const float* w, int
     // caller that ignores the return value still cannot take it for a result
     memcpy(host_y, c->py.p, ybytes);
     return fused ? flag_ok(c, *flag, c->fused.epoch) : true;
+}
+
+bool eahmmf_hip_moe_decode_resident(const eahmmf_hip_expert* experts, const float* w, int k, const float* host_x,
+                                    float* host_y, uint32_t* skipped_mask) {
+    if (!experts || !w || !host_x || !host_y || !skipped_mask) return set_error("null argument"), false;
+    if (k <= 0 || k > kMaxSlots) return set_error("k=%d outside 1..%d", k, kMaxSlots), false;
+    // the device-resident slots, in slot order
+    eahmmf_hip_expert res[kMaxSlots];
+    float wr[kMaxSlots];
+    int kr = 0;
+    uint32_t skipped = 0;
+    for (int j = 0; j < k; j++) {
+        const eahmmf_hip_expert& e = experts[j];
+        if (!e.gate.dev || !e.up.dev || !e.down.dev) {
+            skipped |= 1u << j;
+            continue;
+        }
+        res[kr] = e;
+        wr[kr++] = w[j];
+    }
+    *skipped_mask = skipped;
+    if (kr == 0) {  // nothing resident: the whole block is the caller's
+        memset(host_y, 0, sizeof(float) * (size_t)experts[0].gate.ne0);
+        return true;
+    }
+    return eahmmf_hip_moe_decode(res, wr, kr, host_x, host_y);
 }
 
 static bool shape_from_abi(const eahmmf_hip_moe_shape* sh, MoeShape& s) {

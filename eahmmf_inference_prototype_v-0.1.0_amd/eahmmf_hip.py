@@ -25,7 +25,7 @@ EXPORTS = (
     "eahmmf_hip_set_fused", "eahmmf_hip_device_flags", "eahmmf_hip_fused_exchange", "eahmmf_hip_moe_grouped",
     "eahmmf_hip_moe_grouped_async", "eahmmf_hip_set_grouped_mfma", "eahmmf_hip_stream_read_async",
     "eahmmf_hip_h2d_batch", "eahmmf_hip_fused_status_async", "eahmmf_hip_set_fault_injection",
-    "eahmmf_hip_moe_layer_decode_noalloc", "eahmmf_hip_expf_ref_async",
+    "eahmmf_hip_moe_layer_decode_noalloc", "eahmmf_hip_expf_ref_async", "eahmmf_hip_moe_decode_resident",
 )
 
 
@@ -105,6 +105,7 @@ def load(path=LIB_PATH):
         "eahmmf_hip_route_topk_async": (c_int, [vp, c_int, c_int, c_int, vp, vp, vp]),
         "eahmmf_hip_stream_read_async": (c_int, [vp, ctypes.c_size_t, vp, vp]),
         "eahmmf_hip_expf_ref_async": (c_int, [vp, vp, c_i64, vp]),
+        "eahmmf_hip_moe_decode_resident": (c_bool, [ctypes.POINTER(Expert), vp, c_int, vp, vp, vp]),
         "eahmmf_hip_h2d_batch": (c_int, [ctypes.POINTER(Copy), c_int]),
         "eahmmf_hip_dequantize": (c_int, [vp, c_int, c_i64, c_i64, c_sz, vp, vp]),
         "eahmmf_hip_row_bytes": (c_sz, [c_int, c_i64]),

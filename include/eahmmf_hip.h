@@ -92,6 +92,17 @@ typedef struct {
 bool eahmmf_hip_moe_decode(const eahmmf_hip_expert* experts, const float* w, int k,
                            const float* host_x, float* host_y);
 
+/* The same under partial residency: a slot whose expert has no device copy
+ * (a null gate/up/down dev pointer: the store served that lease from RAM or
+ * the SSD mapping, eahmmf.h:721-742, e.g. when the VRAM budget is full of
+ * pinned experts) is skipped, and bit j of *skipped_mask is set for skipped
+ * slot j.  host_y[D] is then the weighted sum over the resident slots only
+ * (all zeros if none is resident; D is taken from experts[0].gate.ne0), and
+ * the caller adds the skipped experts' contributions on the CPU.  The
+ * resident slots must share one shape, as for eahmmf_hip_moe_decode. */
+bool eahmmf_hip_moe_decode_resident(const eahmmf_hip_expert* experts, const float* w, int k, const float* host_x,
+                                    float* host_y, uint32_t* skipped_mask);
+
 /* Same on device buffers, asynchronous on `stream` (a hipStream_t, 0 for the
  * null stream).  experts/w are read on the host during the call. */
 int eahmmf_hip_moe_decode_async(const eahmmf_hip_moe_shape* shape, const eahmmf_hip_expert_ptrs* experts,

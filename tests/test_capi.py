@@ -33,7 +33,10 @@ def test_invalid_arguments_fail_without_touching_the_device(binding, hip):
     assert not hip.eahmmf_hip_matmul(fake, 2, 256, 8, 144, x.ctypes.data, 1, 256, out.ctypes.data, 8)
     assert "type" in hip.eahmmf_hip_last_error().decode()
     assert not hip.eahmmf_hip_matmul(fake, 12, 256, 8, 144, x.ctypes.data, 1, 128, out.ctypes.data, 8)
-    assert not hip.eahmmf_hip_matmul(fake, 12, 256, 8, 140, x.ctypes.data, 1, 256, out.ctypes.data, 8)
+    assert not hip.eahmmf_hip_matmul(fake, 12, 256, 8, 140, x.ctypes.data, 1, 256, out.ctypes.data, 8)  # too short
+    assert not hip.eahmmf_hip_matmul(fake, 12, 256, 8, 152, x.ctypes.data, 1, 256, out.ctypes.data, 8)  # unaligned
+    assert "multiple of 16" in hip.eahmmf_hip_last_error().decode()
+    assert not hip.eahmmf_hip_matmul(fake, 14, 256, 8, 211, x.ctypes.data, 1, 256, out.ctypes.data, 8)
     assert not hip.eahmmf_hip_matmul(fake, 12, 200, 8, 144, x.ctypes.data, 1, 256, out.ctypes.data, 8)
     assert not hip.eahmmf_hip_matmul_pair(fake, 12, 256, 8, 144, fake, 12, 256, 4, 144, x.ctypes.data, 1, 256,
                                           out.ctypes.data, 8, out.ctypes.data, 8)

@@ -102,6 +102,23 @@ def test_matmul_vs_oracle(torch_dev, hip, t, ne0, ne1, nb):
     assert np.all(out[:, ne1:] == 7.0)  # padding untouched
 
 
+@pytest.mark.parametrize("t,pad", [(Q4_K, 48), (Q6_K, 6), (Q8_0, 2), (Q5_K, 16)])
+def test_matmul_padded_row_stride(torch_dev, hip, t, pad):
+    """Rows at a stride longer than their blocks (the reference's matmul
+    takes any row_bytes, expert_cuda.cu:263-267): the padding is skipped."""
+    torch = torch_dev
+    ne0, ne1, nb = 512, 40, 3
+    rng = np.random.default_rng(t * 100 + pad)
+    w = synth.random_rows(t, ne1, ne0, rng)
+    wp = np.concatenate([w, rng.integers(0, 256, (ne1, pad), dtype=np.uint8)], axis=1)
+    x = rng.normal(0, 1, (nb, ne0)).astype(np.float32)
+    dw = to_dev(torch, wp)
+    out = np.empty((nb, ne1), dtype=np.float32)
+    assert hip.eahmmf_hip_matmul(ptr(dw), t, ne0, ne1, wp.shape[1], x.ctypes.data, nb, ne0, out.ctypes.data, ne1), \
+        hip.eahmmf_hip_last_error()
+    close(out, oracle.matmul(t, w, ne0, x))
+
+
 def test_matmul_golden_cases(torch_dev, hip):
     torch = torch_dev
     g = np.load(os.path.join(GOLDEN, "matmul_golden.npz"))
@@ -198,6 +215,45 @@ def test_moe_decode_vs_oracle(torch_dev, binding, hip, path, name, types, D, FF,
     assert hip.eahmmf_hip_moe_decode(experts, wk.ctypes.data, k, x.ctypes.data, y.ctypes.data), \
         hip.eahmmf_hip_last_error()
     close(y, want)
+
+
+def test_moe_decode_resident_subset(torch_dev, binding, hip, path):
+    """Partial residency (eahmmf.h:721-742): 3 of 8 routed experts have no
+    device copy.  The GPU computes the resident five and reports the other
+    three; their contributions added on the CPU (the oracle) give the
+    oracle's whole block."""
+    torch = torch_dev
+    D, FF, k = 2048, 768, 8
+    rng = np.random.default_rng(2024)
+    layer = make_layer(binding, (Q4_K, Q4_K, Q6_K), D, FF, k, rng)
+    x = rng.normal(0, 1, (1, D)).astype(np.float32)
+    ids = np.arange(k, dtype=np.int32)[None, :]
+    w = rng.uniform(0.05, 1.0, (1, k)).astype(np.float32)
+    w /= w.sum()
+    missing = [1, 4, 6]
+    dev = [[to_dev(torch, layer[e][c][1]) for c in range(3)] for e in range(k)]
+    experts = (binding.Expert * k)()
+    for j in range(k):
+        for c, (nm, ne0, ne1) in enumerate((("gate", D, FF), ("up", D, FF), ("down", FF, D))):
+            t = layer[j][c][0]
+            p = 0 if j in missing else dev[j][c].data_ptr()
+            setattr(experts[j], nm, binding.Weight(p, t, ne0, ne1, binding.row_bytes(t, ne0)))
+    y = np.full(D, np.nan, dtype=np.float32)
+    mask = ctypes.c_uint32(0xFFFF)
+    wk = np.ascontiguousarray(w[0])
+    assert hip.eahmmf_hip_moe_decode_resident(experts, wk.ctypes.data, k, x.ctypes.data, y.ctypes.data,
+                                              ctypes.byref(mask)), binding.last_error()
+    assert mask.value == sum(1 << j for j in missing)
+    keep = np.array([j for j in range(k) if j not in missing])
+    close(y, oracle.moe_layer(layer, x, ids[:, keep], w[:, keep])[0])
+    cpu = oracle.moe_layer(layer, x, ids[:, missing], w[:, missing])[0]
+    close(y + cpu, oracle.moe_layer(layer, x, ids, w)[0])
+    # none resident: zeros and a full mask, no launch
+    for j in range(k):
+        experts[j].gate.dev = 0
+    assert hip.eahmmf_hip_moe_decode_resident(experts, wk.ctypes.data, k, x.ctypes.data, y.ctypes.data,
+                                              ctypes.byref(mask))
+    assert mask.value == (1 << k) - 1 and not y.any()
 
 
 @pytest.mark.parametrize("nbytes", [16, 4096 + 48, 3 * (1 << 20) + 16 * 37, 24_477_696, (1 << 28) + 4096 + 48])
