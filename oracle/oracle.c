@@ -14,6 +14,8 @@
 #include "oracle.h"
 
 #include <math.h>
+#include <omp.h>
+#include <time.h>
 #include <stdlib.h>
 #include <string.h>
 
@@ -200,6 +202,48 @@ int orc_matmul(int type, int64_t ne0, int64_t ne1, size_t row_bytes, const uint8
     return 0;
 }
 
+static float silu_mul(float g, float u) { return g / (1.0f + expf(-g)) * u; }
+
+/* The timed CPU baseline when the compiled reference is absent: the expert
+ * block of qwen3moe.cpp:1024-1067 at nb = 1 over n_tok tokens per
+ * repetition through orc_matmul (stacked experts: e's gate at
+ * gate + e*FF*grb, its down at down + e*D*drb; ids ascending per token);
+ * secs[i] = wall time of timed repetition i after `warmup` untimed ones. */
+int orc_time_expert_tokens(int gt, int dt, int D, int FF, size_t grb, size_t drb, const uint8_t* gate,
+                           const uint8_t* up, const uint8_t* down, const float* xs, const int* ids, const float* w,
+                           int k, int n_tok, int threads, int warmup, int reps, double* secs) {
+    if (!orc_blck(gt) || !orc_blck(dt) || threads < 1) return -1;
+    omp_set_num_threads(threads);
+    float* g = (float*)malloc(sizeof(float) * (size_t)FF);
+    float* u = (float*)malloc(sizeof(float) * (size_t)FF);
+    float* yd = (float*)malloc(sizeof(float) * (size_t)D);
+    float* y = (float*)malloc(sizeof(float) * (size_t)D);
+    for (int rep = 0; rep < warmup + reps; rep++) {
+        struct timespec t0, t1;
+        clock_gettime(CLOCK_MONOTONIC, &t0);
+        for (int t = 0; t < n_tok; t++) {
+            const float* x = xs + (size_t)t * D;
+            memset(y, 0, sizeof(float) * (size_t)D);
+            for (int j = 0; j < k; j++) {
+                const int e = ids[(size_t)t * k + j];
+                orc_matmul(gt, D, FF, grb, gate + (size_t)e * FF * grb, x, 1, D, g, FF);
+                orc_matmul(gt, D, FF, grb, up + (size_t)e * FF * grb, x, 1, D, u, FF);
+                for (int i = 0; i < FF; i++) g[i] = silu_mul(g[i], u[i]);
+                orc_matmul(dt, FF, D, drb, down + (size_t)e * D * drb, g, 1, FF, yd, D);
+                const float wj = w[(size_t)t * k + j];
+                for (int r = 0; r < D; r++) y[r] += wj * yd[r];
+            }
+        }
+        clock_gettime(CLOCK_MONOTONIC, &t1);
+        if (rep >= warmup) secs[rep - warmup] = (double)(t1.tv_sec - t0.tv_sec) + 1e-9 * (double)(t1.tv_nsec - t0.tv_nsec);
+    }
+    free(g);
+    free(u);
+    free(yd);
+    free(y);
+    return 0;
+}
+
 /* qwen3moe.cpp:527-532 */
 void orc_rmsnorm(const float* x, const float* w, float* out, int n, float eps) {
     float ss = 0.f;
@@ -242,7 +286,6 @@ void orc_expf_array(const float* x, float* y, int64_t n) {
     for (int64_t i = 0; i < n; i++) y[i] = expf(x[i]);
 }
 
-static float silu_mul(float g, float u) { return g / (1.0f + expf(-g)) * u; }
 
 /* qwen3moe.cpp:1024-1067 */
 int orc_moe_layer(const orc_experts* ex, const float* xn, int nb, int k,

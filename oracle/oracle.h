@@ -49,6 +49,9 @@ int orc_dequant_rows(int type, const uint8_t* w, int64_t ne0, int64_t nrows, siz
 /* out[t*ldo + r] = sum_k W[r,k] * x[t*ldx + k], block-wise fp32 like the reference */
 int orc_matmul(int type, int64_t ne0, int64_t ne1, size_t row_bytes, const uint8_t* w,
                const float* x, int nb, int ldx, float* out, int ldo);
+int orc_time_expert_tokens(int gt, int dt, int D, int FF, size_t grb, size_t drb, const uint8_t* gate,
+                           const uint8_t* up, const uint8_t* down, const float* xs, const int* ids, const float* w,
+                           int k, int n_tok, int threads, int warmup, int reps, double* secs);
 void orc_rmsnorm(const float* x, const float* w, float* out, int n, float eps);
 
 /* softmax -> top-k (e desc, index asc) -> renorm in rank order.
