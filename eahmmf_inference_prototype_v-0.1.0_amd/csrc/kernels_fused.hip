@@ -412,9 +412,14 @@ __device__ void route_keys(const FusedArgs& a, FusedLds& L, int lane, After afte
     after_loads();
     float mx = fmaxf(fmaxf(l[0], l[1]), fmaxf(l[2], l[3]));
     mx = dpp_max(mx);
+    const int nc = (n + 63) / 64;  // chunks of 64 ids holding candidates (wave-uniform)
 #pragma unroll
     for (int c = 0; c < 4; c++) {
         const int id = lane + 64 * c;
+        if (c >= nc) {  // no candidate in this chunk: its keys rank last
+            L.rkey[id] = (uint64_t)(uint32_t)~id;
+            continue;
+        }
         double rr;
         uint64_t ki;
         float sp;
@@ -829,6 +834,11 @@ __device__ void fused_body(const FusedArgs& a, FusedLds& L) {
 
     SegCodes<DT> pre[NPD];  // B waves: their first phase-B tasks, decoded
     BTask tb[NPD];          // and where those tasks are
+    // A waves: the round-0 task after the B waves' (task (8 - 4) NPD + wave),
+    // decoded once the passes are done, while h is on its way
+    const int task_a = (kWaves - kAWaves) * NPD + wave;
+    SegCodes<DT> pre_a;
+    BTask tb_a;
     if (wave < kAWaves) {
         // ---- 2A. this wave's passes through its LDS ring.  Every load the
         // compiler issued is retired first: the copies below are invisible to
@@ -868,6 +878,14 @@ __device__ void fused_body(const FusedArgs& a, FusedLds& L) {
             }
             // every lane's reads of this slot have returned (their values are used above)
             if (pp + NPA < npass) issue(pp + NPA);
+        }
+        if (task_a < n_tasks0) {
+            wait_lds(&L.b_landed, (unsigned)(kWaves - kAWaves));  // the staged down rows
+            tb_a = btask(task_a, rr0, 0);
+            RawSeg<DT> raw;
+            raw.template load<LdsLd>(tb_a.row, tb_a.sg);
+            pre_a = raw.decode(tb_a.sg);
+            pre_a.pin_all();  // decoded here, not after the barrier
         }
         // ---- 4A. the partition's h as int8 levels, once every word carries
         // this launch's epoch (it overwrites the activation levels: every A
@@ -928,16 +946,19 @@ __device__ void fused_body(const FusedArgs& a, FusedLds& L) {
             const float v = k.dot(hs);
             if (t.r < rr) L.part[__mul24(__mul24(t.e, rr) + t.r, segB) + t.sg] = wgt[t.e] * v;
         };
-        int first = 0;
+        int first = wave;
         if (r0 == 0) {
             if (wave >= kAWaves) {
 #pragma unroll
                 for (int i = 0; i < NPD; i++)
                     if (wave - kAWaves + (kWaves - kAWaves) * i < n_tasks0) finish(tb[i], pre[i]);
+                first = (kWaves - kAWaves) * NPD + wave;
+            } else {
+                if (task_a < n_tasks0) finish(tb_a, pre_a);
+                first = task_a + kWaves;
             }
-            first = (kWaves - kAWaves) * NPD;
         }
-        for (int task = first + wave; task < n_tasks(rr); task += kWaves) {
+        for (int task = first; task < n_tasks(rr); task += kWaves) {
             const BTask t = btask(task, rr, r0);
             RawSeg<DT> raw;
             raw.template load<LdsLd>(t.row, t.sg);
