@@ -444,7 +444,138 @@ def bench_dropin(args, torch, b, hip):
         "us_per_call": round(el * 1e6 / (2 * K_), 2)}), flush=True)
 
 
+def device_blocks(torch, t, nrows, ne0, gen, scale):
+    """nrows rows of type t built on the device: random codes, fp16 scale
+    fields uniform in [0.5, 1.5) x scale (F32: N(0, scale) values)."""
+    if t == 0:
+        return torch.randn((nrows, ne0), device="cuda", generator=gen).mul_(scale)
+    blck, nbytes = {Q8_0: (32, 34), Q4_K: (256, 144), Q5_K: (256, 176), Q6_K: (256, 210)}[t]
+    nblk = nrows * (ne0 // blck)
+    raw = torch.randint(0, 256, (nblk, nbytes), dtype=torch.uint8, device="cuda", generator=gen)
+
+    def put(off):
+        d = (torch.rand(nblk, device="cuda", generator=gen) + 0.5).mul_(scale).half()
+        raw[:, off:off + 2] = d.view(torch.uint8).view(nblk, 2)
+
+    if t == Q6_K:
+        put(208)
+    else:
+        put(0)
+        if t in (Q4_K, Q5_K):
+            put(2)
+    return raw.view(nrows, (ne0 // blck) * nbytes)
+
+
+def c3_model(torch, b, expert_type, n_ctx, seed=3):
+    """The 48-layer Qwen3-30B-A3B-shaped model in HBM: D=2048, 32 query / 4 KV
+    heads of dim 128, 128 experts top-8, FF 768, vocab 151936; experts all
+    expert_type, attention, embedding and output head Q8_0, router F32, norm
+    weights 1.  Weights are generated on the device (random codes with
+    fp16 scales sized for ~0.02 weights) and borrowed by the model."""
+    NL, D_, NH, NKV, HD, E_, K_, FF_, V = 48, 2048, 32, 4, 128, 128, 8, 768, 151936
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(seed)
+    sc = {Q8_0: 3e-4, Q5_K: 5e-5, Q4_K: 1e-4, Q6_K: 1e-5}
+    keep, tensors = [], {}
+
+    def add(name, t, ne0, rows, ne=None, scale=None):
+        d = device_blocks(torch, t, rows, ne0, gen, sc.get(t, 0.02) if scale is None else scale)
+        keep.append(d)
+        tensors[name] = (t, ne if ne else [ne0, rows], d.data_ptr())
+
+    ones = torch.ones(D_, device="cuda")
+    ones_h = torch.ones(HD, device="cuda")
+    keep += [ones, ones_h]
+    add("token_embd.weight", Q8_0, D_, V)
+    add("output.weight", Q8_0, D_, V)
+    tensors["output_norm.weight"] = (0, [D_], ones.data_ptr())
+    for l in range(NL):
+        p = f"blk.{l}."
+        for nm in ("attn_norm", "ffn_norm"):
+            tensors[p + nm + ".weight"] = (0, [D_], ones.data_ptr())
+        for nm in ("attn_q_norm", "attn_k_norm"):
+            tensors[p + nm + ".weight"] = (0, [HD], ones_h.data_ptr())
+        add(p + "attn_q.weight", Q8_0, D_, NH * HD)
+        add(p + "attn_k.weight", Q8_0, D_, NKV * HD)
+        add(p + "attn_v.weight", Q8_0, D_, NKV * HD)
+        add(p + "attn_output.weight", Q8_0, NH * HD, D_)
+        add(p + "ffn_gate_inp.weight", 0, D_, E_, scale=0.02)
+        add(p + "ffn_gate_exps.weight", expert_type, D_, E_ * FF_, ne=[D_, FF_, E_])
+        add(p + "ffn_up_exps.weight", expert_type, D_, E_ * FF_, ne=[D_, FF_, E_])
+        add(p + "ffn_down_exps.weight", expert_type, FF_, E_ * D_, ne=[FF_, D_, E_])
+    torch.cuda.synchronize()
+    hp = dict(n_layer=NL, D=D_, n_head=NH, n_kv=NKV, hd=HD, n_expert=E_, n_used=K_, FF=FF_, n_vocab=V, n_ctx=n_ctx,
+              eps=1e-6, rope_base=1e6)
+    m = b.DeviceModel(hp, tensors)
+    return m, keep, hp
+
+
+def c3_token_bytes(b, hp, expert_type, n_pos):
+    """Algorithmic HBM bytes of one decode token at n_pos cached positions:
+    every dense weight once (Q, K, V, output projections, router, output
+    head), the 8 routed experts' three matrices per layer, the K and V rows of
+    n_pos positions per layer (fp32) plus the new row, one embedding row."""
+    D_, FF_, NL, KD, QD = hp["D"], hp["FF"], hp["n_layer"], hp["n_kv"] * hp["hd"], hp["n_head"] * hp["hd"]
+    q8 = lambda ne0: b.row_bytes(Q8_0, ne0)
+    dense = (QD + 2 * KD) * q8(D_) + D_ * q8(QD) + hp["n_expert"] * D_ * 4
+    experts = hp["n_used"] * (2 * FF_ * b.row_bytes(expert_type, D_) + D_ * b.row_bytes(expert_type, FF_))
+    kv = 2 * (n_pos + 1) * KD * 4
+    return NL * (dense + experts + kv) + hp["n_vocab"] * q8(D_) + q8(D_)
+
+
 def bench_c3(args, torch, b, hip):
+    """Single-token decode of the full 48-layer Qwen3-30B-A3B-shaped model at
+    a 2048-token KV context (every layer on the device: attention with its
+    Q8_0 projections, norms, RoPE, KV cache, router, the fused expert block,
+    output head, greedy argmax), for the two expert variants all-Q5_K and
+    all-Q8_0.  The KV cache is filled by a 2048-token prefill (batches of 64);
+    the timed region is one eahmmf_hip_model_generate_greedy call of `steps`
+    tokens (one host wait at its end).  value = tokens/s of the Q5_K variant."""
+    CTX = 2048
+    steps = args.steps if args.steps else 64
+    warm = args.warmup if args.warmup else 8
+    rng = np.random.default_rng(5)
+    results = {}
+    for name, et in (("q5_k", Q5_K), ("q8_0", Q8_0)):
+        t0 = time.perf_counter()
+        m, keep, hp = c3_model(torch, b, et, CTX + warm + steps + 1)
+        t_build = time.perf_counter() - t0
+        prompt = rng.integers(0, hp["n_vocab"], CTX - warm).astype(np.int32)
+        t0 = time.perf_counter()
+        lg = m.eval(prompt, 0, 64)
+        t_prefill = time.perf_counter() - t0
+        assert np.isfinite(lg).all(), "non-finite logits after the prefill"
+        first = int(np.argmax(lg))
+        toks, lg = m.generate_greedy(first, CTX - warm, warm)
+        t0 = time.perf_counter()
+        toks, lg = m.generate_greedy(int(toks[-1]), CTX, steps)
+        el = time.perf_counter() - t0
+        assert np.isfinite(lg).all(), "non-finite logits after decode"
+        bt = c3_token_bytes(b, hp, et, CTX + steps // 2)
+        results[name] = {"tokens_per_s": round(steps / el, 1), "ms_per_token": round(el * 1e3 / steps, 4),
+                         "bytes_per_token": bt, "GB_s": round(bt * steps / el / 1e9, 1),
+                         "pct_of_hbm_peak": round(100 * bt * steps / el / 1e9 / HBM_PEAK_GBS, 2),
+                         "prefill_tokens_per_s": round(len(prompt) / t_prefill, 1),
+                         "build_s": round(t_build, 1)}
+        print(f"# c3 {name}: {results[name]}", file=sys.stderr, flush=True)
+        m.close()
+        del keep
+        torch.cuda.empty_cache()
+    r = results["q5_k"]
+    print(json.dumps({
+        "metric": "decode tokens/s, 48-layer Qwen3-30B-A3B-shaped model, 2048-token KV context", "unit": "tokens/s",
+        "value": r["tokens_per_s"], "n_gpus": 1, "steps": steps, "warmup": warm, "ms_per_step": r["ms_per_token"],
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32", "data": "synthetic",
+        "config": {"workload": "single-token greedy decode, 48 layers D=2048 32/4 heads hd=128, 128 experts top-8 "
+                               "FF=768, vocab 151936, KV context 2048 (prefilled), experts Q5_K (value) / Q8_0, "
+                               "attention + embedding + output head Q8_0, router F32; everything on the device"},
+        "roofline": {"bound": "hbm", "kernel": "whole decode token (all launches)",
+                     "achieved": r["GB_s"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(r["GB_s"] / HBM_PEAK_GBS, 4), "traffic": None},
+        "variants": results}), flush=True)
+
+
+def bench_c3_experts(args, torch, b, hip):
     """Expert-only decode of one token through all 48 MoE layers of the
     Qwen3-30B-A3B shape (D=2048, FF=768, 128 experts, top-8), every layer
     resident at its own HBM addresses; one step = 48 layer launches (routing on
@@ -674,8 +805,9 @@ def main():
     ap.add_argument("--cpu-tokens", type=int, default=64, help="C2 layer-tokens per CPU-baseline repetition")
     ap.add_argument("--cpu-child", type=int, default=0, help=argparse.SUPPRESS)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--workload", choices=("c2", "c3", "c4", "c5", "c5b16", "stream", "staging", "dropin"), default="c2",
-                    help="c2 (default): the headline single-token layer; c3: one token through 48 layers; "
+    ap.add_argument("--workload", choices=("c2", "c3", "c3x", "c4", "c5", "c5b16", "stream", "staging", "dropin"), default="c2",
+                    help="c2 (default): the headline single-token layer; c3: one decode token through the whole "
+                         "48-layer model; c3x: the 48 layers' expert blocks only; "
                          "c4: ragged grouped prefill; c5: single-token layer at the 235B shape; "
                          "c5b16: a 16-sequence decode batch at the 235B shape; "
                          "stream: the achievable HBM read rate (streaming-read kernel); "
@@ -704,7 +836,7 @@ def main():
     if args.workload != "c2":
         hip_ = b.lib()
         torch.cuda.set_device(0)
-        {"c3": bench_c3, "c4": bench_c4, "c5": bench_c5, "c5b16": bench_c5_batch, "stream": bench_stream,
+        {"c3": bench_c3, "c3x": bench_c3_experts, "c4": bench_c4, "c5": bench_c5, "c5b16": bench_c5_batch, "stream": bench_stream,
          "staging": bench_staging, "dropin": bench_dropin}[args.workload](args, torch, b, hip_)
         return
     hip = b.lib()

@@ -151,4 +151,54 @@ bool fused_path_enabled();
 int noalloc_device_flags();
 bool type_supported(int t);
 
+// Dense decode steps (kernels_dense.hip), nb tokens at positions p0 ...
+// x[t] = dequantized row toks[t] of tab (or, with key, nb = 1: the argmax id
+// held in the key, which is cleared and stored in *hist if given); a token id
+// outside [0, n_vocab) sets *bad.
+hipError_t launch_embed(int type, const uint8_t* tab, size_t row_bytes, int n_vocab, int D, const int* toks,
+                        unsigned long long* key, int* hist, int nb, float* x, int* bad, hipStream_t st);
+hipError_t launch_rmsnorm(const float* x, const float* w, float* out, int rows, int n, float eps, hipStream_t st);
+// Floats of partial-result scratch launch_attention needs for nb tokens whose
+// last position is n_pos - 1.
+size_t attention_part_floats(int nb, int n_head, int hd, int n_pos);
+// Causal attention of nb tokens at p0.. from raw q [nb][n_head*hd], k/v
+// [nb][n_kv*hd]: head RMSNorm + NeoX RoPE (rope [pos][hd/2] cos/sin pairs),
+// the batch's K/V rows appended to kc/vc (this layer's [n_ctx][n_kv*hd]),
+// out [nb][n_head*hd].  cnt: nb * n_kv counters, zero before the first
+// launch (each launch leaves them zero).  hd 64 or 128, n_head / n_kv in
+// {1, 2, 4, 8, 16}.
+bool attention_supported(int n_head, int n_kv, int hd);
+hipError_t launch_attention(const float* q, const float* k, const float* v, const float* q_norm, const float* k_norm,
+                            const float* rope, float* kc, float* vc, float* out, int nb, int n_head, int n_kv, int hd,
+                            int p0, float eps, float scale, float* part, unsigned* cnt, hipStream_t st);
+// Single-token matrix-vector products with fused input and output steps
+// (kernels_gemv.hip).  Up to three weight matrices of one type and row
+// length; out[r] = (resid ? resid[r] : 0) + sum_i W[r][i] * in[i] where
+// in = x (+ x_add), RMS-normalized with norm_w when given.  Block 0 stores
+// x + x_add in x_sum_out and the normalized input in xn_out when given.
+// amax (if set) receives atomicMax of (ordered value, ~global row) keys.
+struct GemvSeg {
+    const uint8_t* w;
+    float* out;
+    const float* resid;
+    int rows;
+};
+struct GemvArgs {
+    GemvSeg seg[3];
+    int nseg;
+    int ne0, rb;
+    int ni, rpw, nbuf, total_rows;  // set by launch_gemv
+    const float* x;
+    const float* x_add;
+    const float* norm_w;
+    float eps;
+    float* x_sum_out;
+    float* xn_out;
+    unsigned long long* amax;
+};
+bool gemv_supported(int type, int ne0, size_t rb);
+hipError_t launch_gemv(int type, GemvArgs a, hipStream_t st);
+
+hipError_t launch_add(float* x, const float* y, size_t n, hipStream_t st);
+
 }  // namespace eahmmf

@@ -171,14 +171,15 @@ __device__ __forceinline__ void scale_min_k4(int j, uint32_t s0, uint32_t s1, ui
 // Segment decoders: 32 dequantized values, bit-identical to the reference.
 // `blk` points at the block (super-block) start; `j` is the segment in it.
 
+template <class LD = GlobalLd>
 __device__ __forceinline__ void decode_seg_q4k(const uint8_t* blk, int j, float* w) {
-    const uint4 hdr = ld16(blk);
+    const uint4 hdr = LD::b16(blk);
     const float d = half_to_float(hdr.x & 0xFFFFu), dmin = half_to_float(hdr.x >> 16);
     uint32_t sc, mn;
     scale_min_k4(j, hdr.y, hdr.z, hdr.w, sc, mn);
     const float ds = d * (float)sc, dm = dmin * (float)mn;
     const int g = j >> 1, sh = (j & 1) * 4;
-    const uint4 a = ld16(blk + 16 + 32 * g), b = ld16(blk + 32 + 32 * g);
+    const uint4 a = LD::b16(blk + 16 + 32 * g), b = LD::b16(blk + 32 + 32 * g);
     const uint32_t q[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
 #pragma unroll
     for (int i = 0; i < 32; i++) {
@@ -187,15 +188,16 @@ __device__ __forceinline__ void decode_seg_q4k(const uint8_t* blk, int j, float*
     }
 }
 
+template <class LD = GlobalLd>
 __device__ __forceinline__ void decode_seg_q5k(const uint8_t* blk, int j, float* w) {
-    const uint4 hdr = ld16(blk);
+    const uint4 hdr = LD::b16(blk);
     const float d = half_to_float(hdr.x & 0xFFFFu), dmin = half_to_float(hdr.x >> 16);
     uint32_t sc, mn;
     scale_min_k4(j, hdr.y, hdr.z, hdr.w, sc, mn);
     const float ds = d * (float)sc, dm = dmin * (float)mn;
     const int g = j >> 1, sh = (j & 1) * 4;
-    const uint4 h0 = ld16(blk + 16), h1 = ld16(blk + 32);
-    const uint4 a = ld16(blk + 48 + 32 * g), b = ld16(blk + 64 + 32 * g);
+    const uint4 h0 = LD::b16(blk + 16), h1 = LD::b16(blk + 32);
+    const uint4 a = LD::b16(blk + 48 + 32 * g), b = LD::b16(blk + 64 + 32 * g);
     const uint32_t q[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
     const uint32_t qh[8] = {h0.x, h0.y, h0.z, h0.w, h1.x, h1.y, h1.z, h1.w};
 #pragma unroll
@@ -206,12 +208,13 @@ __device__ __forceinline__ void decode_seg_q5k(const uint8_t* blk, int j, float*
     }
 }
 
+template <class LD = GlobalLd>
 __device__ __forceinline__ void decode_seg_q6k(const uint8_t* blk, int j, float* w) {
     const int n = j >> 2, u = j & 3;
-    const float d = half_to_float(ld_u16(blk + 208));
-    const Bytes32A2 lo = ld32_a2(blk + 64 * n + 32 * (u & 1));
-    const Bytes32A2 hi = ld32_a2(blk + 128 + 32 * n);
-    const uint16_t scw = ld_u16(blk + 192 + 8 * n + 2 * u);  // scales for l<16 and l>=16
+    const float d = half_to_float(LD::u16(blk + 208));
+    const Bytes32A2 lo = LD::b32a2(blk + 64 * n + 32 * (u & 1));
+    const Bytes32A2 hi = LD::b32a2(blk + 128 + 32 * n);
+    const uint16_t scw = LD::u16(blk + 192 + 8 * n + 2 * u);  // scales for l<16 and l>=16
     const float ds0 = d * (float)(int8_t)(scw & 0xFFu);
     const float ds1 = d * (float)(int8_t)(scw >> 8);
     const int shl = (u >> 1) * 4, shh = 2 * u;
@@ -224,9 +227,10 @@ __device__ __forceinline__ void decode_seg_q6k(const uint8_t* blk, int j, float*
     }
 }
 
+template <class LD = GlobalLd>
 __device__ __forceinline__ void decode_seg_q8_0(const uint8_t* blk, float* w) {
-    const float d = half_to_float(ld_u16(blk));
-    const Bytes32A2 q = ld32_a2(blk + 2);
+    const float d = half_to_float(LD::u16(blk));
+    const Bytes32A2 q = LD::b32a2(blk + 2);
 #pragma unroll
     for (int i = 0; i < 32; i++) w[i] = d * (float)(int8_t)byte_of(q.w[i >> 2], i & 3);
 }
@@ -241,12 +245,12 @@ __device__ __forceinline__ void decode_seg_f32(const uint8_t* blk, float* w) {
 }
 
 // Segment s (0-based, 32 values each) of a row.
-template <int T>
+template <int T, class LD = GlobalLd>
 __device__ __forceinline__ void decode_row_seg(const uint8_t* row, int s, float* w) {
-    if constexpr (T == kQ4_K) decode_seg_q4k(row + (size_t)(s >> 3) * 144, s & 7, w);
-    else if constexpr (T == kQ5_K) decode_seg_q5k(row + (size_t)(s >> 3) * 176, s & 7, w);
-    else if constexpr (T == kQ6_K) decode_seg_q6k(row + (size_t)(s >> 3) * 210, s & 7, w);
-    else if constexpr (T == kQ8_0) decode_seg_q8_0(row + (size_t)s * 34, w);
+    if constexpr (T == kQ4_K) decode_seg_q4k<LD>(row + (size_t)(s >> 3) * 144, s & 7, w);
+    else if constexpr (T == kQ5_K) decode_seg_q5k<LD>(row + (size_t)(s >> 3) * 176, s & 7, w);
+    else if constexpr (T == kQ6_K) decode_seg_q6k<LD>(row + (size_t)(s >> 3) * 210, s & 7, w);
+    else if constexpr (T == kQ8_0) decode_seg_q8_0<LD>(row + (size_t)s * 34, w);
     else decode_seg_f32(row + (size_t)s * 128, w);
 }
 

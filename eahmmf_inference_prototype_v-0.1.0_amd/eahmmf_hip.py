@@ -26,6 +26,9 @@ EXPORTS = (
     "eahmmf_hip_moe_grouped_async", "eahmmf_hip_set_grouped_mfma", "eahmmf_hip_stream_read_async",
     "eahmmf_hip_h2d_batch", "eahmmf_hip_fused_status_async", "eahmmf_hip_set_fault_injection",
     "eahmmf_hip_moe_layer_decode_noalloc", "eahmmf_hip_expf_ref_async", "eahmmf_hip_moe_decode_resident",
+    "eahmmf_hip_model_create", "eahmmf_hip_model_forward", "eahmmf_hip_model_eval", "eahmmf_hip_model_generate_greedy",
+    "eahmmf_hip_model_set_trace", "eahmmf_hip_model_trace", "eahmmf_hip_model_trace_clear", "eahmmf_hip_model_stream",
+    "eahmmf_hip_model_free",
 )
 
 
@@ -50,6 +53,23 @@ class MoeShape(ctypes.Structure):
     _fields_ = [("gate_type", ctypes.c_int), ("up_type", ctypes.c_int), ("down_type", ctypes.c_int),
                 ("D", ctypes.c_int), ("FF", ctypes.c_int), ("gate_row_bytes", ctypes.c_size_t),
                 ("up_row_bytes", ctypes.c_size_t), ("down_row_bytes", ctypes.c_size_t)]
+
+
+class Tensor(ctypes.Structure):
+    _fields_ = [("data", ctypes.c_void_p), ("on_device", ctypes.c_int), ("type", ctypes.c_int),
+                ("ne0", ctypes.c_int64), ("ne1", ctypes.c_int64), ("row_bytes", ctypes.c_size_t)]
+
+
+class LayerDesc(ctypes.Structure):
+    _fields_ = [(n, Tensor) for n in ("attn_norm", "ffn_norm", "q_norm", "k_norm", "wq", "wk", "wv", "wo", "router",
+                                      "gate_exps", "up_exps", "down_exps")]
+
+
+class ModelDesc(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_int) for n in ("n_layer", "D", "n_head", "n_kv", "hd", "n_expert", "n_used", "FF",
+                                            "n_vocab", "n_ctx")] + \
+               [("eps", ctypes.c_float), ("rope_base", ctypes.c_float), ("tok_embd", Tensor),
+                ("output_norm", Tensor), ("output", Tensor), ("layers", ctypes.POINTER(LayerDesc))]
 
 
 def row_bytes(gtype, ne0):
@@ -107,6 +127,15 @@ def load(path=LIB_PATH):
         "eahmmf_hip_expf_ref_async": (c_int, [vp, vp, c_i64, vp]),
         "eahmmf_hip_moe_decode_resident": (c_bool, [ctypes.POINTER(Expert), vp, c_int, vp, vp, vp]),
         "eahmmf_hip_h2d_batch": (c_int, [ctypes.POINTER(Copy), c_int]),
+        "eahmmf_hip_model_create": (vp, [ctypes.POINTER(ModelDesc)]),
+        "eahmmf_hip_model_forward": (c_int, [vp, vp, c_int, c_int, vp]),
+        "eahmmf_hip_model_eval": (c_int, [vp, vp, c_int, c_int, c_int, vp]),
+        "eahmmf_hip_model_generate_greedy": (c_int, [vp, c_int, c_int, c_int, vp, vp]),
+        "eahmmf_hip_model_set_trace": (c_int, [vp, c_int]),
+        "eahmmf_hip_model_trace": (c_int, [vp, vp, vp, c_int]),
+        "eahmmf_hip_model_trace_clear": (None, [vp]),
+        "eahmmf_hip_model_stream": (vp, [vp]),
+        "eahmmf_hip_model_free": (None, [vp]),
         "eahmmf_hip_dequantize": (c_int, [vp, c_int, c_i64, c_i64, c_sz, vp, vp]),
         "eahmmf_hip_row_bytes": (c_sz, [c_int, c_i64]),
         "eahmmf_hip_quantize_rows": (c_i64, [c_int, vp, c_i64, c_i64, vp]),
@@ -152,3 +181,115 @@ def quantize_rows(gtype, src):
     if n != nrows * rb:
         raise RuntimeError(f"quantize_rows failed: {last_error()}")
     return out
+
+
+_HP = ("n_layer", "D", "n_head", "n_kv", "hd", "n_expert", "n_used", "FF", "n_vocab", "n_ctx")
+_LAYER = (("attn_norm", "attn_norm"), ("ffn_norm", "ffn_norm"), ("q_norm", "attn_q_norm"), ("k_norm", "attn_k_norm"),
+          ("wq", "attn_q"), ("wk", "attn_k"), ("wv", "attn_v"), ("wo", "attn_output"), ("router", "ffn_gate_inp"),
+          ("gate_exps", "ffn_gate_exps"), ("up_exps", "ffn_up_exps"), ("down_exps", "ffn_down_exps"))
+
+
+class DeviceModel:
+    """A whole Qwen3-MoE model on the current device (eahmmf_hip_model_*): the
+    reference's Engine (qwen3moe.cpp:859-1084) with every layer on the GPU.
+
+    ``hp``: mapping with n_layer, D, n_head, n_kv, hd, n_expert, n_used, FF,
+    n_vocab, n_ctx, eps, rope_base.  ``tensors``: GGUF tensor name ->
+    (ggml type, ne with ne0 first, data), data a numpy array of the tensor's
+    bytes or values (copied to the device at creation) or an int device
+    address (used in place; the caller keeps it alive).  A missing
+    ``output.weight`` ties the output head to ``token_embd.weight``
+    (qwen3moe.cpp:881-882)."""
+
+    def __init__(self, hp, tensors):
+        import numpy as np
+        self._lib = lib()
+        keep = []
+
+        def desc(name):
+            t, ne, data = tensors[name]
+            ne0 = int(ne[0])
+            ne1 = int(np.prod([int(v) for v in ne[1:]])) if len(ne) > 1 else 1
+            if isinstance(data, int):
+                return Tensor(data, 1, t, ne0, ne1, row_bytes(t, ne0))
+            arr = np.ascontiguousarray(data)
+            keep.append(arr)
+            return Tensor(arr.ctypes.data, 0, t, ne0, ne1, row_bytes(t, ne0))
+
+        L = int(hp["n_layer"])
+        layers = (LayerDesc * L)()
+        for l in range(L):
+            for field, nm in _LAYER:
+                setattr(layers[l], field, desc(f"blk.{l}.{nm}.weight"))
+        d = ModelDesc()
+        for n in _HP:
+            setattr(d, n, int(hp[n]))
+        d.eps = float(hp["eps"])
+        d.rope_base = float(hp["rope_base"])
+        d.tok_embd = desc("token_embd.weight")
+        d.output_norm = desc("output_norm.weight")
+        d.output = desc("output.weight") if "output.weight" in tensors else Tensor()
+        d.layers = layers
+        self.n_vocab = int(hp["n_vocab"])
+        self.n_layer, self.n_used = L, int(hp["n_used"])
+        self.h = self._lib.eahmmf_hip_model_create(ctypes.byref(d))
+        if not self.h:
+            raise RuntimeError(f"eahmmf_hip_model_create: {last_error()}")
+
+    def _check(self, rc, what):
+        if rc != 0:
+            raise RuntimeError(f"{what} ({rc}): {last_error()}")
+
+    def forward(self, toks, p0, logits=True):
+        """Engine::forward: tokens at p0..; the last token's logits (or None)."""
+        import numpy as np
+        t = np.ascontiguousarray(toks, dtype=np.int32)
+        out = np.empty(self.n_vocab, np.float32) if logits else None
+        self._check(self._lib.eahmmf_hip_model_forward(self.h, t.ctypes.data, len(t), int(p0),
+                                                       out.ctypes.data if logits else None), "forward")
+        return out
+
+    def eval(self, toks, p0, n_batch):
+        """Engine::eval: chunks of n_batch from p0; the last token's logits."""
+        import numpy as np
+        t = np.ascontiguousarray(toks, dtype=np.int32)
+        out = np.empty(self.n_vocab, np.float32)
+        self._check(self._lib.eahmmf_hip_model_eval(self.h, t.ctypes.data, len(t), int(p0), int(n_batch),
+                                                    out.ctypes.data), "eval")
+        return out
+
+    def generate_greedy(self, first, p0, n):
+        """Feeds ``first`` at p0 and then each argmax, n forwards in all, with
+        one host synchronisation; returns (the n argmax tokens, last logits)."""
+        import numpy as np
+        toks = np.empty(n, np.int32)
+        lg = np.empty(self.n_vocab, np.float32)
+        self._check(self._lib.eahmmf_hip_model_generate_greedy(self.h, int(first), int(p0), int(n), toks.ctypes.data,
+                                                               lg.ctypes.data), "generate_greedy")
+        return toks, lg
+
+    def set_trace(self, on):
+        return self._lib.eahmmf_hip_model_set_trace(self.h, 1 if on else 0)
+
+    def trace(self):
+        """(ids, weights) recorded since the last clear, per forward: layer, token, rank."""
+        import numpy as np
+        n = self._lib.eahmmf_hip_model_trace(self.h, None, None, 0)
+        ids, w = np.empty(n, np.int32), np.empty(n, np.float32)
+        self._lib.eahmmf_hip_model_trace(self.h, ids.ctypes.data, w.ctypes.data, n)
+        return ids, w
+
+    def trace_clear(self):
+        self._lib.eahmmf_hip_model_trace_clear(self.h)
+
+    @property
+    def stream(self):
+        return self._lib.eahmmf_hip_model_stream(self.h)
+
+    def close(self):
+        if getattr(self, "h", None):
+            self._lib.eahmmf_hip_model_free(self.h)
+            self.h = None
+
+    def __del__(self):
+        self.close()

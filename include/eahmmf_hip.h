@@ -282,6 +282,70 @@ int eahmmf_hip_fused_status_async(unsigned* dst, void* stream);
  * kernel's own bounded waits give up while every kernel still exits
  * normally.  Not for production use. */
 void eahmmf_hip_set_fault_injection(unsigned spin_limit, int drop_partition);
+/* ---------------------------------------------------------------------------
+ * Whole-model decode on the device.  The reference's Engine
+ * (qwen3moe.cpp:859-1084) runs embedding, attention, norms, RoPE, the KV
+ * cache, the router and the output head on the CPU and sends expert matmuls
+ * to the GPU; this engine keeps the entire forward on one device: token
+ * embedding, RMSNorm, the Q/K/V/output projections and the router and output
+ * head (the quantized matmul kernel, any supported type incl. F32), per-head
+ * Q/K RMSNorm with NeoX RoPE, an fp32 KV cache [n_layer][n_ctx][n_kv * hd],
+ * causal attention, and the expert block (the fused routed layer kernel for
+ * one token, routing + grouped kernels for a batch).  No counterpart entry
+ * point exists in the reference; the arguments mirror Engine::load /
+ * forward / eval and the routing trace (qwen3moe.cpp:862-922, 932-1084). */
+typedef struct {
+    const void* data;  /* the tensor's bytes: rows of row_bytes */
+    int on_device;     /* 0: host memory, copied at create; 1: device memory, borrowed */
+    int type;          /* 0 F32, 8 Q8_0, 12 Q4_K, 13 Q5_K, 14 Q6_K */
+    int64_t ne0, ne1;  /* values per row, rows (stacked expert tensors: n_expert * rows) */
+    size_t row_bytes;
+} eahmmf_hip_tensor;
+
+/* One layer's tensors (GGUF names blk.N.*, qwen3moe.cpp:883-905).  The
+ * norm weights are F32 vectors (ne1 = 1); gate/up/down_exps hold the
+ * n_expert experts back to back (expert e's gate at e * FF * row_bytes). */
+typedef struct {
+    eahmmf_hip_tensor attn_norm, ffn_norm, q_norm, k_norm;
+    eahmmf_hip_tensor wq, wk, wv, wo, router;
+    eahmmf_hip_tensor gate_exps, up_exps, down_exps;
+} eahmmf_hip_layer_desc;
+
+typedef struct {
+    int n_layer, D, n_head, n_kv, hd, n_expert, n_used, FF, n_vocab, n_ctx;
+    float eps, rope_base;
+    eahmmf_hip_tensor tok_embd, output_norm, output; /* output.data null: tied to tok_embd */
+    const eahmmf_hip_layer_desc* layers;             /* n_layer entries */
+} eahmmf_hip_model_desc;
+
+/* Builds a model on the current device: copies host tensors, builds the
+ * expert tables, the RoPE table (cos/sin of pos * inv_freq as the reference
+ * computes them, in double) and a zeroed KV cache.  NULL on failure
+ * (eahmmf_hip_last_error says why): unsupported shape or type, out of memory. */
+void* eahmmf_hip_model_create(const eahmmf_hip_model_desc* desc);
+/* Engine::forward: nb (1..64) host tokens at positions p0 .. p0+nb-1; if
+ * logits is non-null, the host receives the last token's n_vocab logits.
+ * Synchronous.  0 on success; -1 bad arguments (batch size, context overflow,
+ * token id out of range); -3 a HIP error or a fused expert launch that gave
+ * up a wait (outputs invalid). */
+int eahmmf_hip_model_forward(void* model, const int* toks, int nb, int p0, float* logits);
+/* Engine::eval: n tokens from p0 in chunks of n_batch (1..64); logits of the last. */
+int eahmmf_hip_model_eval(void* model, const int* toks, int n, int p0, int n_batch, float* logits);
+/* Greedy decoding without host round trips: feeds `first` at position p0,
+ * then n - 1 times the argmax (first largest) of the last logits; out_toks
+ * receives the n argmax tokens; last_logits (may be null) the final logits.
+ * One synchronisation at the end.  Same return codes as forward. */
+int eahmmf_hip_model_generate_greedy(void* model, int first, int p0, int n, int* out_toks, float* last_logits);
+/* Routing trace (Engine::trace_routing): when on, every forward appends, per
+ * layer and token, the n_used expert ids and weights in routing order. */
+int eahmmf_hip_model_set_trace(void* model, int on);
+/* Copies up to cap trace entries; returns the number recorded. */
+int eahmmf_hip_model_trace(void* model, int* ids, float* w, int cap);
+void eahmmf_hip_model_trace_clear(void* model);
+/* The model's stream (a hipStream_t), for callers that time or order work around it. */
+void* eahmmf_hip_model_stream(void* model);
+void eahmmf_hip_model_free(void* model);
+
 const char* eahmmf_hip_last_error(void);
 int eahmmf_hip_device_count(void);
 /* Frees the calling device's scratch, staging buffers and stream. */
