@@ -159,3 +159,87 @@ def test_model_create_rejects_bad_shapes(torch_dev, binding):
     t["blk.1.attn_q.weight"] = (ty, [ne[0], ne[1] - 1], data)
     with pytest.raises(RuntimeError, match="attn_q"):
         binding.DeviceModel(hp, t)
+
+
+# ---------------------------------------------------------------------------
+# Long contexts and other head shapes, against the oracle's forward (the
+# golden runs above stop at 48 positions: one attention split).  A 2500-token
+# prompt takes 32 splits of 79 positions -- several chunks per wave, batch
+# rows inside splits, the cross-block merge -- and the decode steps after it
+# read a 2500-row cache.  Tolerance as above: 1e-4 absolute on the logits.
+
+def small_spec(seed, D, NH, NKV, HD, E, K, FF, V, NL, CTX, attn_type):
+    """A random model with the library's quantizer: experts Q8_0, attention
+    projections attn_type, everything else F32 ~ N(0, 0.02)."""
+    from conftest import load_binding
+    b = load_binding()
+    rng = np.random.default_rng(seed)
+    spec = gt.ModelSpec(n_layer=NL, D=D, n_head=NH, n_kv=NKV, hd=HD, n_expert=E, n_used=K, FF=FF, n_vocab=V,
+                        n_ctx=CTX, ctx_train=CTX, eps=1e-6, rope_base=1e6)
+
+    def n(*shape):
+        return rng.normal(0, 0.02, shape).astype(np.float32)
+
+    def addf(name, arr):
+        spec.add(name, gt.F32, list(reversed(arr.shape)), np.asarray(arr, np.float32))
+
+    def addq(name, t, arr):
+        if t == gt.F32:
+            return addf(name, arr)
+        spec.add(name, t, list(reversed(arr.shape)), b.quantize_rows(t, arr.reshape(-1, arr.shape[-1])))
+
+    addf("token_embd.weight", n(V, D))
+    addf("output.weight", n(V, D))
+    addf("output_norm.weight", 1 + n(D))
+    for l in range(NL):
+        p = f"blk.{l}."
+        addf(p + "attn_norm.weight", 1 + n(D))
+        addf(p + "ffn_norm.weight", 1 + n(D))
+        addf(p + "attn_q_norm.weight", 1 + n(HD))
+        addf(p + "attn_k_norm.weight", 1 + n(HD))
+        addq(p + "attn_q.weight", attn_type, n(NH * HD, D))
+        addq(p + "attn_k.weight", attn_type, n(NKV * HD, D))
+        addq(p + "attn_v.weight", attn_type, n(NKV * HD, D))
+        addq(p + "attn_output.weight", attn_type, n(D, NH * HD))
+        addf(p + "ffn_gate_inp.weight", n(E, D))
+        for nm, shape in (("ffn_gate_exps", (E, FF, D)), ("ffn_up_exps", (E, FF, D)), ("ffn_down_exps", (E, D, FF))):
+            spec.add(p + nm + ".weight", gt.Q8_0, list(reversed(shape)),
+                     b.quantize_rows(gt.Q8_0, n(*shape).reshape(-1, shape[-1])))
+    return spec
+
+
+@pytest.mark.parametrize("shape", [
+    dict(D=256, NH=4, NKV=2, HD=64, n_prompt=2500, attn=gt.F32),      # the config-0 heads, 32 splits
+    dict(D=256, NH=16, NKV=2, HD=128, n_prompt=2100, attn=gt.Q8_0),   # 8 query heads per KV head (30B-A3B)
+    dict(D=256, NH=32, NKV=2, HD=128, n_prompt=700, attn=gt.Q8_0),    # 16 per KV head (235B-A22B)
+    dict(D=256, NH=2, NKV=2, HD=64, n_prompt=300, attn=gt.Q8_0),      # one per KV head
+], ids=["hd64-grp2-2500", "hd128-grp8-2100", "hd128-grp16-700", "hd64-grp1-300"])
+def test_long_context_against_oracle(torch_dev, binding, shape):
+    import oracle
+    n_prompt = shape["n_prompt"]
+    spec = small_spec(3, shape["D"], shape["NH"], shape["NKV"], shape["HD"], 8, 2, 128, 512, 1, n_prompt + 8,
+                      shape["attn"])
+    prompt = np.random.default_rng(11).integers(0, spec.n_vocab, n_prompt).astype(np.int32)
+    m = binding.DeviceModel(hp_of(spec), spec.tensors)
+    try:
+        o = oracle.OracleModel(spec)
+        lg, lo = m.eval(prompt, 0, 64), o.eval(prompt, 0, 64)
+        np.testing.assert_allclose(lg, lo, rtol=0, atol=1e-4)
+        pos = n_prompt
+        for _ in range(4):
+            t = int(np.argmax(lo))
+            lg, lo = m.forward([t], pos), o.forward([t], pos)
+            pos += 1
+            np.testing.assert_allclose(lg, lo, rtol=0, atol=1e-4)
+        # the device greedy loop from the same state matches the host loop
+        toks, lg = m.generate_greedy(int(np.argmax(lo)), pos, 3)
+        want = []
+        t = int(np.argmax(lo))
+        for i in range(3):
+            lo = o.forward([t], pos + i)
+            t = int(np.argmax(lo))
+            want.append(t)
+        assert list(toks) == want
+        np.testing.assert_allclose(lg, lo, rtol=0, atol=1e-4)
+    finally:
+        m.close()
