@@ -8,6 +8,7 @@
 // with the same expression order per element; the sums run in parallel
 // (tree order instead of the reference's sequential one).  The single-token
 // projections and their norms are in kernels_gemv.hip.
+#include "dpp.h"
 #include "internal.h"
 #include "kquant.h"
 
@@ -128,13 +129,6 @@ struct AttnArgs {
     float eps, scale;
 };
 
-template <int LPH>
-__device__ __forceinline__ float group_sum(float v) {
-#pragma unroll
-    for (int off = LPH / 2; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
-    return v;
-}
-
 // Head RMSNorm + NeoX rotation of a head held DPL values per lane (lane
 // group of LPH lanes): x holds dims g*DPL .. g*DPL+DPL-1 (g = lane % LPH);
 // the partner holding dim d + HD/2 is lane ^ (LPH/2).  cs: the position's
@@ -142,20 +136,26 @@ __device__ __forceinline__ float group_sum(float v) {
 template <int HD, int LPH, int DPL>
 __device__ __forceinline__ void norm_rope(float (&x)[DPL], const float* __restrict__ nw, const float* __restrict__ cs,
                                           float eps, int g) {
+    const bool lo = g < LPH / 2;
+    const int i0 = (lo ? g : g - LPH / 2) * DPL;  // pair index of element 0
+    float wv[DPL], cv[DPL], sv[DPL];  // loaded first: in flight during the reduction
+#pragma unroll
+    for (int e = 0; e < DPL; e++) {
+        wv[e] = nw[g * DPL + e];
+        cv[e] = cs[2 * (i0 + e)];
+        sv[e] = cs[2 * (i0 + e) + 1];
+    }
     float ss = 0.f;
 #pragma unroll
     for (int e = 0; e < DPL; e++) ss += x[e] * x[e];
-    ss = group_sum<LPH>(ss);
+    ss = group_sum_all<LPH>(ss);
     const float sc = 1.0f / sqrtf(ss / (float)HD + eps);
 #pragma unroll
-    for (int e = 0; e < DPL; e++) x[e] = x[e] * sc * nw[g * DPL + e];
-    const bool lo = g < LPH / 2;
-    const int i0 = (lo ? g : g - LPH / 2) * DPL;  // pair index of element 0
+    for (int e = 0; e < DPL; e++) x[e] = x[e] * sc * wv[e];
 #pragma unroll
     for (int e = 0; e < DPL; e++) {
         const float other = __shfl_xor(x[e], LPH / 2, 64);
-        const float c = cs[2 * (i0 + e)], s = cs[2 * (i0 + e) + 1];
-        x[e] = lo ? x[e] * c - other * s : other * s + x[e] * c;
+        x[e] = lo ? x[e] * cv[e] - other * sv[e] : other * sv[e] + x[e] * cv[e];
     }
 }
 
@@ -193,7 +193,6 @@ __global__ __launch_bounds__((AttnShape<HD, GRP>::W * 64)) void attention_kernel
     constexpr int LPH = S::LPH, DPL = S::DPL, C = S::C, W = S::W;
     __shared__ __align__(16) float smem[W * 2 * S::SLOT > W * GRP * HD ? W * 2 * S::SLOT : W * GRP * HD];
     __shared__ float wm[W][GRP], wl[W][GRP];
-    __shared__ float fm[kMaxSplit][GRP];
     __shared__ unsigned last;
     const int n_kv = a.n_kv, KD = n_kv * HD, QD = a.n_head * HD;
     const int t = blockIdx.x / n_kv, kvh = blockIdx.x % n_kv, s = blockIdx.y;
@@ -263,7 +262,7 @@ __global__ __launch_bounds__((AttnShape<HD, GRP>::W * 64)) void attention_kernel
             float p = 0.f;
 #pragma unroll
             for (int e = 0; e < DPL; e++) p = __builtin_fmaf(q[e], kr[e], p);
-            p = group_sum<LPH>(p) * a.scale;
+            p = group_sum_all<LPH>(p) * a.scale;
             sc[j] = j < nc ? p : -INFINITY;
             mc = fmaxf(mc, sc[j]);
         }
@@ -292,20 +291,31 @@ __global__ __launch_bounds__((AttnShape<HD, GRP>::W * 64)) void attention_kernel
         wl[w][h] = l;
     }
     __syncthreads();
+    // per (wave, head): the wave's factor expf(m - M) (kept in wm) and the
+    // head's M and L (kept in wl[0] / wl[1])
+    if (tid < GRP) {
+        float M = -INFINITY;
+#pragma unroll
+        for (int u = 0; u < W; u++) M = fmaxf(M, wm[u][tid]);
+        float L = 0.f;
+#pragma unroll
+        for (int u = 0; u < W; u++) {
+            const float f = wm[u][tid] == -INFINITY ? 0.f : expf(wm[u][tid] - M);
+            L = __builtin_fmaf(wl[u][tid], f, L);
+            wm[u][tid] = f;
+        }
+        wl[0][tid] = M;
+        wl[1][tid] = L;
+    }
+    __syncthreads();
     const size_t rec = HD + 4;  // split record per (t, head, split): o, m, l (16-byte records)
     float* base = a.part + ((size_t)t * a.n_head + kvh * GRP) * a.n_split * rec;
     for (int i = tid; i < GRP * HD; i += W * 64) {
         const int hh = i / HD, d = i % HD;
-        float M = -INFINITY;
+        const float M = wl[0][hh], L = wl[1][hh];
+        float acc = 0.f;
 #pragma unroll
-        for (int u = 0; u < W; u++) M = fmaxf(M, wm[u][hh]);
-        float L = 0.f, acc = 0.f;
-#pragma unroll
-        for (int u = 0; u < W; u++) {
-            const float f = wm[u][hh] == -INFINITY ? 0.f : expf(wm[u][hh] - M);
-            L = __builtin_fmaf(wl[u][hh], f, L);
-            acc = __builtin_fmaf(wo[u * GRP * HD + i], f, acc);
-        }
+        for (int u = 0; u < W; u++) acc = __builtin_fmaf(wo[u * GRP * HD + i], wm[u][hh], acc);
         if (a.n_split == 1) {
             a.out[(size_t)t * QD + (size_t)(kvh * GRP + hh) * HD + d] = acc / L;
         } else {
@@ -326,38 +336,44 @@ __global__ __launch_bounds__((AttnShape<HD, GRP>::W * 64)) void attention_kernel
     __syncthreads();
     if (!last) return;
     // the other blocks' records: drop this XCD's cached copies of older
-    // contents (the records of earlier launches), then ordinary loads, all in
-    // flight together
+    // contents (the records of earlier launches), then ordinary loads.  A
+    // thread takes four dimensions of one head and loads, in one round, the
+    // head's m and l and its four o values of every split.
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-    // merge the splits: weights per (split, head) first, then the outputs
-    for (int i = tid; i < GRP * kMaxSplit; i += W * 64) {
-        const int hh = i / kMaxSplit, u = i % kMaxSplit;  // one lane per (head, split)
-        const float* r = base + ((size_t)hh * a.n_split + u) * rec + HD;
-        const float mu = u < a.n_split ? r[0] : -INFINITY;
-        const float lu = u < a.n_split ? r[1] : 0.f;
-        // max and sum over the head's kMaxSplit lanes (a power-of-two group)
-        float M = mu;
+    for (int i = tid; i < GRP * HD / 4; i += W * 64) {
+        const int hh = i / (HD / 4), d = (i % (HD / 4)) * 4;
+        const float* r = base + (size_t)hh * a.n_split * rec;
+        float4 ov[kMaxSplit];
+        float2 ml[kMaxSplit];
 #pragma unroll
-        for (int off = kMaxSplit / 2; off > 0; off >>= 1) M = fmaxf(M, __shfl_xor(M, off, 64));
-        const float f = mu == -INFINITY ? 0.f : expf(mu - M);
-        fm[u][hh] = f;
-        float L = lu * f;
+        for (int u = 0; u < kMaxSplit; u++) {
+            if (u < a.n_split) {
+                ov[u] = *reinterpret_cast<const float4*>(r + (size_t)u * rec + d);
+                ml[u] = *reinterpret_cast<const float2*>(r + (size_t)u * rec + HD);
+            } else {
+                ov[u] = make_float4(0.f, 0.f, 0.f, 0.f);
+                ml[u] = make_float2(-INFINITY, 0.f);
+            }
+        }
+        float M = -INFINITY;
 #pragma unroll
-        for (int off = kMaxSplit / 2; off > 0; off >>= 1) L += __shfl_xor(L, off, 64);
-        if (u == 0) wl[0][hh] = L;
-    }
-    __syncthreads();
-    for (int i = tid; i < GRP * HD; i += W * 64) {
-        const int hh = i / HD, d = i % HD;
-        const float* r = base + (size_t)hh * a.n_split * rec + d;
-        float vals[kMaxSplit];
+        for (int u = 0; u < kMaxSplit; u++) M = fmaxf(M, ml[u].x);
+        float L = 0.f;
+        float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
-        for (int u = 0; u < kMaxSplit; u++) vals[u] = u < a.n_split ? r[(size_t)u * rec] : 0.f;
-        float acc = 0.f;
-#pragma unroll
-        for (int u = 0; u < kMaxSplit; u++)
-            if (u < a.n_split) acc = __builtin_fmaf(vals[u], fm[u][hh], acc);
-        a.out[(size_t)t * QD + (size_t)(kvh * GRP + hh) * HD + d] = acc / wl[0][hh];
+        for (int u = 0; u < kMaxSplit; u++) {
+            const float f = ml[u].x == -INFINITY ? 0.f : expf(ml[u].x - M);
+            L = __builtin_fmaf(ml[u].y, f, L);
+            acc.x = __builtin_fmaf(ov[u].x, f, acc.x);
+            acc.y = __builtin_fmaf(ov[u].y, f, acc.y);
+            acc.z = __builtin_fmaf(ov[u].z, f, acc.z);
+            acc.w = __builtin_fmaf(ov[u].w, f, acc.w);
+        }
+        float* o = a.out + (size_t)t * QD + (size_t)(kvh * GRP + hh) * HD + d;
+        o[0] = acc.x / L;
+        o[1] = acc.y / L;
+        o[2] = acc.z / L;
+        o[3] = acc.w / L;
     }
     if (tid == 0) __hip_atomic_store(&a.cnt[t * n_kv + kvh], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }

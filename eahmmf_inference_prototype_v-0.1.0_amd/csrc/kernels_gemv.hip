@@ -20,13 +20,15 @@
 // (bit-identical dequantization, kquant.h) against the input held in LDS in a
 // segment-transposed layout (lane s reads segment s's values without bank
 // conflicts).
+#include "dpp.h"
 #include "internal.h"
 #include "kquant.h"
 
 namespace eahmmf {
 
-constexpr int kGemvThreads = 256;
-constexpr int kGemvWaves = kGemvThreads / 64;
+constexpr int kGemvWaves = 4;      // waves per block when streaming
+constexpr int kGemvMaxWaves = 4;   // at most, in a single-shot launch (measured: 8 and 16 start later)
+constexpr int kCUs = 256;  // MI355X compute units
 
 // Orderable key of (value, index): larger value wins, then smaller index.
 __device__ __forceinline__ unsigned long long argmax_key(float v, unsigned idx) {
@@ -105,12 +107,14 @@ __device__ __forceinline__ void issue_unit(const Segs& g, int u, uint8_t* buf, i
     }
 }
 
-template <int T>
-__global__ __launch_bounds__(kGemvThreads) void gemv_kernel(GemvArgs a) {
+// IN: four-value input groups per thread (ne0 <= IN * 4 * 256)
+template <int T, int IN>
+__global__ __launch_bounds__(kGemvMaxWaves * 64) void gemv_kernel(GemvArgs a) {
     extern __shared__ __align__(16) uint8_t smem[];
-    __shared__ float red[kGemvWaves];
-    __shared__ unsigned long long bkey[kGemvWaves];
+    __shared__ float red[kGemvMaxWaves];
+    __shared__ unsigned long long bkey[kGemvMaxWaves];
     const int tid = threadIdx.x, w = __builtin_amdgcn_readfirstlane(tid / 64), lane = tid % 64;
+    const int waves = blockDim.x / 64;
     const int nseg = a.ne0 / 32;
     const Segs g{a.seg[0].w, a.seg[1].w, a.seg[2].w, a.seg[0].out, a.seg[1].out, a.seg[2].out,
                  a.seg[0].resid, a.seg[1].resid, a.seg[2].resid, a.seg[0].rows, a.seg[1].rows,
@@ -119,35 +123,48 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_kernel(GemvArgs a) {
     const size_t unit_bytes = (size_t)a.rpw * a.ni * 1024;
     uint8_t* bufs = smem + (size_t)a.ne0 * 4 + (size_t)w * a.nbuf * unit_bytes;  // nbuf units per wave
     const int n_units = (a.total_rows + a.rpw - 1) / a.rpw;
-    const int stride = gridDim.x * kGemvWaves;
-    int u = blockIdx.x * kGemvWaves + w;
+    const int stride = gridDim.x * waves;
+    int u = blockIdx.x * waves + w;
     // the first unit's rows are on their way while the input is formed
     if (u < n_units) issue_unit(g, u, bufs, lane);
-    // ---- input: x (+ x_add), optionally RMS-normalized
+    // ---- input: x (+ x_add), optionally RMS-normalized; each thread keeps
+    // its IN four-value groups in registers, and every load (x, x_add, the
+    // norm weights) is issued in one round
+    float4 xv[IN], nv[IN];
     float ss = 0.f;
-    for (int i = tid * 4; i < a.ne0; i += kGemvThreads * 4) {
-        float4 v = *reinterpret_cast<const float4*>(a.x + i);
-        if (a.x_add) {
-            const float4 q = *reinterpret_cast<const float4*>(a.x_add + i);
-            v.x += q.x; v.y += q.y; v.z += q.z; v.w += q.w;
-            if (a.x_sum_out && blockIdx.x == 0) *reinterpret_cast<float4*>(a.x_sum_out + i) = v;
+#pragma unroll
+    for (int k = 0; k < IN; k++) {
+        const int i = (tid + k * waves * 64) * 4;
+        if (i < a.ne0) {
+            xv[k] = *reinterpret_cast<const float4*>(a.x + i);
+            if (a.norm_w) nv[k] = *reinterpret_cast<const float4*>(a.norm_w + i);
+            if (a.x_add) {
+                const float4 q = *reinterpret_cast<const float4*>(a.x_add + i);
+                xv[k].x += q.x; xv[k].y += q.y; xv[k].z += q.z; xv[k].w += q.w;
+                if (a.x_sum_out && blockIdx.x == 0) *reinterpret_cast<float4*>(a.x_sum_out + i) = xv[k];
+            }
+            ss += xv[k].x * xv[k].x + xv[k].y * xv[k].y + xv[k].z * xv[k].z + xv[k].w * xv[k].w;
         }
-        ss += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
-        xt[((i % 32) / 4) * nseg + i / 32] = v;
     }
+    float sc = 1.f;
     if (a.norm_w) {
-        ss = wave_sum(ss);
+        ss = group_sum_all<64>(ss);
         if (lane == 0) red[w] = ss;
         __syncthreads();
         float tot = 0.f;
+        for (int i = 0; i < waves; i++) tot += red[i];
+        sc = 1.0f / sqrtf(tot / (float)a.ne0 + a.eps);
+    }
 #pragma unroll
-        for (int i = 0; i < kGemvWaves; i++) tot += red[i];
-        const float sc = 1.0f / sqrtf(tot / (float)a.ne0 + a.eps);
-        for (int i = tid * 4; i < a.ne0; i += kGemvThreads * 4) {
-            float4& v = xt[((i % 32) / 4) * nseg + i / 32];
-            const float4 nw = *reinterpret_cast<const float4*>(a.norm_w + i);
-            v.x = v.x * sc * nw.x; v.y = v.y * sc * nw.y; v.z = v.z * sc * nw.z; v.w = v.w * sc * nw.w;
-            if (a.xn_out && blockIdx.x == 0) *reinterpret_cast<float4*>(a.xn_out + i) = v;
+    for (int k = 0; k < IN; k++) {
+        const int i = (tid + k * waves * 64) * 4;
+        if (i < a.ne0) {
+            float4 v = xv[k];
+            if (a.norm_w) {
+                v.x = v.x * sc * nv[k].x; v.y = v.y * sc * nv[k].y; v.z = v.z * sc * nv[k].z; v.w = v.w * sc * nv[k].w;
+                if (a.xn_out && blockIdx.x == 0) *reinterpret_cast<float4*>(a.xn_out + i) = v;
+            }
+            xt[((i % 32) / 4) * nseg + i / 32] = v;
         }
     }
     __syncthreads();
@@ -186,8 +203,8 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_kernel(GemvArgs a) {
                 }
                 acc += p;
             }
-            acc = wave_sum(acc);
-            if (lane == 0) {
+            acc = group_sum<64>(acc);  // the total is in lane 63
+            if (lane == 63) {
                 const float v = resid ? rv + acc : acc;
                 g.out(sg)[row] = v;
                 if (v > best || best_i == 0xFFFFFFFFu) {
@@ -200,23 +217,40 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_kernel(GemvArgs a) {
         if (a.nbuf == 1 && u + stride < n_units) issue_unit(g, u + stride, bufs, lane);
     }
     if (a.amax) {  // one atomic per block, and only when it can raise the key
-        if (lane == 0) bkey[w] = best_i == 0xFFFFFFFFu ? 0ull : argmax_key(best, best_i);
+        if (lane == 63) bkey[w] = best_i == 0xFFFFFFFFu ? 0ull : argmax_key(best, best_i);
         __syncthreads();
         if (tid == 0) {
             unsigned long long kmax = bkey[0];
-            for (int i = 1; i < kGemvWaves; i++) kmax = bkey[i] > kmax ? bkey[i] : kmax;
+            for (int i = 1; i < waves; i++) kmax = bkey[i] > kmax ? bkey[i] : kmax;
             if (kmax > __hip_atomic_load(a.amax, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) atomicMax(a.amax, kmax);
         }
     }
 }
 
-size_t gemv_lds_bytes(const GemvArgs& a) {
-    return (size_t)a.ne0 * 4 + (size_t)kGemvWaves * a.nbuf * a.rpw * a.ni * 1024;
+template <int IN>
+static bool launch_in(int type, int blocks, int th, size_t lds, const GemvArgs& a, hipStream_t st) {
+    switch (type) {
+        case kF32: gemv_kernel<kF32, IN><<<blocks, th, lds, st>>>(a); return true;
+        case kQ8_0: gemv_kernel<kQ8_0, IN><<<blocks, th, lds, st>>>(a); return true;
+        case kQ4_K: gemv_kernel<kQ4_K, IN><<<blocks, th, lds, st>>>(a); return true;
+        case kQ5_K: gemv_kernel<kQ5_K, IN><<<blocks, th, lds, st>>>(a); return true;
+        case kQ6_K: gemv_kernel<kQ6_K, IN><<<blocks, th, lds, st>>>(a); return true;
+        default: return false;
+    }
+}
+
+static bool launch_typed(int type, int in, int blocks, int th, size_t lds, const GemvArgs& a, hipStream_t st) {
+    return in == 2 ? launch_in<2>(type, blocks, th, lds, a, st)
+                   : (in == 4 ? launch_in<4>(type, blocks, th, lds, a, st) : launch_in<8>(type, blocks, th, lds, a, st));
+}
+
+size_t gemv_lds_bytes(const GemvArgs& a, int waves) {
+    return (size_t)a.ne0 * 4 + (size_t)waves * a.nbuf * a.rpw * a.ni * 1024;
 }
 
 bool gemv_supported(int type, int ne0, size_t rb) {
     if (type != kF32 && !type_supported(type)) return false;
-    if (ne0 <= 0 || ne0 % 32 || ne0 % type_blck(type) || ne0 > 8192) return false;
+    if (ne0 <= 0 || ne0 % 32 || ne0 % type_blck(type) || ne0 > 8192) return false;  // 8192 = 8 x 4 x 256
     // one slot of one row per wave must fit next to the input in 64 KiB
     const size_t ni = (rb + 19 + 1023) / 1024;
     return rb >= (size_t)(ne0 / type_blck(type)) * type_bytes(type) && ni <= 15 &&
@@ -233,28 +267,45 @@ hipError_t launch_gemv(int type, GemvArgs a, hipStream_t st) {
     // a row's LDS slot: 1 KiB DMA groups holding its bytes at any 16-byte phase
     // (up to 15 bytes of lead) plus the 4 bytes the realigning reads may touch
     a.ni = (a.rb + 19 + 1023) / 1024;
-    // two units of rpw rows per wave in LDS (one if two do not fit), at most
-    // 15 DMA instructions a unit
-    const int avail_kb = (64 * 1024 - a.ne0 * 4) / 1024;
-    a.nbuf = avail_kb >= kGemvWaves * 2 * a.ni ? 2 : 1;
-    a.rpw = avail_kb / (kGemvWaves * a.nbuf * a.ni);
-    if (a.rpw > 2) a.rpw = 2;
-    if (a.rpw * a.ni > 15) a.rpw = 15 / a.ni;
-    if (a.rpw < 1) return hipErrorInvalidValue;
-    const int n_units = (a.total_rows + a.rpw - 1) / a.rpw;
-    const int want = (n_units + kGemvWaves - 1) / kGemvWaves;
-    const int blocks = want < 2048 ? want : 2048;
-    const size_t lds = gemv_lds_bytes(a);
+    // Single shot when one row per wave for every row fits on the chip at
+    // once (blocks resident together, by LDS and by waves per CU): every
+    // row's DMA is in flight from the start.  Otherwise stream: two units of
+    // rpw rows per wave in LDS (one if two do not fit), at most 15 DMA
+    // instructions a unit, the next unit in flight while one is decoded.
+    // (single shot: the most waves per block whose LDS stays within 64 KiB,
+    // so that fewer, larger blocks form the input fewer times)
+    int waves = kGemvWaves, blocks = 0;
+    for (int wv = kGemvMaxWaves; wv >= kGemvWaves; wv /= 2) {
+        const int lds1 = a.ne0 * 4 + wv * a.ni * 1024;
+        if (lds1 > 64 * 1024) continue;
+        const int per_cu = min(32 / wv, (160 * 1024) / lds1);
+        const int blocks1 = (a.total_rows + wv - 1) / wv;
+        if (blocks1 <= kCUs * per_cu) {
+            waves = wv;
+            blocks = blocks1;
+            break;
+        }
+    }
+    if (blocks) {
+        a.nbuf = 1;
+        a.rpw = 1;
+    } else {
+        const int avail_kb = (64 * 1024 - a.ne0 * 4) / 1024;
+        a.nbuf = avail_kb >= kGemvWaves * 2 * a.ni ? 2 : 1;
+        a.rpw = avail_kb / (kGemvWaves * a.nbuf * a.ni);
+        if (a.rpw > 2) a.rpw = 2;
+        if (a.rpw * a.ni > 15) a.rpw = 15 / a.ni;
+        if (a.rpw < 1) return hipErrorInvalidValue;
+        const int n_units = (a.total_rows + a.rpw - 1) / a.rpw;
+        const int want = (n_units + kGemvWaves - 1) / kGemvWaves;
+        blocks = want < 2048 ? want : 2048;
+    }
+    const size_t lds = gemv_lds_bytes(a, waves);
     if (lds > 64 * 1024) return hipErrorInvalidValue;
     clear_stale_error();
-    switch (type) {
-        case kF32: gemv_kernel<kF32><<<blocks, kGemvThreads, lds, st>>>(a); break;
-        case kQ8_0: gemv_kernel<kQ8_0><<<blocks, kGemvThreads, lds, st>>>(a); break;
-        case kQ4_K: gemv_kernel<kQ4_K><<<blocks, kGemvThreads, lds, st>>>(a); break;
-        case kQ5_K: gemv_kernel<kQ5_K><<<blocks, kGemvThreads, lds, st>>>(a); break;
-        case kQ6_K: gemv_kernel<kQ6_K><<<blocks, kGemvThreads, lds, st>>>(a); break;
-        default: return hipErrorInvalidValue;
-    }
+    const int th = waves * 64;
+    const int in = a.ne0 <= 2048 ? 2 : (a.ne0 <= 4096 ? 4 : 8);
+    if (!launch_typed(type, in, blocks, th, lds, a, st)) return hipErrorInvalidValue;
     return hipGetLastError();
 }
 
