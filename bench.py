@@ -557,6 +557,8 @@ def bench_c3(args, torch, b, hip):
                          "pct_of_hbm_peak": round(100 * bt * steps / el / 1e9 / HBM_PEAK_GBS, 2),
                          "prefill_tokens_per_s": round(len(prompt) / t_prefill, 1),
                          "build_s": round(t_build, 1)}
+        if not args.no_cpu_baseline and name == "q5_k":  # the headline variant only (about 2 minutes)
+            results[name]["cpu_baseline"] = c3_cpu_baseline(et)
         print(f"# c3 {name}: {results[name]}", file=sys.stderr, flush=True)
         m.close()
         del keep
@@ -572,6 +574,7 @@ def bench_c3(args, torch, b, hip):
         "roofline": {"bound": "hbm", "kernel": "whole decode token (all launches)",
                      "achieved": r["GB_s"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(r["GB_s"] / HBM_PEAK_GBS, 4), "traffic": None},
+        "cpu_baseline": r.get("cpu_baseline"),
         "variants": results}), flush=True)
 
 
@@ -632,6 +635,40 @@ def bench_c3_experts(args, torch, b, hip):
         "variants": results}), flush=True)
 
 
+def router_variant(b, hip, torch, tables, dx, dy, dids, dw, shape, stream, R, NS, steps=400):
+    """The same layer-token from the residual stream: RMSNorm + the F32
+    router matmul (128 x 2048, 1 MiB) + routing + experts
+    (eahmmf_hip_moe_layer_decode_xn_async, two launches); HIP events on the
+    launch stream over `steps` back-to-back layer-tokens."""
+    rng = np.random.default_rng(9)
+    router = torch.from_numpy(rng.normal(0, 0.02, (E, D)).astype(np.float32)).cuda()
+    norm_w = torch.from_numpy((1 + rng.normal(0, 0.05, D)).astype(np.float32)).cuda()
+    sp, vp = ctypes.c_void_p(stream.cuda_stream), ctypes.c_void_p
+
+    def step(i):
+        s = i % NS
+        rc = hip.eahmmf_hip_moe_layer_decode_xn_async(ctypes.byref(shape), vp(tables[i % R].data_ptr()), E,
+                                                      vp(router.data_ptr()), vp(norm_w.data_ptr()),
+                                                      ctypes.c_float(1e-6), vp(dx[s].data_ptr()), K,
+                                                      vp(dy[s].data_ptr()), vp(dids[s].data_ptr()),
+                                                      vp(dw[s].data_ptr()), None, None, sp)
+        assert rc == 0, b.last_error()
+
+    for i in range(50):
+        step(i)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for i in range(steps):
+        step(i)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    assert hip.eahmmf_hip_device_flags() == 0
+    us = e0.elapsed_time(e1) * 1e3 / steps
+    return {"us_per_layer_token": round(us, 3), "launches": 2,
+            "what": "RMSNorm + F32 router matmul + routing + expert block from the residual stream "
+                    "(eahmmf_hip_moe_layer_decode_xn_async), HIP events over back-to-back layer-tokens"}
+
+
 def host_io_rate(b, hip, torch, dgate, dup, ddown, steps=2000):
     """The reference's calling convention at C2: routing on the host, then the
     synchronous eahmmf_hip_moe_decode with pageable host x / y (two 8 KB copies
@@ -673,15 +710,112 @@ def host_io_rate(b, hip, torch, dgate, dup, ddown, steps=2000):
 def random_blocks(rng, t, nrows, ne0):
     """Rows of valid blocks (random codes, small fp16 scales): the CPU kernel's
     time does not depend on the values."""
-    blck, nbytes = {Q4_K: (256, 144), Q6_K: (256, 210)}[t]
+    blck, nbytes = {Q8_0: (32, 34), Q4_K: (256, 144), Q5_K: (256, 176), Q6_K: (256, 210)}[t]
     raw = rng.integers(0, 256, (nrows, ne0 // blck, nbytes), dtype=np.uint8)
-    d = (rng.uniform(.5, 1.5, (nrows, ne0 // blck, 1)) * 3e-5).astype(np.float16).view(np.uint8)
+    d = (rng.uniform(.5, 1.5, (nrows, ne0 // blck, 1)) * (3e-4 if t == Q8_0 else 3e-5)).astype(np.float16)
+    d = d.view(np.uint8)
     if t == Q6_K:
         raw[:, :, 208:210] = d
     else:
         raw[:, :, 0:2] = d
-        raw[:, :, 2:4] = d
+        if t in (Q4_K, Q5_K):
+            raw[:, :, 2:4] = d
     return raw.reshape(nrows, -1)
+
+
+def c3_cpu_child(layers, etype, threads, steps, warmup=2):
+    """The reference engine (oracle/_ref, compiled from the reference's
+    qwen3moe.cpp) on a GGUF file of `layers` layers at the 48-layer model's
+    shape (D=2048, 32/4 heads of 128, 128 experts of `etype` top-8, FF 768,
+    Q8_0 attention, embedding and output head, vocab 151936): single-token
+    forwards at position 2047 (a 2048-row KV cache; its contents do not change
+    the work), each timed on the host clock.  In a process of its own, with
+    OpenMP placement from its environment and no GPU runtime loaded."""
+    import tempfile
+    sys.path.insert(0, ROOT)
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    import oracle
+    import gguf_tools as gt
+    flags = open("/proc/cpuinfo").read() if os.path.exists("/proc/cpuinfo") else ""
+    avx512 = os.path.join(ROOT, "oracle", "_ref", "libref_avx512.so")
+    path = avx512 if (" avx512f " in flags and os.path.exists(avx512)) else oracle.REF_PORTABLE_SO
+    if not os.path.exists(path):
+        print(json.dumps({"error": "the compiled reference is not built"}), flush=True)
+        return
+    lib = oracle.ref(path)
+    D_, NH, NKV, HD, E_, K_, FF_, V = 2048, 32, 4, 128, 128, 8, 768, 151936
+    rng = np.random.default_rng(21)
+    spec = gt.ModelSpec(n_layer=layers, D=D_, n_head=NH, n_kv=NKV, hd=HD, n_expert=E_, n_used=K_, FF=FF_, n_vocab=V,
+                        n_ctx=4096, ctx_train=4096, eps=1e-6, rope_base=1e6)
+
+    def f32(*shape, base=0.0):
+        return (base + rng.normal(0, 0.02, shape)).astype(np.float32)
+
+    spec.add("token_embd.weight", Q8_0, [D_, V], random_blocks(rng, Q8_0, V, D_))
+    spec.add("output.weight", Q8_0, [D_, V], random_blocks(rng, Q8_0, V, D_))
+    spec.add("output_norm.weight", 0, [D_], f32(D_, base=1.0))
+    for l in range(layers):
+        p = f"blk.{l}."
+        for nm, n in (("attn_norm", D_), ("ffn_norm", D_), ("attn_q_norm", HD), ("attn_k_norm", HD)):
+            spec.add(p + nm + ".weight", 0, [n], f32(n, base=1.0))
+        spec.add(p + "attn_q.weight", Q8_0, [D_, NH * HD], random_blocks(rng, Q8_0, NH * HD, D_))
+        spec.add(p + "attn_k.weight", Q8_0, [D_, NKV * HD], random_blocks(rng, Q8_0, NKV * HD, D_))
+        spec.add(p + "attn_v.weight", Q8_0, [D_, NKV * HD], random_blocks(rng, Q8_0, NKV * HD, D_))
+        spec.add(p + "attn_output.weight", Q8_0, [NH * HD, D_], random_blocks(rng, Q8_0, D_, NH * HD))
+        spec.add(p + "ffn_gate_inp.weight", 0, [D_, E_], f32(E_, D_))
+        spec.add(p + "ffn_gate_exps.weight", etype, [D_, FF_, E_], random_blocks(rng, etype, E_ * FF_, D_))
+        spec.add(p + "ffn_up_exps.weight", etype, [D_, FF_, E_], random_blocks(rng, etype, E_ * FF_, D_))
+        spec.add(p + "ffn_down_exps.weight", etype, [FF_, D_, E_], random_blocks(rng, etype, E_ * D_, FF_))
+    fd, gguf = tempfile.mkstemp(suffix=".gguf", dir=os.environ.get("TMPDIR", "/tmp"))
+    os.close(fd)
+    try:
+        gt.write_gguf(spec, gguf)
+        del spec
+        eng = lib.ref_engine_new(gguf.encode(), 2100)
+        logits = np.empty(V, np.float32)
+        tok = np.array([1], np.int32)
+        secs = []
+        for i in range(warmup + steps):
+            tok[0] = 1 + i
+            t0 = time.perf_counter()
+            lib.ref_engine_forward(eng, tok.ctypes.data, 1, 2047, logits.ctypes.data)
+            if i >= warmup:
+                secs.append(time.perf_counter() - t0)
+        lib.ref_engine_free(eng)
+    finally:
+        os.unlink(gguf)
+    print(json.dumps({"layers": layers, "threads": threads, "secs": secs, "lib": os.path.relpath(path, ROOT)}),
+          flush=True)
+
+
+def c3_cpu_baseline(etype, steps=8):
+    """Decode tokens/s of the reference engine for the 48-layer model, from a
+    bounded sample: 1- and 3-layer models of the same shape (full vocabulary
+    head), median forward time each; per-layer time = (T3 - T1) / 2, the
+    48-layer token = T1 + 47 x per-layer.  Every core of the host
+    (OMP_PLACES=cores, OMP_PROC_BIND=close)."""
+    import subprocess
+    ncores = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
+    env = dict(os.environ, OMP_NUM_THREADS=str(ncores), OMP_PLACES="cores", OMP_PROC_BIND="close")
+    med = {}
+    for layers in (1, 3):
+        r = subprocess.run([sys.executable, os.path.abspath(__file__), "--c3-cpu-child", str(layers),
+                            "--c3-cpu-etype", str(etype), "--steps", str(steps)], env=env, capture_output=True,
+                           text=True, timeout=900)
+        if r.returncode != 0:
+            return {"value": None, "error": r.stderr[-500:]}
+        d = json.loads(r.stdout.strip().splitlines()[-1])
+        if "error" in d:
+            return {"value": None, "error": d["error"]}
+        med[layers] = float(np.median(d["secs"]))
+    per_layer = (med[3] - med[1]) / 2
+    t48 = med[1] + 47 * per_layer
+    return {"value": round(1.0 / t48, 3), "unit": "tokens/s", "cores": ncores, "kind": "reference",
+            "sample": f"the compiled reference engine on 1- and 3-layer GGUF models of this shape (full 151936-row "
+                      f"Q8_0 head), {steps} single-token forwards each at position 2047 after 2 warm-up forwards; "
+                      f"median T1 {med[1] * 1e3:.2f} ms, T3 {med[3] * 1e3:.2f} ms; 48-layer token = T1 + 47 x "
+                      f"(T3 - T1) / 2 = {t48 * 1e3:.1f} ms",
+            "ms_per_token_48_layers": round(t48 * 1e3, 2), "ms_per_layer": round(per_layer * 1e3, 3)}
 
 
 def cpu_child(threads, n_tok, reps, warmup):
@@ -804,6 +938,8 @@ def main():
     ap.add_argument("--replicas", type=int, default=None, help="layer copies in HBM (c2 16, c4 4, c5 4)")
     ap.add_argument("--cpu-tokens", type=int, default=64, help="C2 layer-tokens per CPU-baseline repetition")
     ap.add_argument("--cpu-child", type=int, default=0, help=argparse.SUPPRESS)
+    ap.add_argument("--c3-cpu-child", type=int, default=0, help=argparse.SUPPRESS)
+    ap.add_argument("--c3-cpu-etype", type=int, default=Q5_K, help=argparse.SUPPRESS)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--workload", choices=("c2", "c3", "c3x", "c4", "c5", "c5b16", "stream", "staging", "dropin"), default="c2",
                     help="c2 (default): the headline single-token layer; c3: one decode token through the whole "
@@ -818,6 +954,10 @@ def main():
     args = ap.parse_args()
     if args.cpu_child:
         cpu_child(args.cpu_child, args.cpu_tokens, 21, 3)
+        return
+    if args.c3_cpu_child:
+        c3_cpu_child(args.c3_cpu_child, args.c3_cpu_etype, int(os.environ.get("OMP_NUM_THREADS", "1")),
+                     args.steps or 8)
         return
     if args.workload == "c2":
         args.steps = 2000 if args.steps is None else args.steps
@@ -938,6 +1078,7 @@ def main():
                      "p90_us_with_event_overhead": round(float(np.percentile(durs, 90)), 3),
                      "xcd_local_exchange": int(hip.eahmmf_hip_fused_exchange())},
     }
+    out["router_from_activations"] = router_variant(b, hip, torch, tables, dx, dy, dids, dw, shape, stream, R, NS)
     out["host_io"] = host_io_rate(b, hip, torch, dgate, dup, ddown)
     # the measured read ceiling at the same launch size, timed the same way
     sr = stream_rates(torch, hip)

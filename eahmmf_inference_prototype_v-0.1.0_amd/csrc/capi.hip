@@ -58,7 +58,7 @@ constexpr size_t kRingChunk = (size_t)32 << 20;
 
 struct DevCtx {
     hipStream_t stream = nullptr;
-    DeviceBuf dx, dy, dy2, dh, dids, dw, dyp, dhx, dgs, dtab;  // device scratch
+    DeviceBuf dx, dy, dy2, dh, dids, dw, dyp, dhx, dgs, dtab, drt;  // device scratch
     DeviceBuf px, py, py2;                // pinned host staging
     unsigned* dsync = nullptr;            // fused-launch error word and ticket counters (zeroed once)
     FusedState fused;                     // the fused kernel's scratch set (dhx, dyp, dsync) and epochs
@@ -559,6 +559,42 @@ int eahmmf_hip_moe_layer_decode_async(const eahmmf_hip_moe_shape* shape, const e
                 "routed moe decode launch"))
         return -3;
     return 0;
+}
+
+int eahmmf_hip_moe_layer_decode_xn_async(const eahmmf_hip_moe_shape* shape, const eahmmf_hip_expert_ptrs* dev_table,
+                                         int n_expert, const float* dev_router, const float* dev_norm_w, float eps,
+                                         const float* dev_x, int k, float* dev_y, int* dev_ids_out, float* dev_w_out,
+                                         float* dev_xn_out, float* dev_logits_out, void* stream) {
+    MoeShape s{};
+    if (!shape_from_abi(shape, s)) return -1;
+    if (!dev_table || !dev_router || !dev_x || !dev_y) return set_error("null argument"), -1;
+    if (n_expert <= 0 || n_expert > 512 || k <= 0 || k > kMaxSlots || k > n_expert)
+        return set_error("bad routing shape n_expert=%d k=%d", n_expert, k), -1;
+    if (!gemv_supported(kF32, s.D, (size_t)s.D * 4)) return set_error("router: D=%d not supported", s.D), -1;
+    DevCtx* c = ctx_for_current_device();
+    if (!c) return -2;
+    float* xn = dev_xn_out;
+    float* logits = dev_logits_out;
+    if ((dev_norm_w && !xn) || !logits) {
+        const size_t xn_floats = ((size_t)s.D + 63) & ~(size_t)63;
+        if (!grow_device(c->drt, (xn_floats + (size_t)n_expert) * sizeof(float))) return -2;
+        if (dev_norm_w && !xn) xn = (float*)c->drt.p;
+        if (!logits) logits = (float*)c->drt.p + xn_floats;
+    }
+    // the router matmul over the (normalized) input; the kernel's block 0
+    // also stores the normalized input the expert block reads
+    GemvArgs g{};
+    g.x = dev_x;
+    g.norm_w = dev_norm_w;
+    g.eps = eps;
+    g.xn_out = dev_norm_w ? xn : nullptr;
+    g.seg[0] = GemvSeg{reinterpret_cast<const uint8_t*>(dev_router), logits, nullptr, n_expert};
+    g.nseg = 1;
+    g.ne0 = s.D;
+    g.rb = s.D * 4;
+    if (!hip_ok(launch_gemv(kF32, g, (hipStream_t)stream), "router launch")) return -3;
+    return eahmmf_hip_moe_layer_decode_async(shape, dev_table, n_expert, logits, k, dev_norm_w ? xn : dev_x, dev_y,
+                                             dev_ids_out, dev_w_out, stream);
 }
 
 int eahmmf_hip_moe_grouped_async(const eahmmf_hip_moe_shape* shape, const eahmmf_hip_expert_ptrs* dev_table,

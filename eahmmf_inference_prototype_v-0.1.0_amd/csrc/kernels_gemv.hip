@@ -126,7 +126,8 @@ __global__ __launch_bounds__(kGemvMaxWaves * 64) void gemv_kernel(GemvArgs a) {
     const int stride = gridDim.x * waves;
     int u = blockIdx.x * waves + w;
     // the first unit's rows are on their way while the input is formed
-    if (u < n_units) issue_unit(g, u, bufs, lane);
+    // (ni == 0: rows too long to stage, read straight from memory)
+    if (a.ni && u < n_units) issue_unit(g, u, bufs, lane);
     // ---- input: x (+ x_add), optionally RMS-normalized; each thread keeps
     // its IN four-value groups in registers, and every load (x, x_add, the
     // norm weights) is issued in one round
@@ -175,23 +176,27 @@ __global__ __launch_bounds__(kGemvMaxWaves * 64) void gemv_kernel(GemvArgs a) {
     const int per_unit = a.rpw * a.ni;  // DMA instructions per unit
     for (int k = 0; u < n_units; u += stride, k++) {
         uint8_t* cur = bufs + (a.nbuf == 2 ? (k & 1) * unit_bytes : 0);
-        if (a.nbuf == 2 && u + stride < n_units) {
+        if (a.ni && a.nbuf == 2 && u + stride < n_units) {
             issue_unit(g, u + stride, bufs + ((k + 1) & 1) * unit_bytes, lane);
             wait_vm_n(per_unit);
-        } else {
+        } else if (a.ni) {
             wait_vm();
         }
         const int r0 = u * a.rpw, nr = min(a.rpw, a.total_rows - r0);
         for (int r = 0; r < nr; r++) {
             int row = r0 + r;
             const int sg = g.seg_of(row);
-            const uint8_t* rl = cur + (size_t)r * a.ni * 1024 + ((uintptr_t)(g.w(sg) + (size_t)row * a.rb) & 15);
+            const uint8_t* rg = g.w(sg) + (size_t)row * a.rb;
+            const uint8_t* rl = cur + (size_t)r * a.ni * 1024 + ((uintptr_t)rg & 15);
             const float* resid = g.resid(sg);
             const float rv = resid ? scalar_ld(resid + row) : 0.f;
             float acc = 0.f;
             for (int s = lane; s < nseg; s += 64) {
                 float wv[32];
-                decode_row_seg<T, LdsLd>(rl, s, wv);
+                if (a.ni)
+                    decode_row_seg<T, LdsLd>(rl, s, wv);
+                else
+                    decode_row_seg<T, GlobalLd>(rg, s, wv);
                 float p = 0.f;
 #pragma unroll
                 for (int i4 = 0; i4 < 8; i4++) {
@@ -214,7 +219,7 @@ __global__ __launch_bounds__(kGemvMaxWaves * 64) void gemv_kernel(GemvArgs a) {
             }
         }
         // one slot: the next unit's copy starts once this one is decoded
-        if (a.nbuf == 1 && u + stride < n_units) issue_unit(g, u + stride, bufs, lane);
+        if (a.ni && a.nbuf == 1 && u + stride < n_units) issue_unit(g, u + stride, bufs, lane);
     }
     if (a.amax) {  // one atomic per block, and only when it can raise the key
         if (lane == 63) bkey[w] = best_i == 0xFFFFFFFFu ? 0ull : argmax_key(best, best_i);
@@ -251,10 +256,9 @@ size_t gemv_lds_bytes(const GemvArgs& a, int waves) {
 bool gemv_supported(int type, int ne0, size_t rb) {
     if (type != kF32 && !type_supported(type)) return false;
     if (ne0 <= 0 || ne0 % 32 || ne0 % type_blck(type) || ne0 > 8192) return false;  // 8192 = 8 x 4 x 256
-    // one slot of one row per wave must fit next to the input in 64 KiB
-    const size_t ni = (rb + 19 + 1023) / 1024;
-    return rb >= (size_t)(ne0 / type_blck(type)) * type_bytes(type) && ni <= 15 &&
-           (size_t)ne0 * 4 + (size_t)kGemvWaves * ni * 1024 <= 64 * 1024;
+    // rows of 16-byte loads (F32, Q4_K, Q5_K) 16-byte aligned for the direct reads
+    const bool a16 = type == kF32 || type == kQ4_K || type == kQ5_K;
+    return rb >= (size_t)(ne0 / type_blck(type)) * type_bytes(type) && (!a16 || rb % 16 == 0);
 }
 
 hipError_t launch_gemv(int type, GemvArgs a, hipStream_t st) {
@@ -265,8 +269,22 @@ hipError_t launch_gemv(int type, GemvArgs a, hipStream_t st) {
         a.total_rows += a.seg[i].rows;
     }
     // a row's LDS slot: 1 KiB DMA groups holding its bytes at any 16-byte phase
-    // (up to 15 bytes of lead) plus the 4 bytes the realigning reads may touch
+    // (up to 15 bytes of lead) plus the 4 bytes the realigning reads may touch;
+    // rows whose slots do not fit next to the input (at most 15 DMA
+    // instructions a row, 64 KiB of LDS) are read straight from memory
     a.ni = (a.rb + 19 + 1023) / 1024;
+    if (a.ni > 15 || a.ne0 * 4 + kGemvWaves * a.ni * 1024 > 64 * 1024) {
+        a.ni = 0;
+        a.nbuf = 1;
+        a.rpw = 1;
+        const int want = (a.total_rows + kGemvWaves - 1) / kGemvWaves;
+        const int blocks = want < 2048 ? want : 2048;
+        clear_stale_error();
+        if (!launch_typed(type, a.ne0 <= 2048 ? 2 : (a.ne0 <= 4096 ? 4 : 8), blocks, kGemvWaves * 64,
+                          (size_t)a.ne0 * 4, a, st))
+            return hipErrorInvalidValue;
+        return hipGetLastError();
+    }
     // Single shot when one row per wave for every row fits on the chip at
     // once (blocks resident together, by LDS and by waves per CU): every
     // row's DMA is in flight from the start.  Otherwise stream: two units of

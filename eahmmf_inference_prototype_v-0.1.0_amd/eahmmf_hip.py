@@ -28,7 +28,7 @@ EXPORTS = (
     "eahmmf_hip_moe_layer_decode_noalloc", "eahmmf_hip_expf_ref_async", "eahmmf_hip_moe_decode_resident",
     "eahmmf_hip_model_create", "eahmmf_hip_model_forward", "eahmmf_hip_model_eval", "eahmmf_hip_model_generate_greedy",
     "eahmmf_hip_model_set_trace", "eahmmf_hip_model_trace", "eahmmf_hip_model_trace_clear", "eahmmf_hip_model_stream",
-    "eahmmf_hip_model_free",
+    "eahmmf_hip_model_free", "eahmmf_hip_moe_layer_decode_xn_async",
 )
 
 
@@ -110,6 +110,8 @@ def load(path=LIB_PATH):
                                                        vp]),
         "eahmmf_hip_moe_layer_decode_async": (c_int, [ctypes.POINTER(MoeShape), vp, c_int, vp, c_int, vp, vp, vp,
                                                       vp, vp]),
+        "eahmmf_hip_moe_layer_decode_xn_async": (c_int, [ctypes.POINTER(MoeShape), vp, c_int, vp, vp, ctypes.c_float,
+                                                         vp, c_int, vp, vp, vp, vp, vp, vp]),
         "eahmmf_hip_moe_layer_decode_noalloc": (c_int, [ctypes.POINTER(MoeShape), vp, c_int, vp, c_int, vp, vp, vp,
                                                         vp, vp]),
         "eahmmf_hip_set_fused": (c_int, [c_int]),

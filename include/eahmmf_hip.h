@@ -142,6 +142,26 @@ int eahmmf_hip_moe_layer_decode_noalloc(const eahmmf_hip_moe_shape* shape, const
                                         int n_expert, const float* dev_logits, int k, const float* dev_x,
                                         float* dev_y, int* dev_ids_out, float* dev_w_out, void* stream);
 
+/* Single-token MoE block from the layer's residual stream, on the device:
+ * RMSNorm of dev_x [D] with dev_norm_w [D] (eps; dev_norm_w null: dev_x is
+ * already normalized), the router matmul with dev_router (F32, n_expert rows
+ * of D values), softmax/top-k routing and the expert block, as the
+ * reference's nb = 1 step does (qwen3moe.cpp:1020-1067: rmsnorm, matmul
+ * router, partial_sort, experts).  Two launches on `stream` (the router
+ * matmul, then the fused routed layer kernel).  dev_xn_out / dev_logits_out
+ * (optional, device) receive the normalized input and the router logits;
+ * dev_ids_out / dev_w_out as in eahmmf_hip_moe_layer_decode_async.  The
+ * logits sum in a different order than the reference's sequential loop, so
+ * two experts whose logits differ by a few ulps may rank the other way round
+ * (the ids then differ from the reference's; the output stays within
+ * tolerance of the reference's for the ids it reports).  No single
+ * counterpart in the reference (its router runs on the CPU); 0, or -1/-2/-3
+ * as the other async entry points. */
+int eahmmf_hip_moe_layer_decode_xn_async(const eahmmf_hip_moe_shape* shape, const eahmmf_hip_expert_ptrs* dev_table,
+                                         int n_expert, const float* dev_router, const float* dev_norm_w, float eps,
+                                         const float* dev_x, int k, float* dev_y, int* dev_ids_out, float* dev_w_out,
+                                         float* dev_xn_out, float* dev_logits_out, void* stream);
+
 /* Ragged grouped expert block for a batch of nb tokens (prefill, batched
  * decode), in the reference's by_exp form: group g (ascending expert id) is
  * experts[g] applied to tokens[group_offsets[g] .. group_offsets[g+1]) with

@@ -113,6 +113,17 @@ def matmul(t, w, ne0, x):
     return out
 
 
+def rmsnorm(x, w, eps):
+    """x / sqrt(mean(x^2) + eps) * w per row (qwen3moe.cpp:527-532)."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    w = np.ascontiguousarray(w, dtype=np.float32)
+    rows = x.reshape(-1, x.shape[-1])
+    out = np.empty_like(rows)
+    for r in range(rows.shape[0]):
+        lib().orc_rmsnorm(_ptr(rows[r]), _ptr(w), _ptr(out[r]), rows.shape[1], ctypes.c_float(eps))
+    return out.reshape(x.shape)
+
+
 def route_topk(logits, k):
     logits = np.ascontiguousarray(logits, dtype=np.float32)
     nb, E = logits.shape

@@ -390,6 +390,65 @@ def test_moe_layer_decode_vs_oracle(torch_dev, binding, hip, path, name, types, 
         close(y[t], want)
 
 
+@pytest.mark.parametrize("name,types,D,FF,E,k,use_norm", [
+    ("c2_q4_k_m", (Q4_K, Q4_K, Q6_K), 2048, 768, 128, 8, True),
+    ("c1_q8_0", (Q8_0, Q8_0, Q8_0), 256, 128, 8, 2, True),
+    ("c5_q4_k_m", (Q4_K, Q4_K, Q6_K), 4096, 1536, 128, 8, True),
+    ("c2_given_xn", (Q4_K, Q4_K, Q6_K), 2048, 768, 128, 8, False),
+], ids=lambda c: c if isinstance(c, str) else None)
+def test_moe_layer_decode_xn_vs_oracle(torch_dev, binding, hip, path, name, types, D, FF, E, k, use_norm):
+    """The layer from its residual stream: RMSNorm, the F32 router matmul,
+    routing and experts on the device (eahmmf_hip_moe_layer_decode_xn_async)
+    against the oracle's rmsnorm -> matmul -> route_topk -> expert block
+    (qwen3moe.cpp:1020-1067): normalized input and logits to fp32 rounding,
+    ids bit-exact, weights to a few ulps, y within tolerance."""
+    torch = torch_dev
+    rng = np.random.default_rng(E + D + 7)
+    n_unique = min(E, 16)
+    uniq = make_layer(binding, types, D, FF, n_unique, rng)
+    layer = [uniq[e % n_unique] for e in range(E)]
+    dev_u = [[to_dev(torch, uniq[e][c][1]) for c in range(3)] for e in range(n_unique)]
+    table = np.array([[dev_u[e % n_unique][c].data_ptr() for c in range(3)] for e in range(E)], dtype=np.uint64)
+    dtable = to_dev(torch, table.view(np.int64))
+    gt_, ut, dt_ = types
+    shape = binding.MoeShape(gt_, ut, dt_, D, FF, binding.row_bytes(gt_, D), binding.row_bytes(ut, D),
+                             binding.row_bytes(dt_, FF))
+    T, eps = 4, 1e-6
+    hs = (rng.normal(0, 1, (T, D)) * rng.uniform(0.5, 3.0, (T, 1))).astype(np.float32)
+    norm_w = (1 + rng.normal(0, 0.05, D)).astype(np.float32)
+    router = rng.normal(0, 0.05, (E, D)).astype(np.float32)
+    xn_want = oracle.rmsnorm(hs, norm_w, eps) if use_norm else hs
+    logits_want = oracle.matmul(0, router.view(np.uint8), D, xn_want)
+    ids, w = oracle.route_topk(logits_want, k)
+    dh, dnw, dr = to_dev(torch, hs), to_dev(torch, norm_w), to_dev(torch, router)
+    dy = torch.full((T, D), float("nan"), device="cuda")
+    dxn = torch.full((T, D), float("nan"), device="cuda")
+    dlog = torch.full((T, E), float("nan"), device="cuda")
+    dids = torch.full((T, k), -7, dtype=torch.int32, device="cuda")
+    dw = torch.zeros((T, k), dtype=torch.float32, device="cuda")
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    for t in range(T):
+        rc = hip.eahmmf_hip_moe_layer_decode_xn_async(
+            ctypes.byref(shape), ptr(dtable), E, ptr(dr), ptr(dnw) if use_norm else None, ctypes.c_float(eps),
+            ptr(dh[t]), k, ptr(dy[t]), ptr(dids[t]), ptr(dw[t]), ptr(dxn[t]) if use_norm else None, ptr(dlog[t]),
+            stream)
+        assert rc == 0, hip.eahmmf_hip_last_error()
+    torch.cuda.synchronize()
+    if use_norm:
+        np.testing.assert_allclose(dxn.cpu().numpy(), xn_want, rtol=2e-6, atol=1e-7)
+    lg = dlog.cpu().numpy()
+    assert np.abs(lg - logits_want).max() <= 1e-5 * max(1.0, np.abs(logits_want).max())
+    # the drawn logits leave no near-tie at the k-th place (else the summation
+    # order could swap two ids, as the entry point's declaration says)
+    srt = -np.sort(-logits_want, axis=1)
+    assert (srt[:, k - 1] - srt[:, k]).min() > 1e-4
+    assert np.array_equal(dids.cpu().numpy(), ids)
+    np.testing.assert_allclose(dw.cpu().numpy(), w, rtol=1e-5, atol=0)
+    y = dy.cpu().numpy()
+    for t in range(T):
+        close(y[t], oracle.moe_layer(layer, xn_want[t:t + 1], ids[t:t + 1], w[t:t + 1])[0])
+
+
 @pytest.mark.parametrize("n_expert,k,levels", [(128, 8, 3), (256, 16, 2), (64, 8, 1), (100, 6, 4)])
 def test_layer_routing_ties(torch_dev, binding, hip, path, n_expert, k, levels):
     """Logits drawn from a few levels (many exact ties): the chosen ids follow
