@@ -295,3 +295,107 @@ class DeviceModel:
 
     def __del__(self):
         self.close()
+
+
+# ---------------------------------------------------------------------------
+# GGUF v3 reader (the file layout qwen3moe.cpp:285-346 parses): key/values,
+# the tensor table and zero-copy views of the tensor bytes in a memory map.
+
+_GGUF_SCALAR = {0: "<B", 1: "<b", 2: "<H", 3: "<h", 4: "<I", 5: "<i", 6: "<f", 7: "<?", 10: "<Q", 11: "<q", 12: "<d"}
+
+
+def read_gguf(path):
+    """-> (kv: dict, tensors: {name: (ggml type, ne (ne0 first), numpy view)}).
+    Quantized tensors are uint8 [rows][row_bytes] views, F32 tensors float32
+    [rows][ne0]; both read-only views of a memory map of the file."""
+    import mmap
+    import struct
+
+    import numpy as np
+    with open(path, "rb") as f:
+        mm = mmap.mmap(f.fileno(), 0, access=mmap.ACCESS_READ)
+    pos = 0
+
+    def take(fmt):
+        nonlocal pos
+        v = struct.unpack_from(fmt, mm, pos)
+        pos += struct.calcsize(fmt)
+        return v[0]
+
+    def string():
+        nonlocal pos
+        n = take("<Q")
+        s = bytes(mm[pos:pos + n]).decode("utf-8", "replace")
+        pos += n
+        return s
+
+    def value(t):
+        if t in _GGUF_SCALAR:
+            return take(_GGUF_SCALAR[t])
+        if t == 8:
+            return string()
+        if t == 9:
+            et, n = take("<I"), take("<Q")
+            return [value(et) for _ in range(n)]
+        raise ValueError(f"{path}: unknown GGUF value type {t}")
+
+    if bytes(mm[0:4]) != b"GGUF":
+        raise ValueError(f"{path}: not a GGUF file")
+    pos = 4
+    version, n_tensors, n_kv = take("<I"), take("<Q"), take("<Q")
+    if version < 2:
+        raise ValueError(f"{path}: GGUF version {version} not supported")
+    kv = {}
+    for _ in range(n_kv):
+        key = string()
+        kv[key] = value(take("<I"))
+    infos = []
+    for _ in range(n_tensors):
+        name = string()
+        nd = take("<I")
+        ne = [take("<Q") for _ in range(nd)]
+        t, off = take("<I"), take("<Q")
+        infos.append((name, t, ne, off))
+    align = int(kv.get("general.alignment", 32))
+    base = (pos + align - 1) // align * align
+    buf = np.frombuffer(mm, dtype=np.uint8)
+    tensors = {}
+    for name, t, ne, off in infos:
+        if t not in BLOCK:
+            raise ValueError(f"{path}: tensor {name} has unsupported type {t}")
+        rb = row_bytes(t, ne[0])
+        rows = int(np.prod(ne[1:])) if len(ne) > 1 else 1
+        raw = buf[base + off: base + off + rb * rows].reshape(rows, rb)
+        tensors[name] = (t, list(ne), raw.view(np.float32) if t == GGML_F32 else raw)
+    return kv, tensors
+
+
+def gguf_hparams(kv, tensors, ctx):
+    """The model hyper-parameters as the reference's Engine::load reads them
+    (qwen3moe.cpp:862-882): required keys, the same defaults, n_ctx =
+    min(ctx, context_length), n_vocab from the output head's rows."""
+    if kv.get("general.architecture") != "qwen3moe":
+        raise ValueError(f"unsupported architecture {kv.get('general.architecture')!r} (need qwen3moe)")
+    a = "qwen3moe."
+
+    def need(key):
+        if a + key not in kv:
+            raise ValueError(f"missing GGUF key {a + key}")
+        return kv[a + key]
+
+    hp = dict(n_layer=int(need("block_count")), D=int(need("embedding_length")), n_head=int(need("attention.head_count")),
+              n_kv=int(need("attention.head_count_kv")), n_expert=int(need("expert_count")),
+              n_used=int(need("expert_used_count")), FF=int(need("expert_feed_forward_length")))
+    hp["hd"] = int(kv.get(a + "attention.key_length", hp["D"] // hp["n_head"]))
+    hp["eps"] = float(kv.get(a + "attention.layer_norm_rms_epsilon", 1e-6))
+    hp["rope_base"] = float(kv.get(a + "rope.freq_base", 1e6))
+    hp["n_ctx"] = min(int(ctx), int(kv.get(a + "context_length", 4096)))
+    head = tensors.get("output.weight", tensors["token_embd.weight"])
+    hp["n_vocab"] = int(head[1][1])
+    return hp
+
+
+def model_from_gguf(path, ctx):
+    """A DeviceModel of a qwen3moe GGUF file (the reference's Engine::load)."""
+    kv, tensors = read_gguf(path)
+    return DeviceModel(gguf_hparams(kv, tensors, ctx), tensors)

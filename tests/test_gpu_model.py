@@ -243,3 +243,18 @@ def test_long_context_against_oracle(torch_dev, binding, shape):
         np.testing.assert_allclose(lg, lo, rtol=0, atol=1e-4)
     finally:
         m.close()
+
+
+def test_model_from_gguf_file(tmp_path, torch_dev, binding):
+    """The tiny model loaded from a GGUF file through the binding's reader
+    gives the reference's baseline logits (as Engine::load + eval)."""
+    spec = gt.test_tiny_spec()
+    path = tmp_path / "tiny.gguf"
+    gt.write_gguf(spec, str(path))
+    ref = np.load(os.path.join(GOLDEN, "tiny_ref.npz"))
+    m = binding.model_from_gguf(str(path), 128)
+    try:
+        lg = m.eval(ref["prompt"], 0, 32)
+        np.testing.assert_allclose(lg, ref["logits_b32"], rtol=0, atol=1e-4)
+    finally:
+        m.close()
