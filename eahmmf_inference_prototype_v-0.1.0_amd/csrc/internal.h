@@ -121,11 +121,23 @@ bool grouped_mfma_gate_up_ok(const MoeShape& s);
 bool grouped_mfma_down_ok(const MoeShape& s);
 hipError_t launch_prep_rows(const int* offs, int E, const int* tok, const float* src, int ld, int n, int P,
                             _Float16* vh, _Float16* vl, _Float16* sh, _Float16* sl, float* vscale, hipStream_t st);
+// (experts holding fewer than tmin tokens are left to the per-wave kernels)
 hipError_t launch_gate_up_mfma(const MoeShape& s, const ExpertEntry* table, int E, const int* offs, int nb,
                                const _Float16* xh, const _Float16* xl, const _Float16* xsh, const _Float16* xsl,
-                               const float* xscale, float* h, hipStream_t st);
+                               const float* xscale, float* h, int tmin, hipStream_t st);
 hipError_t launch_down_mfma(const MoeShape& s, const ExpertEntry* table, int E, const int* offs, int nb,
-                            const _Float16* hh, const _Float16* hl, const float* hscale, float* yp, hipStream_t st);
+                            const _Float16* hh, const _Float16* hl, const float* hscale, float* yp, int tmin,
+                            hipStream_t st);
+// Per-wave matrix-core matmuls for experts holding 1..tmax tokens, tmax <= 32
+// (kernels_grouped_wave.hip); the same formats as the workgroup kernels.
+hipError_t launch_gate_up_wave(const MoeShape& s, const ExpertEntry* table, int E, const int* offs, const _Float16* xh,
+                               const _Float16* xl, const _Float16* xsh, const _Float16* xsl, const float* xscale,
+                               float* h, int tmax, hipStream_t st);
+hipError_t launch_down_wave(const MoeShape& s, const ExpertEntry* table, int E, const int* offs, const _Float16* hh,
+                            const _Float16* hl, const float* hscale, float* yp, int tmax, hipStream_t st);
+// Largest expert (in tokens) the per-wave kernels take (0: none, at most 32);
+// a negative argument only queries.  Returns the previous value.
+int set_grouped_wave_max(int tmax);
 // 1 (default): the grouped block uses the matrix-core matmuls where the formats
 // allow; 0: the vector-ALU kernels only.  A negative argument only queries.
 int set_grouped_mfma(int enable);

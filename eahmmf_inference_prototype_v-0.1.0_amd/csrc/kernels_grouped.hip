@@ -292,6 +292,16 @@ int set_grouped_mfma(int enable) {
     return prev;
 }
 
+// Experts holding at most this many tokens run on the per-wave matrix-core
+// kernels (kernels_grouped_wave.hip), the rest on the workgroup kernels.
+int g_wave_max = 32;
+
+int set_grouped_wave_max(int tmax) {
+    const int prev = g_wave_max;
+    if (tmax >= 0) g_wave_max = tmax > 32 ? 32 : tmax;
+    return prev;
+}
+
 size_t grouped_scratch_bytes(const MoeShape& s, int nb, int k, int n_expert) {
     const size_t P = (size_t)nb * k, nchunks = ((size_t)nb + 63) / 64;
     auto al = [](size_t b) { return (b + 255) & ~(size_t)255; };
@@ -337,10 +347,15 @@ hipError_t launch_moe_grouped(const MoeShape& s, const ExpertEntry* table, int n
     group_pairs_kernel<<<1, kGroupThreads, lds, st>>>(ids, w, nb, k, n_expert, cnt, offs, tok, pw, pos);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
+    const int wave_max = g_wave_max;
     if (mf_gu) {
         if ((e = launch_prep_rows(offs, n_expert, tok, x, ldx, s.D, (int)P, xh, xl, xsh, xsl, xsc, st)) != hipSuccess)
             return e;
-        if ((e = launch_gate_up_mfma(s, table, n_expert, offs, nb, xh, xl, xsh, xsl, xsc, h, st)) != hipSuccess)
+        if (wave_max > 0 &&
+            (e = launch_gate_up_wave(s, table, n_expert, offs, xh, xl, xsh, xsl, xsc, h, wave_max, st)) != hipSuccess)
+            return e;
+        if ((e = launch_gate_up_mfma(s, table, n_expert, offs, nb, xh, xl, xsh, xsl, xsc, h, wave_max + 1, st)) !=
+            hipSuccess)
             return e;
     } else {
         const dim3 ga((unsigned)((s.FF + 3) / 4), (unsigned)n_expert);
@@ -358,7 +373,10 @@ hipError_t launch_moe_grouped(const MoeShape& s, const ExpertEntry* table, int n
         if ((e = launch_prep_rows(offs, n_expert, nullptr, h, s.FF, s.FF, (int)P, hh, hl, nullptr, nullptr, hsc, st)) !=
             hipSuccess)
             return e;
-        if ((e = launch_down_mfma(s, table, n_expert, offs, nb, hh, hl, hsc, yp, st)) != hipSuccess) return e;
+        if (wave_max > 0 && (e = launch_down_wave(s, table, n_expert, offs, hh, hl, hsc, yp, wave_max, st)) != hipSuccess)
+            return e;
+        if ((e = launch_down_mfma(s, table, n_expert, offs, nb, hh, hl, hsc, yp, wave_max + 1, st)) != hipSuccess)
+            return e;
     } else {
         const dim3 gd((unsigned)((s.D + 3) / 4), (unsigned)n_expert);
         switch (s.down_type) {

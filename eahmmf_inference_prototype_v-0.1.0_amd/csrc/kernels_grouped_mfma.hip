@@ -26,39 +26,9 @@
 // once.
 #include "internal.h"
 #include "kquant.h"
+#include "mfma_frag.h"
 
 namespace eahmmf {
-
-typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
-typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
-typedef float f32x4 __attribute__((ext_vector_type(4)));
-
-constexpr int kPassTok = 64;  // tokens per pass: four 16-token tiles
-constexpr float kSumScale = 1.0f / 16.0f;  // sub-block sums (32 values) kept below 2^14
-
-struct __attribute__((packed, aligned(2))) Bytes8A2 { uint32_t x, y; };
-__device__ __forceinline__ uint2 ld8_a2(const uint8_t* p) {
-    const Bytes8A2 v = *reinterpret_cast<const Bytes8A2*>(p);
-    return make_uint2(v.x, v.y);
-}
-__device__ __forceinline__ uint2 ld8(const uint8_t* p) { return *reinterpret_cast<const uint2*>(p); }
-
-// Two fp16 values b0, b1 from bytes 2m, 2m+1 of w (each < 256): the byte is
-// placed under the exponent of 1024 (0x64XX = 1024 + XX) and 1024 removed.
-template <int M>
-__device__ __forceinline__ f16x2 byte_pair(uint32_t w) {
-    constexpr uint32_t sel = M == 0 ? 0x04010400u : 0x04030402u;
-    const f16x2 v = __builtin_bit_cast(f16x2, __builtin_amdgcn_perm(0x64646464u, w, sel));
-    return v - (f16x2){(_Float16)1024.0f, (_Float16)1024.0f};
-}
-
-// Eight codes (bytes of c) times an integer factor f (|code * f| exact in fp16).
-__device__ __forceinline__ f16x8 codes_times(uint2 c, _Float16 f, _Float16 bias) {
-    const f16x2 fv = {f, f}, bv = {bias, bias};
-    const f16x2 a = (byte_pair<0>(c.x) + bv) * fv, b = (byte_pair<1>(c.x) + bv) * fv;
-    const f16x2 d = (byte_pair<0>(c.y) + bv) * fv, e = (byte_pair<1>(c.y) + bv) * fv;
-    return (f16x8){a.x, a.y, b.x, b.y, d.x, d.y, e.x, e.y};
-}
 
 // Workgroup barrier for LDS hand-offs only.  __syncthreads() carries a
 // workgroup release fence, which on this target waits for every outstanding
@@ -72,14 +42,6 @@ __device__ __forceinline__ void lds_barrier() {
     __builtin_amdgcn_s_waitcnt(0xC07F);
     __builtin_amdgcn_s_barrier();
     __atomic_signal_fence(__ATOMIC_SEQ_CST);
-}
-
-__device__ __forceinline__ f32x4 mfma(f16x8 a, f16x8 b, f32x4 c) {
-    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
-}
-
-__device__ __forceinline__ float half_at(const uint8_t* p) {
-    return (float)__builtin_bit_cast(_Float16, *reinterpret_cast<const uint16_t*>(p));
 }
 
 // ---------------------------------------------------------------------------
@@ -177,7 +139,8 @@ __global__ __launch_bounds__(512) void gate_up_mfma_kernel(MoeShape s, const Exp
                                                            const _Float16* __restrict__ xl,
                                                            const _Float16* __restrict__ xsh,
                                                            const _Float16* __restrict__ xsl,
-                                                           const float* __restrict__ xscale, float* __restrict__ h) {
+                                                           const float* __restrict__ xscale, float* __restrict__ h,
+                                                           int tmin) {
     static_assert(T == kQ4_K || T == kQ5_K, "gate/up MFMA path: Q4_K or Q5_K");
     constexpr int BB = Fmt<T>::bytes;
     constexpr int QS = T == kQ5_K ? 48 : 16;  // offset of the 4-bit codes in a super-block
@@ -185,7 +148,7 @@ __global__ __launch_bounds__(512) void gate_up_mfma_kernel(MoeShape s, const Exp
     const int e = blockIdx.y;
     const int p0 = offs[e], p1 = offs[e + 1];
     const int pb = p0 + (int)blockIdx.z * kGuTok;
-    if (pb >= p1) return;  // whole workgroup
+    if (pb >= p1 || p1 - p0 < tmin) return;  // whole workgroup (experts below tmin: the per-wave kernel)
     const int tid = threadIdx.x, wave = tid >> 6, l = tid & 63;
     const int lr = l & 15, kq = l >> 4;
     const int rw = blockIdx.x * kGuRows;
@@ -369,12 +332,12 @@ __global__ __launch_bounds__(512) void down_mfma_q6k_kernel(MoeShape s, const Ex
                                                             const _Float16* __restrict__ hh,
                                                             const _Float16* __restrict__ hl,
                                                             const float* __restrict__ hscale,
-                                                            float* __restrict__ yp) {
+                                                            float* __restrict__ yp, int tmin) {
     __shared__ _Float16 LB[2][2][kPassTok][kBRow];  // [stage][hi, lo][token][k]
     const int e = blockIdx.y;
     const int p0 = offs[e], p1 = offs[e + 1];
     const int pb = p0 + (int)blockIdx.z * kPassTok;
-    if (pb >= p1) return;
+    if (pb >= p1 || p1 - p0 < tmin) return;
     const int tid = threadIdx.x, wave = tid >> 6, l = tid & 63;
     const int lr = l & 15, kq = l >> 4;
     const int r0 = blockIdx.x * kDnRows + wave * 16;
@@ -515,19 +478,20 @@ hipError_t launch_prep_rows(const int* offs, int E, const int* tok, const float*
 
 hipError_t launch_gate_up_mfma(const MoeShape& s, const ExpertEntry* table, int E, const int* offs, int nb,
                                const _Float16* xh, const _Float16* xl, const _Float16* xsh, const _Float16* xsl,
-                               const float* xscale, float* h, hipStream_t st) {
+                               const float* xscale, float* h, int tmin, hipStream_t st) {
     const dim3 g((unsigned)((s.FF + kGuRows - 1) / kGuRows), (unsigned)E, (unsigned)((nb + kGuTok - 1) / kGuTok));
     if (s.gate_type == kQ4_K)
-        gate_up_mfma_kernel<kQ4_K><<<g, 512, 0, st>>>(s, table, offs, xh, xl, xsh, xsl, xscale, h);
+        gate_up_mfma_kernel<kQ4_K><<<g, 512, 0, st>>>(s, table, offs, xh, xl, xsh, xsl, xscale, h, tmin);
     else
-        gate_up_mfma_kernel<kQ5_K><<<g, 512, 0, st>>>(s, table, offs, xh, xl, xsh, xsl, xscale, h);
+        gate_up_mfma_kernel<kQ5_K><<<g, 512, 0, st>>>(s, table, offs, xh, xl, xsh, xsl, xscale, h, tmin);
     return hipGetLastError();
 }
 
 hipError_t launch_down_mfma(const MoeShape& s, const ExpertEntry* table, int E, const int* offs, int nb,
-                            const _Float16* hh, const _Float16* hl, const float* hscale, float* yp, hipStream_t st) {
+                            const _Float16* hh, const _Float16* hl, const float* hscale, float* yp, int tmin,
+                            hipStream_t st) {
     const dim3 g((unsigned)((s.D + kDnRows - 1) / kDnRows), (unsigned)E, (unsigned)((nb + kPassTok - 1) / kPassTok));
-    down_mfma_q6k_kernel<<<g, 512, 0, st>>>(s, table, offs, hh, hl, hscale, yp);
+    down_mfma_q6k_kernel<<<g, 512, 0, st>>>(s, table, offs, hh, hl, hscale, yp, tmin);
     return hipGetLastError();
 }
 

@@ -1,0 +1,51 @@
+// mfma_frag.h - exact fp16 operands for v_mfma_f32_16x16x32_f16 in the
+// grouped expert matmuls (kernels_grouped_mfma.hip, kernels_grouped_wave.hip).
+//
+// Operand layout (16x16x32): lane l holds A[l%16][8*(l/16) + i],
+// B[8*(l/16) + i][l%16] and C[4*(l/16) + i][l%16], i < 8 (C: i < 4).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace eahmmf {
+
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kPassTok = 64;  // tokens per pass: four 16-token tiles
+constexpr float kSumScale = 1.0f / 16.0f;  // sub-block sums (32 values) kept below 2^14
+
+struct __attribute__((packed, aligned(2))) Bytes8A2 { uint32_t x, y; };
+__device__ __forceinline__ uint2 ld8_a2(const uint8_t* p) {
+    const Bytes8A2 v = *reinterpret_cast<const Bytes8A2*>(p);
+    return make_uint2(v.x, v.y);
+}
+__device__ __forceinline__ uint2 ld8(const uint8_t* p) { return *reinterpret_cast<const uint2*>(p); }
+
+// Two fp16 values b0, b1 from bytes 2m, 2m+1 of w (each < 256): the byte is
+// placed under the exponent of 1024 (0x64XX = 1024 + XX) and 1024 removed.
+template <int M>
+__device__ __forceinline__ f16x2 byte_pair(uint32_t w) {
+    constexpr uint32_t sel = M == 0 ? 0x04010400u : 0x04030402u;
+    const f16x2 v = __builtin_bit_cast(f16x2, __builtin_amdgcn_perm(0x64646464u, w, sel));
+    return v - (f16x2){(_Float16)1024.0f, (_Float16)1024.0f};
+}
+
+// Eight codes (bytes of c) times an integer factor f (|code * f| exact in fp16).
+__device__ __forceinline__ f16x8 codes_times(uint2 c, _Float16 f, _Float16 bias) {
+    const f16x2 fv = {f, f}, bv = {bias, bias};
+    const f16x2 a = (byte_pair<0>(c.x) + bv) * fv, b = (byte_pair<1>(c.x) + bv) * fv;
+    const f16x2 d = (byte_pair<0>(c.y) + bv) * fv, e = (byte_pair<1>(c.y) + bv) * fv;
+    return (f16x8){a.x, a.y, b.x, b.y, d.x, d.y, e.x, e.y};
+}
+
+__device__ __forceinline__ f32x4 mfma(f16x8 a, f16x8 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ float half_at(const uint8_t* p) {
+    return (float)__builtin_bit_cast(_Float16, *reinterpret_cast<const uint16_t*>(p));
+}
+
+}  // namespace eahmmf

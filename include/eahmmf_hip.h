@@ -278,6 +278,12 @@ int eahmmf_hip_fused_exchange(void);
  * kernels only (0); a negative argument only queries.  Returns the previous
  * setting. */
 int eahmmf_hip_set_grouped_mfma(int enable);
+/* Largest expert group, in tokens, that the grouped block's matrix-core
+ * matmuls run on the per-wave kernels (each wave its own 16 rows, one or two
+ * 16-token tiles); larger groups use the workgroup kernels.  0 disables the
+ * per-wave kernels, at most 32 (default 32); a negative argument only
+ * queries.  Returns the previous value.  No counterpart in the reference. */
+int eahmmf_hip_set_grouped_wave_max(int max_tokens);
 /* The single-launch expert block's workgroups wait for each other's words
  * (h, per-partition partials).  Every wait is bounded; when one gives up the
  * launch writes NaN where the missing words were needed and records its

@@ -508,11 +508,17 @@ GROUPED_CASES = [
 ]
 
 
-@pytest.fixture(params=[1, 0], ids=["mfma", "valu"])
+@pytest.fixture(params=[(1, 32), (1, 16), (1, 0), (0, 32)], ids=["mfma", "mfma_wave16", "mfma_wg", "valu"])
 def grouped_mode(request, hip):
-    prev = hip.eahmmf_hip_set_grouped_mfma(request.param)
+    """Matrix-core or VALU grouped kernels; with the matrix cores, experts of
+    at most `wave_max` tokens go to the per-wave kernels (two 16-token tiles
+    above 16, one at or below), the rest to the workgroup kernels."""
+    mfma, wave_max = request.param
+    prev = hip.eahmmf_hip_set_grouped_mfma(mfma)
+    prev_w = hip.eahmmf_hip_set_grouped_wave_max(wave_max)
     yield request.param
     hip.eahmmf_hip_set_grouped_mfma(prev)
+    hip.eahmmf_hip_set_grouped_wave_max(prev_w)
 
 
 @pytest.mark.parametrize("name,types,D,FF,E,k,nb", GROUPED_CASES, ids=[c[0] for c in GROUPED_CASES])
