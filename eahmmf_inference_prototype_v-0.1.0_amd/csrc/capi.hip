@@ -712,6 +712,8 @@ int eahmmf_hip_set_grouped_mfma(int enable) { return set_grouped_mfma(enable); }
 
 int eahmmf_hip_set_grouped_wave_max(int max_tokens) { return set_grouped_wave_max(max_tokens); }
 
+int eahmmf_hip_set_grouped_dot_max(int max_tokens) { return set_grouped_dot_max(max_tokens); }
+
 int eahmmf_hip_set_fused(int enable) {
     const int prev = fused_enabled() ? 1 : 0;
     if (enable >= 0) g_fused = enable ? 1 : 0;

@@ -128,16 +128,30 @@ hipError_t launch_gate_up_mfma(const MoeShape& s, const ExpertEntry* table, int 
 hipError_t launch_down_mfma(const MoeShape& s, const ExpertEntry* table, int E, const int* offs, int nb,
                             const _Float16* hh, const _Float16* hl, const float* hscale, float* yp, int tmin,
                             hipStream_t st);
-// Per-wave matrix-core matmuls for experts holding 1..tmax tokens, tmax <= 32
+// Per-wave matrix-core matmuls for experts holding tmin..tmax tokens, tmax <= 32
 // (kernels_grouped_wave.hip); the same formats as the workgroup kernels.
 hipError_t launch_gate_up_wave(const MoeShape& s, const ExpertEntry* table, int E, const int* offs, const _Float16* xh,
                                const _Float16* xl, const _Float16* xsh, const _Float16* xsl, const float* xscale,
-                               float* h, int tmax, hipStream_t st);
+                               float* h, int tmin, int tmax, hipStream_t st);
 hipError_t launch_down_wave(const MoeShape& s, const ExpertEntry* table, int E, const int* offs, const _Float16* hh,
-                            const _Float16* hl, const float* hscale, float* yp, int tmax, hipStream_t st);
+                            const _Float16* hl, const float* hscale, float* yp, int tmin, int tmax, hipStream_t st);
 // Largest expert (in tokens) the per-wave kernels take (0: none, at most 32);
 // a negative argument only queries.  Returns the previous value.
 int set_grouped_wave_max(int tmax);
+// Integer-dot matmuls for experts holding tmin..tmax tokens, tmax <= 32
+// (kernels_grouped_dot.hip): gate/up from x rows to h's int8 levels
+// (hq [P][3][FF], hsc [P][3][FF/64], hs32 [P][FF/32]), down from those levels.
+bool grouped_dot_gate_up_ok(const MoeShape& s);
+bool grouped_dot_down_ok(const MoeShape& s);
+hipError_t launch_gate_up_dot(const MoeShape& s, const ExpertEntry* table, int E, const int* offs, const int* tok,
+                              const float* x, int ldx, int8_t* hq, float* hsc, float* hs32, int tmin, int tmax,
+                              hipStream_t st);
+hipError_t launch_down_dot(const MoeShape& s, const ExpertEntry* table, int E, const int* offs, const int8_t* hq,
+                           const float* hsc, const float* hs32, float* yp, int tmin, int tmax, hipStream_t st);
+// Largest expert (in tokens) the integer-dot kernels take in a batch of more
+// than 32 tokens (0: none; batches of at most 32 tokens run on them whole
+// unless this is 0); a negative argument only queries.  Returns the previous value.
+int set_grouped_dot_max(int tmax);
 // 1 (default): the grouped block uses the matrix-core matmuls where the formats
 // allow; 0: the vector-ALU kernels only.  A negative argument only queries.
 int set_grouped_mfma(int enable);

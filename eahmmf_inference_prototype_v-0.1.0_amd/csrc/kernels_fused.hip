@@ -261,50 +261,6 @@ __device__ __forceinline__ bool load8_words(const uint64_t* src, int seg, int pa
     return good;
 }
 
-// Levels of the eight values v of segment seg; every lane of the wave calls it
-// (the segment's amax and sums are exchanged by shuffles).
-__device__ __forceinline__ void quantize8(const float (&v)[8], int seg, int part, bool active, int8_t* q, int qstride,
-                                          float* sc, int scstride, float* s32) {
-    float amax = 0.f, sum = 0.f;
-#pragma unroll
-    for (int i = 0; i < 8; i++) {
-        amax = fmaxf(amax, fabsf(v[i]));
-        sum += v[i];
-    }
-    // over the 8 threads of the segment (DPP quad swaps and row_half_mirror)
-    amax = dpp_fmax_step<0xB1, 0xF>(amax, amax);
-    amax = dpp_fmax_step<0x4E, 0xF>(amax, amax);
-    amax = dpp_fmax_step<0x141, 0xF>(amax, amax);
-    sum = dpp_add_step<0xB1>(sum);
-    sum = dpp_add_step<0x4E>(sum);  // four threads = 32 values
-    if (!active) return;
-    // Scales need only be consistent, not exact quotients: each level's
-    // residual r - q*s is formed exactly (fma), and an inverse within an ulp
-    // (v_rcp) keeps |residual| <= s/2 (1 + 2^-22), inside the next level's
-    // +-127 * s/254 range up to its clamp.
-    const float s1 = amax * (1.0f / 127.0f);
-    const float s2 = s1 * (1.0f / 254.0f), s3 = s2 * (1.0f / 254.0f);
-    const float lsc[kLevels] = {s1, s2, s3};
-    float r[8];
-#pragma unroll
-    for (int i = 0; i < 8; i++) r[i] = v[i];
-#pragma unroll
-    for (int lv = 0; lv < kLevels; lv++) {
-        const float inv = lsc[lv] > 0.f ? __builtin_amdgcn_rcpf(lsc[lv]) : 0.f;
-        uint32_t packed[2] = {0u, 0u};
-#pragma unroll
-        for (int i = 0; i < 8; i++) {
-            float qf = __builtin_rintf(r[i] * inv);
-            qf = fminf(127.f, fmaxf(-127.f, qf));
-            r[i] = __builtin_fmaf(-qf, lsc[lv], r[i]);
-            packed[i >> 2] |= ((uint32_t)(int)qf & 0xFFu) << (8 * (i & 3));
-        }
-        *reinterpret_cast<uint2*>(q + lv * qstride + seg * 64 + part * 8) = make_uint2(packed[0], packed[1]);
-        if (part == 0) sc[lv * scstride + seg] = lsc[lv];
-    }
-    if ((part & 3) == 0) s32[seg * 2 + part / 4] = sum;
-}
-
 // Levels of n values held as exchange words, by threads t in [0, nthr) (nthr
 // a multiple of 64).  False if a wait gave up.
 __device__ bool quantize_words(const uint64_t* src, int n, unsigned epoch, unsigned* sync, unsigned spin_limit,

@@ -37,28 +37,6 @@ __device__ __forceinline__ unsigned long long argmax_key(float v, unsigned idx) 
     return ((unsigned long long)o << 32) | (unsigned long long)(0xFFFFFFFFu - idx);
 }
 
-// s_waitcnt vmcnt(n) for a run-time n (0..15).
-__device__ __forceinline__ void wait_vm_n(int n) {
-    switch (n) {
-        case 0: wait_vm_upto<0>(); break;
-        case 1: wait_vm_upto<1>(); break;
-        case 2: wait_vm_upto<2>(); break;
-        case 3: wait_vm_upto<3>(); break;
-        case 4: wait_vm_upto<4>(); break;
-        case 5: wait_vm_upto<5>(); break;
-        case 6: wait_vm_upto<6>(); break;
-        case 7: wait_vm_upto<7>(); break;
-        case 8: wait_vm_upto<8>(); break;
-        case 9: wait_vm_upto<9>(); break;
-        case 10: wait_vm_upto<10>(); break;
-        case 11: wait_vm_upto<11>(); break;
-        case 12: wait_vm_upto<12>(); break;
-        case 13: wait_vm_upto<13>(); break;
-        case 14: wait_vm_upto<14>(); break;
-        default: wait_vm_upto<15>(); break;
-    }
-}
-
 // The launch's row segments in registers (no reference to the kernel
 // argument block: taking its address would copy it to scratch memory, and a
 // scratch load's wait would also wait for the DMA in flight).

@@ -131,10 +131,10 @@ __global__ __launch_bounds__(256) void grouped_gate_up_kernel(MoeShape s, const 
                                                               const int* __restrict__ offs,
                                                               const int* __restrict__ tok,
                                                               const float* __restrict__ x, int ldx,
-                                                              float* __restrict__ h) {
+                                                              float* __restrict__ h, int tmin) {
     const int e = blockIdx.y;
     const int p0 = offs[e], p1 = offs[e + 1];
-    if (p1 <= p0) return;
+    if (p1 <= p0 || p1 - p0 < tmin) return;  // (smaller groups: the integer-dot kernels)
     const int lane = threadIdx.x & 63;
     const int r = blockIdx.x * 4 + (threadIdx.x >> 6);
     if (r >= s.FF) return;  // whole wave
@@ -190,10 +190,10 @@ __global__ __launch_bounds__(256) void grouped_gate_up_kernel(MoeShape s, const 
 template <int DT>
 __global__ __launch_bounds__(256) void grouped_down_kernel(MoeShape s, const ExpertEntry* __restrict__ table,
                                                            const int* __restrict__ offs, const float* __restrict__ h,
-                                                           float* __restrict__ yp) {
+                                                           float* __restrict__ yp, int tmin) {
     const int e = blockIdx.y;
     const int p0 = offs[e], p1 = offs[e + 1];
-    if (p1 <= p0) return;
+    if (p1 <= p0 || p1 - p0 < tmin) return;
     const int lane = threadIdx.x & 63;
     const int r = blockIdx.x * 4 + (threadIdx.x >> 6);
     if (r >= s.D) return;
@@ -235,7 +235,10 @@ __global__ __launch_bounds__(256) void grouped_down_kernel(MoeShape s, const Exp
 }
 
 // y[t][d] = sum over the token's valid pairs, ascending expert id, of
-// w * yp[pos][d].  One thread per (token, 4 consecutive d).
+// w * yp[pos][d].  One thread per (token, 4 consecutive d).  The token's
+// slots are read once into registers; a slot's place in the sum is its rank
+// (ids are distinct per token; equal ids keep slot order), so the fma chain
+// runs in ascending id with no data-dependent indexing.
 __global__ __launch_bounds__(256) void grouped_combine_kernel(const int* __restrict__ ids, const int* __restrict__ pos,
                                                               const float* __restrict__ pw, int nb, int k, int D,
                                                               const float* __restrict__ yp, float* __restrict__ y,
@@ -244,41 +247,61 @@ __global__ __launch_bounds__(256) void grouped_combine_kernel(const int* __restr
     const int per_tok = D / 4;
     if (q >= nb * per_tok) return;
     const int t = q / per_tok, d = (q % per_tok) * 4;
-    // the token's slots in ascending expert id (k <= kMaxSlots; ids are distinct per token)
-    int order[kMaxSlots];
-    int n = 0;
-    for (int j = 0; j < k; j++) {
-        const int pj = pos[(size_t)t * k + j];
-        if (pj < 0) continue;
-        const int ej = ids[(size_t)t * k + j];
-        int i = n++;
-        while (i > 0 && ids[(size_t)t * k + order[i - 1]] > ej) {
-            order[i] = order[i - 1];
-            i--;
-        }
-        order[i] = j;
+    int pj[kMaxSlots], ej[kMaxSlots];
+#pragma unroll
+    for (int j = 0; j < kMaxSlots; j++) {
+        pj[j] = j < k ? pos[(size_t)t * k + j] : -1;
+        ej[j] = j < k ? ids[(size_t)t * k + j] : 0;
+    }
+    float4 v[kMaxSlots];
+    float wv[kMaxSlots];
+    int rank[kMaxSlots];
+#pragma unroll
+    for (int j = 0; j < kMaxSlots; j++) {
+        const bool ok = pj[j] >= 0;
+        v[j] = ok ? *reinterpret_cast<const float4*>(yp + (size_t)pj[j] * D + d) : make_float4(0.f, 0.f, 0.f, 0.f);
+        wv[j] = ok ? pw[pj[j]] : 0.f;
+        int r = 0;
+#pragma unroll
+        for (int i = 0; i < kMaxSlots; i++)
+            r += (i != j && pj[i] >= 0 && (ej[i] < ej[j] || (ej[i] == ej[j] && i < j))) ? 1 : 0;
+        rank[j] = ok ? r : -1;
     }
     float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-    for (int i = 0; i < n; i++) {
-        const int p = pos[(size_t)t * k + order[i]];
-        const float wv = pw[p];
-        const float4 v = *reinterpret_cast<const float4*>(yp + (size_t)p * D + d);
-        acc.x = __builtin_fmaf(wv, v.x, acc.x);
-        acc.y = __builtin_fmaf(wv, v.y, acc.y);
-        acc.z = __builtin_fmaf(wv, v.z, acc.z);
-        acc.w = __builtin_fmaf(wv, v.w, acc.w);
+#pragma unroll
+    for (int r = 0; r < kMaxSlots; r++) {
+        if (r >= k) break;
+        bool any = false;
+        float w = 0.f;
+        float4 x = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+        for (int j = 0; j < kMaxSlots; j++) {
+            const bool sel = rank[j] == r;
+            any |= sel;
+            w = sel ? wv[j] : w;
+            x.x = sel ? v[j].x : x.x;
+            x.y = sel ? v[j].y : x.y;
+            x.z = sel ? v[j].z : x.z;
+            x.w = sel ? v[j].w : x.w;
+        }
+        if (any) {
+            acc.x = __builtin_fmaf(w, x.x, acc.x);
+            acc.y = __builtin_fmaf(w, x.y, acc.y);
+            acc.z = __builtin_fmaf(w, x.z, acc.z);
+            acc.w = __builtin_fmaf(w, x.w, acc.w);
+        }
     }
     *reinterpret_cast<float4*>(y + (size_t)t * ldy + d) = acc;
 }
 
 template <int GT>
 static hipError_t gate_up_for(int ut, const MoeShape& s, dim3 g, const ExpertEntry* table, const int* offs,
-                              const int* tok, const float* x, int ldx, float* h, hipStream_t st) {
+                              const int* tok, const float* x, int ldx, float* h, int tmin, hipStream_t st) {
     switch (ut) {
-        case kQ4_K: grouped_gate_up_kernel<GT, kQ4_K><<<g, 256, 0, st>>>(s, table, offs, tok, x, ldx, h); break;
-        case kQ5_K: grouped_gate_up_kernel<GT, kQ5_K><<<g, 256, 0, st>>>(s, table, offs, tok, x, ldx, h); break;
-        case kQ6_K: grouped_gate_up_kernel<GT, kQ6_K><<<g, 256, 0, st>>>(s, table, offs, tok, x, ldx, h); break;
-        case kQ8_0: grouped_gate_up_kernel<GT, kQ8_0><<<g, 256, 0, st>>>(s, table, offs, tok, x, ldx, h); break;
+        case kQ4_K: grouped_gate_up_kernel<GT, kQ4_K><<<g, 256, 0, st>>>(s, table, offs, tok, x, ldx, h, tmin); break;
+        case kQ5_K: grouped_gate_up_kernel<GT, kQ5_K><<<g, 256, 0, st>>>(s, table, offs, tok, x, ldx, h, tmin); break;
+        case kQ6_K: grouped_gate_up_kernel<GT, kQ6_K><<<g, 256, 0, st>>>(s, table, offs, tok, x, ldx, h, tmin); break;
+        case kQ8_0: grouped_gate_up_kernel<GT, kQ8_0><<<g, 256, 0, st>>>(s, table, offs, tok, x, ldx, h, tmin); break;
         default: return hipErrorInvalidValue;
     }
     return hipSuccess;
@@ -302,6 +325,19 @@ int set_grouped_wave_max(int tmax) {
     return prev;
 }
 
+// Experts holding at most this many tokens run on the integer-dot kernels
+// (kernels_grouped_dot.hip) in batches of more than kDotWhole tokens; a batch
+// of at most kDotWhole tokens (every expert then holds at most nb tokens: a
+// token's pairs with one expert count once) runs on them whole.
+int g_dot_max = 4;
+constexpr int kDotWhole = 32;
+
+int set_grouped_dot_max(int tmax) {
+    const int prev = g_dot_max;
+    if (tmax >= 0) g_dot_max = tmax > kDotWhole ? kDotWhole : tmax;
+    return prev;
+}
+
 size_t grouped_scratch_bytes(const MoeShape& s, int nb, int k, int n_expert) {
     const size_t P = (size_t)nb * k, nchunks = ((size_t)nb + 63) / 64;
     auto al = [](size_t b) { return (b + 255) & ~(size_t)255; };
@@ -309,7 +345,9 @@ size_t grouped_scratch_bytes(const MoeShape& s, int nb, int k, int n_expert) {
                         al(P * s.FF * 4) + al(P * s.D * 4);
     // fp16 hi/lo activations and sub-block sums for the matrix-core path
     const size_t mf = 2 * al(P * s.D * 2) + 2 * al(P * (s.D / 32) * 2) + al(P * 4) + 2 * al(P * s.FF * 2) + al(P * 4);
-    return base + mf;
+    // h as int8 levels (+ scales, 32-value sums) for the integer-dot path
+    const size_t dt = al(P * 3 * s.FF) + al(P * 3 * (s.FF / 64 + 1) * 4) + al(P * (s.FF / 32) * 4);
+    return base + mf + dt;
 }
 
 bool grouped_supported(const MoeShape& s, int nb, int k, int n_expert) {
@@ -339,54 +377,75 @@ hipError_t launch_moe_grouped(const MoeShape& s, const ExpertEntry* table, int n
     float* xsc = reinterpret_cast<float*>(b); b += al(P * 4);
     _Float16* hh = reinterpret_cast<_Float16*>(b); b += al(P * s.FF * 2);
     _Float16* hl = reinterpret_cast<_Float16*>(b); b += al(P * s.FF * 2);
-    float* hsc = reinterpret_cast<float*>(b);
+    float* hsc = reinterpret_cast<float*>(b); b += al(P * 4);
+    int8_t* dq = reinterpret_cast<int8_t*>(b); b += al(P * 3 * s.FF);
+    float* dsc = reinterpret_cast<float*>(b); b += al(P * 3 * (s.FF / 64 + 1) * 4);
+    float* ds32 = reinterpret_cast<float*>(b);
     const bool mf_gu = g_grouped_mfma && grouped_mfma_gate_up_ok(s);
     const bool mf_dn = g_grouped_mfma && grouped_mfma_down_ok(s);
+    // Group sizes by path: 1..dmax the integer-dot kernels, then the per-wave
+    // matrix-core kernels up to wave_max, then the workgroup kernels (or the
+    // vector-ALU kernels for everything above dmax).  A group holds at most nb
+    // tokens, so launches whose range starts above nb are skipped.
+    const bool dot = g_dot_max > 0 && grouped_dot_gate_up_ok(s) && grouped_dot_down_ok(s);
+    const int dmax = !dot ? 0 : (nb <= kDotWhole ? nb : g_dot_max);
+    const int rest = dmax + 1;  // smallest group left to the other kernels
+    const int wave_max = g_wave_max;
+    const int wg_min = wave_max + 1 > rest ? wave_max + 1 : rest;
     clear_stale_error();
     const size_t lds = (size_t)kGroupWaves * n_expert * 8 + (size_t)n_expert * 4;
     group_pairs_kernel<<<1, kGroupThreads, lds, st>>>(ids, w, nb, k, n_expert, cnt, offs, tok, pw, pos);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    const int wave_max = g_wave_max;
-    if (mf_gu) {
-        if ((e = launch_prep_rows(offs, n_expert, tok, x, ldx, s.D, (int)P, xh, xl, xsh, xsl, xsc, st)) != hipSuccess)
-            return e;
-        if (wave_max > 0 &&
-            (e = launch_gate_up_wave(s, table, n_expert, offs, xh, xl, xsh, xsl, xsc, h, wave_max, st)) != hipSuccess)
-            return e;
-        if ((e = launch_gate_up_mfma(s, table, n_expert, offs, nb, xh, xl, xsh, xsl, xsc, h, wave_max + 1, st)) !=
-            hipSuccess)
-            return e;
-    } else {
-        const dim3 ga((unsigned)((s.FF + 3) / 4), (unsigned)n_expert);
-        switch (s.gate_type) {
-            case kQ4_K: e = gate_up_for<kQ4_K>(s.up_type, s, ga, table, offs, tok, x, ldx, h, st); break;
-            case kQ5_K: e = gate_up_for<kQ5_K>(s.up_type, s, ga, table, offs, tok, x, ldx, h, st); break;
-            case kQ6_K: e = gate_up_for<kQ6_K>(s.up_type, s, ga, table, offs, tok, x, ldx, h, st); break;
-            case kQ8_0: e = gate_up_for<kQ8_0>(s.up_type, s, ga, table, offs, tok, x, ldx, h, st); break;
-            default: e = hipErrorInvalidValue;
+    if (dot && (e = launch_gate_up_dot(s, table, n_expert, offs, tok, x, ldx, dq, dsc, ds32, 1, dmax, st)) != hipSuccess)
+        return e;
+    if (nb >= rest) {
+        if (mf_gu) {
+            if ((e = launch_prep_rows(offs, n_expert, tok, x, ldx, s.D, (int)P, xh, xl, xsh, xsl, xsc, st)) !=
+                hipSuccess)
+                return e;
+            if (wave_max >= rest && (e = launch_gate_up_wave(s, table, n_expert, offs, xh, xl, xsh, xsl, xsc, h, rest,
+                                                             wave_max, st)) != hipSuccess)
+                return e;
+            if (nb >= wg_min && (e = launch_gate_up_mfma(s, table, n_expert, offs, nb, xh, xl, xsh, xsl, xsc, h,
+                                                         wg_min, st)) != hipSuccess)
+                return e;
+        } else {
+            const dim3 ga((unsigned)((s.FF + 3) / 4), (unsigned)n_expert);
+            switch (s.gate_type) {
+                case kQ4_K: e = gate_up_for<kQ4_K>(s.up_type, s, ga, table, offs, tok, x, ldx, h, rest, st); break;
+                case kQ5_K: e = gate_up_for<kQ5_K>(s.up_type, s, ga, table, offs, tok, x, ldx, h, rest, st); break;
+                case kQ6_K: e = gate_up_for<kQ6_K>(s.up_type, s, ga, table, offs, tok, x, ldx, h, rest, st); break;
+                case kQ8_0: e = gate_up_for<kQ8_0>(s.up_type, s, ga, table, offs, tok, x, ldx, h, rest, st); break;
+                default: e = hipErrorInvalidValue;
+            }
+            if (e != hipSuccess) return e;
+            if ((e = hipGetLastError()) != hipSuccess) return e;
         }
-        if (e != hipSuccess) return e;
-        if ((e = hipGetLastError()) != hipSuccess) return e;
     }
-    if (mf_dn) {
-        if ((e = launch_prep_rows(offs, n_expert, nullptr, h, s.FF, s.FF, (int)P, hh, hl, nullptr, nullptr, hsc, st)) !=
-            hipSuccess)
-            return e;
-        if (wave_max > 0 && (e = launch_down_wave(s, table, n_expert, offs, hh, hl, hsc, yp, wave_max, st)) != hipSuccess)
-            return e;
-        if ((e = launch_down_mfma(s, table, n_expert, offs, nb, hh, hl, hsc, yp, wave_max + 1, st)) != hipSuccess)
-            return e;
-    } else {
-        const dim3 gd((unsigned)((s.D + 3) / 4), (unsigned)n_expert);
-        switch (s.down_type) {
-            case kQ4_K: grouped_down_kernel<kQ4_K><<<gd, 256, 0, st>>>(s, table, offs, h, yp); break;
-            case kQ5_K: grouped_down_kernel<kQ5_K><<<gd, 256, 0, st>>>(s, table, offs, h, yp); break;
-            case kQ6_K: grouped_down_kernel<kQ6_K><<<gd, 256, 0, st>>>(s, table, offs, h, yp); break;
-            case kQ8_0: grouped_down_kernel<kQ8_0><<<gd, 256, 0, st>>>(s, table, offs, h, yp); break;
-            default: return hipErrorInvalidValue;
+    if (dot && (e = launch_down_dot(s, table, n_expert, offs, dq, dsc, ds32, yp, 1, dmax, st)) != hipSuccess) return e;
+    if (nb >= rest) {
+        if (mf_dn) {
+            if ((e = launch_prep_rows(offs, n_expert, nullptr, h, s.FF, s.FF, (int)P, hh, hl, nullptr, nullptr, hsc,
+                                      st)) != hipSuccess)
+                return e;
+            if (wave_max >= rest &&
+                (e = launch_down_wave(s, table, n_expert, offs, hh, hl, hsc, yp, rest, wave_max, st)) != hipSuccess)
+                return e;
+            if (nb >= wg_min &&
+                (e = launch_down_mfma(s, table, n_expert, offs, nb, hh, hl, hsc, yp, wg_min, st)) != hipSuccess)
+                return e;
+        } else {
+            const dim3 gd((unsigned)((s.D + 3) / 4), (unsigned)n_expert);
+            switch (s.down_type) {
+                case kQ4_K: grouped_down_kernel<kQ4_K><<<gd, 256, 0, st>>>(s, table, offs, h, yp, rest); break;
+                case kQ5_K: grouped_down_kernel<kQ5_K><<<gd, 256, 0, st>>>(s, table, offs, h, yp, rest); break;
+                case kQ6_K: grouped_down_kernel<kQ6_K><<<gd, 256, 0, st>>>(s, table, offs, h, yp, rest); break;
+                case kQ8_0: grouped_down_kernel<kQ8_0><<<gd, 256, 0, st>>>(s, table, offs, h, yp, rest); break;
+                default: return hipErrorInvalidValue;
+            }
+            if ((e = hipGetLastError()) != hipSuccess) return e;
         }
-        if ((e = hipGetLastError()) != hipSuccess) return e;
     }
     const size_t nthr = (size_t)nb * (s.D / 4);
     grouped_combine_kernel<<<(unsigned)((nthr + 255) / 256), 256, 0, st>>>(ids, pos, pw, nb, k, s.D, yp, y, ldy);

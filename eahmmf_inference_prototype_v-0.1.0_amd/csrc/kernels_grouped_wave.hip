@@ -292,30 +292,31 @@ bool grouped_wave_down_ok(const MoeShape& s) { return grouped_mfma_down_ok(s); }
 
 hipError_t launch_gate_up_wave(const MoeShape& s, const ExpertEntry* table, int E, const int* offs, const _Float16* xh,
                                const _Float16* xl, const _Float16* xsh, const _Float16* xsl, const float* xscale,
-                               float* h, int tmax, hipStream_t st) {
+                               float* h, int tmin, int tmax, hipStream_t st) {
     const dim3 g((unsigned)((s.FF / 16 + kWaveWaves - 1) / kWaveWaves), (unsigned)E);
     const bool two = tmax > 16;
     if (s.gate_type == kQ4_K) {
         if (two)
-            gate_up_wave_kernel<kQ4_K, 2><<<g, kWaveWaves * 64, 0, st>>>(s, table, offs, xh, xl, xsh, xsl, xscale, h, 1, tmax);
+            gate_up_wave_kernel<kQ4_K, 2><<<g, kWaveWaves * 64, 0, st>>>(s, table, offs, xh, xl, xsh, xsl, xscale, h, tmin, tmax);
         else
-            gate_up_wave_kernel<kQ4_K, 1><<<g, kWaveWaves * 64, 0, st>>>(s, table, offs, xh, xl, xsh, xsl, xscale, h, 1, tmax);
+            gate_up_wave_kernel<kQ4_K, 1><<<g, kWaveWaves * 64, 0, st>>>(s, table, offs, xh, xl, xsh, xsl, xscale, h, tmin, tmax);
     } else {
         if (two)
-            gate_up_wave_kernel<kQ5_K, 2><<<g, kWaveWaves * 64, 0, st>>>(s, table, offs, xh, xl, xsh, xsl, xscale, h, 1, tmax);
+            gate_up_wave_kernel<kQ5_K, 2><<<g, kWaveWaves * 64, 0, st>>>(s, table, offs, xh, xl, xsh, xsl, xscale, h, tmin, tmax);
         else
-            gate_up_wave_kernel<kQ5_K, 1><<<g, kWaveWaves * 64, 0, st>>>(s, table, offs, xh, xl, xsh, xsl, xscale, h, 1, tmax);
+            gate_up_wave_kernel<kQ5_K, 1><<<g, kWaveWaves * 64, 0, st>>>(s, table, offs, xh, xl, xsh, xsl, xscale, h, tmin, tmax);
     }
     return hipGetLastError();
 }
 
 hipError_t launch_down_wave(const MoeShape& s, const ExpertEntry* table, int E, const int* offs, const _Float16* hh,
-                            const _Float16* hl, const float* hscale, float* yp, int tmax, hipStream_t st) {
+                            const _Float16* hl, const float* hscale, float* yp, int tmin, int tmax,
+                            hipStream_t st) {
     const dim3 g((unsigned)((s.D / 16 + kWaveWaves - 1) / kWaveWaves), (unsigned)E);
     if (tmax > 16)
-        down_wave_q6k_kernel<2><<<g, kWaveWaves * 64, 0, st>>>(s, table, offs, hh, hl, hscale, yp, 1, tmax);
+        down_wave_q6k_kernel<2><<<g, kWaveWaves * 64, 0, st>>>(s, table, offs, hh, hl, hscale, yp, tmin, tmax);
     else
-        down_wave_q6k_kernel<1><<<g, kWaveWaves * 64, 0, st>>>(s, table, offs, hh, hl, hscale, yp, 1, tmax);
+        down_wave_q6k_kernel<1><<<g, kWaveWaves * 64, 0, st>>>(s, table, offs, hh, hl, hscale, yp, tmin, tmax);
     return hipGetLastError();
 }
 

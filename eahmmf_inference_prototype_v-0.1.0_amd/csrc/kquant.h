@@ -80,10 +80,30 @@ __device__ __forceinline__ Bytes32A2 lds_ld32_a2(const uint8_t* p) {
 // How a weight row segment is read: straight from global memory, or from an
 // LDS copy that keeps the row's global alignment modulo 16 (16-byte loads
 // stay aligned; 2-byte-aligned 32-byte groups are realigned in registers).
+// GlobalLd reads through global-address-space pointers: a row pointer taken
+// from a table in memory is otherwise generic, and generic (flat) loads also
+// count against the LDS/scalar counter, so every wait for a scalar or LDS
+// operation would wait for the weight loads in flight as well.
+typedef uint32_t __attribute__((ext_vector_type(4))) u32x4_t;
+typedef uint32_t __attribute__((aligned(2))) u32_a2_t;
+__device__ __forceinline__ uint4 gld16(const uint8_t* p) {  // 16-byte aligned
+    const u32x4_t v = *(const __attribute__((address_space(1))) u32x4_t*)p;
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ Bytes32A2 gld32_a2(const uint8_t* p) {  // 2-byte aligned
+    const __attribute__((address_space(1))) u32_a2_t* q = (const __attribute__((address_space(1))) u32_a2_t*)p;
+    Bytes32A2 r;
+#pragma unroll
+    for (int i = 0; i < 8; i++) r.w[i] = q[i];
+    return r;
+}
+__device__ __forceinline__ uint16_t gld_u16(const uint8_t* p) {
+    return *(const __attribute__((address_space(1))) uint16_t*)p;
+}
 struct GlobalLd {
-    static __device__ __forceinline__ uint4 b16(const uint8_t* p) { return ld16(p); }
-    static __device__ __forceinline__ Bytes32A2 b32a2(const uint8_t* p) { return ld32_a2(p); }
-    static __device__ __forceinline__ uint16_t u16(const uint8_t* p) { return ld_u16(p); }
+    static __device__ __forceinline__ uint4 b16(const uint8_t* p) { return gld16(p); }
+    static __device__ __forceinline__ Bytes32A2 b32a2(const uint8_t* p) { return gld32_a2(p); }
+    static __device__ __forceinline__ uint16_t u16(const uint8_t* p) { return gld_u16(p); }
 };
 struct LdsLd {
     static __device__ __forceinline__ uint4 b16(const uint8_t* p) { return ld16(p); }
@@ -140,6 +160,28 @@ __device__ __forceinline__ void wait_vm_upto() {
     __atomic_signal_fence(__ATOMIC_SEQ_CST);
     __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
     __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+
+// s_waitcnt vmcnt(n) for a run-time n (0..15).
+__device__ __forceinline__ void wait_vm_n(int n) {
+    switch (n) {
+        case 0: wait_vm_upto<0>(); break;
+        case 1: wait_vm_upto<1>(); break;
+        case 2: wait_vm_upto<2>(); break;
+        case 3: wait_vm_upto<3>(); break;
+        case 4: wait_vm_upto<4>(); break;
+        case 5: wait_vm_upto<5>(); break;
+        case 6: wait_vm_upto<6>(); break;
+        case 7: wait_vm_upto<7>(); break;
+        case 8: wait_vm_upto<8>(); break;
+        case 9: wait_vm_upto<9>(); break;
+        case 10: wait_vm_upto<10>(); break;
+        case 11: wait_vm_upto<11>(); break;
+        case 12: wait_vm_upto<12>(); break;
+        case 13: wait_vm_upto<13>(); break;
+        case 14: wait_vm_upto<14>(); break;
+        default: wait_vm_upto<15>(); break;
+    }
 }
 
 // Exact half -> float.  Finite values and infinities convert exactly in

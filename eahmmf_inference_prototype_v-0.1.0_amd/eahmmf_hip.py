@@ -29,6 +29,7 @@ EXPORTS = (
     "eahmmf_hip_model_create", "eahmmf_hip_model_forward", "eahmmf_hip_model_eval", "eahmmf_hip_model_generate_greedy",
     "eahmmf_hip_model_set_trace", "eahmmf_hip_model_trace", "eahmmf_hip_model_trace_clear", "eahmmf_hip_model_stream",
     "eahmmf_hip_model_free", "eahmmf_hip_moe_layer_decode_xn_async", "eahmmf_hip_set_grouped_wave_max",
+    "eahmmf_hip_set_grouped_dot_max",
 )
 
 
@@ -121,6 +122,7 @@ def load(path=LIB_PATH):
         "eahmmf_hip_fused_exchange": (c_int, []),
         "eahmmf_hip_set_grouped_mfma": (c_int, [c_int]),
         "eahmmf_hip_set_grouped_wave_max": (c_int, [c_int]),
+        "eahmmf_hip_set_grouped_dot_max": (c_int, [c_int]),
         "eahmmf_hip_moe_grouped": (c_bool, [ctypes.POINTER(Expert), c_int, vp, vp, vp, c_int, vp, vp]),
         "eahmmf_hip_moe_grouped_async": (c_int, [ctypes.POINTER(MoeShape), vp, c_int, vp, vp, c_int, c_int, vp, vp,
                                                  vp]),

@@ -505,20 +505,29 @@ GROUPED_CASES = [
     ("q8_0_down_ne0_96", (Q8_0, Q8_0, Q8_0), 128, 96, 6, 2, 130),
     ("q5_k_gate_up_q6_k_down", (Q5_K, Q5_K, Q6_K), 1024, 512, 8, 4, 150),
     ("c5_shape", (Q4_K, Q4_K, Q6_K), 4096, 1536, 4, 2, 33),
+    ("c2_shape_small_groups", (Q4_K, Q4_K, Q6_K), 2048, 768, 64, 8, 48),
+    ("q8_0_d1024_small_groups", (Q8_0, Q8_0, Q8_0), 1024, 256, 32, 4, 40),
+    ("q6_k_gate_up_q4_k_down", (Q6_K, Q6_K, Q4_K), 1024, 512, 16, 4, 20),
 ]
 
 
-@pytest.fixture(params=[(1, 32), (1, 16), (1, 0), (0, 32)], ids=["mfma", "mfma_wave16", "mfma_wg", "valu"])
+@pytest.fixture(params=[(1, 32, 4), (1, 32, 0), (1, 16, 0), (1, 0, 0), (0, 32, 0), (0, 32, 4)],
+                ids=["dot_mfma", "mfma", "mfma_wave16", "mfma_wg", "valu", "dot_valu"])
 def grouped_mode(request, hip):
-    """Matrix-core or VALU grouped kernels; with the matrix cores, experts of
-    at most `wave_max` tokens go to the per-wave kernels (two 16-token tiles
-    above 16, one at or below), the rest to the workgroup kernels."""
-    mfma, wave_max = request.param
+    """Kernel paths of the grouped block: integer-dot kernels for small groups
+    (a block of at most 32 tokens entirely, else groups of at most dot_max
+    tokens) or not, then matrix-core or VALU kernels; with the matrix cores,
+    groups of at most `wave_max` tokens go to the per-wave kernels (two
+    16-token tiles above 16, one at or below), the rest to the workgroup
+    kernels."""
+    mfma, wave_max, dot_max = request.param
     prev = hip.eahmmf_hip_set_grouped_mfma(mfma)
     prev_w = hip.eahmmf_hip_set_grouped_wave_max(wave_max)
+    prev_d = hip.eahmmf_hip_set_grouped_dot_max(dot_max)
     yield request.param
     hip.eahmmf_hip_set_grouped_mfma(prev)
     hip.eahmmf_hip_set_grouped_wave_max(prev_w)
+    hip.eahmmf_hip_set_grouped_dot_max(prev_d)
 
 
 @pytest.mark.parametrize("name,types,D,FF,E,k,nb", GROUPED_CASES, ids=[c[0] for c in GROUPED_CASES])
@@ -584,6 +593,50 @@ def test_grouped_async_device_routing(torch_dev, binding, hip, grouped_mode, nb,
     assert hip.eahmmf_hip_moe_grouped_async(ctypes.byref(shape), ptr(dtable), E, ptr(dids), ptr(dw), nb, k, ptr(dx),
                                             ptr(dy), stream) == 0, hip.eahmmf_hip_last_error()
     torch.cuda.synchronize()
+    ids, w = oracle.route_topk(logits, k)
+    assert np.array_equal(dids.cpu().numpy(), ids)
+    close(dy.cpu().numpy(), oracle.moe_layer(layer, x, ids, w))
+
+
+@pytest.mark.parametrize("nb", [2, 16, 32])
+@pytest.mark.parametrize("fused", [0, 1], ids=["grouped", "default"])
+def test_decode_batch_c5_shape(torch_dev, binding, hip, nb, fused):
+    """A decode batch of nb sequences at the Qwen3-235B-A22B expert shape
+    (D=4096, FF=1536, 128 experts top-8, Q4_K gate/up, Q6_K down), routing on
+    the device from N(0,1) logits.  With the single-token kernel off the batch
+    runs as one grouped block on the integer-dot kernels (every routed
+    expert's rows streamed once for all of its tokens); by default the entry
+    point picks its path.  y of every token matches the oracle on the same ids
+    (qwen3moe.cpp:1009-1067)."""
+    torch = torch_dev
+    D, FF, E, k = 4096, 1536, 128, 8
+    types = (Q4_K, Q4_K, Q6_K)
+    rng = np.random.default_rng(1000 + nb)
+    n_unique = 6
+    uniq = make_layer(binding, types, D, FF, n_unique, rng)
+    layer = [uniq[e % n_unique] for e in range(E)]
+    dev_u = [[to_dev(torch, uniq[e][c][1]) for c in range(3)] for e in range(n_unique)]
+    table = np.array([[dev_u[e % n_unique][c].data_ptr() for c in range(3)] for e in range(E)], dtype=np.uint64)
+    dtable = to_dev(torch, table.view(np.int64))
+    shape = binding.MoeShape(Q4_K, Q4_K, Q6_K, D, FF, binding.row_bytes(Q4_K, D), binding.row_bytes(Q4_K, D),
+                             binding.row_bytes(Q6_K, FF))
+    logits = rng.normal(0, 1, (nb, E)).astype(np.float32)
+    x = rng.normal(0, 1, (nb, D)).astype(np.float32)
+    dl, dx = to_dev(torch, logits), to_dev(torch, x)
+    dids = torch.empty((nb, k), dtype=torch.int32, device="cuda")
+    dw = torch.empty((nb, k), dtype=torch.float32, device="cuda")
+    dy = torch.full((nb, D), float("nan"), device="cuda")
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    prev = hip.eahmmf_hip_set_fused(fused)
+    try:
+        print(f"decode batch nb={nb} fused={fused}", flush=True)
+        assert hip.eahmmf_hip_route_topk_async(ptr(dl), nb, E, k, ptr(dids), ptr(dw), stream) == 0
+        assert hip.eahmmf_hip_moe_grouped_async(ctypes.byref(shape), ptr(dtable), E, ptr(dids), ptr(dw), nb, k,
+                                                ptr(dx), ptr(dy), stream) == 0, hip.eahmmf_hip_last_error()
+        torch.cuda.synchronize()
+    finally:
+        hip.eahmmf_hip_set_fused(prev)
+    assert hip.eahmmf_hip_device_flags() == 0
     ids, w = oracle.route_topk(logits, k)
     assert np.array_equal(dids.cpu().numpy(), ids)
     close(dy.cpu().numpy(), oracle.moe_layer(layer, x, ids, w))
