@@ -156,62 +156,86 @@ def bench_c4(args, torch, b, hip):
 
 
 def bench_c5_batch(args, torch, b, hip):
-    """The 16-sequence ragged decode batch at the Qwen3-235B-A22B expert shape:
-    16 decode tokens (one per sequence) through one MoE layer per step, routing
-    on the device from fresh ~N(0,1) logits, then eahmmf_hip_moe_grouped_async
-    (which runs a batch this small as one single-launch block per token).  Also
-    timed: the same step with the grouped kernels forced (fused launches off),
-    matrix-core and vector-ALU."""
+    """Small decode batches at the Qwen3-235B-A22B expert shape (D=4096,
+    FF=1536, 128 experts top-8, Q4_K/Q6_K): nb decode tokens (one per
+    sequence) through one MoE layer per step, routing on the device from fresh
+    ~N(0,1) logits, then eahmmf_hip_moe_grouped_async (the headline: 16
+    sequences).  Also timed per batch size: the grouped block (each distinct
+    routed expert streamed once) and one single-token launch per token
+    (eahmmf_hip_moe_decode_routed_async), the two paths the entry point
+    chooses between."""
     D_, FF_, E_, K_, NB = 4096, 1536, 128, 8, 16
+    NBMAX = 32
     rng = np.random.default_rng(6)
     uniq, grb, drb = build_layer_replicated(b, rng, D_, FF_, E_, 16)
     R = args.replicas if args.replicas else 4
     comps, tables = upload_layers(torch, uniq, E_, R)
     shape = b.MoeShape(Q4_K, Q4_K, Q6_K, D_, FF_, grb, grb, drb)
     NS = 16
-    dl = torch.from_numpy(rng.normal(0, 1, (NS, NB, E_)).astype(np.float32)).cuda()
-    dx = torch.from_numpy(rng.normal(0, 1, (NS, NB, D_)).astype(np.float32)).cuda()
-    dids = torch.empty((NS, NB, K_), dtype=torch.int32, device="cuda")
-    dw = torch.empty((NS, NB, K_), dtype=torch.float32, device="cuda")
-    dy = torch.empty((NS, NB, D_), dtype=torch.float32, device="cuda")
+    dl = torch.from_numpy(rng.normal(0, 1, (NS, NBMAX, E_)).astype(np.float32)).cuda()
+    dx = torch.from_numpy(rng.normal(0, 1, (NS, NBMAX, D_)).astype(np.float32)).cuda()
+    dids = torch.empty((NS, NBMAX, K_), dtype=torch.int32, device="cuda")
+    dw = torch.empty((NS, NBMAX, K_), dtype=torch.float32, device="cuda")
+    dy = torch.empty((NS, NBMAX, D_), dtype=torch.float32, device="cuda")
     stream = torch.cuda.current_stream()
     sp, vp = ctypes.c_void_p(stream.cuda_stream), ctypes.c_void_p
-    for i in range(NS):
-        assert hip.eahmmf_hip_route_topk_async(vp(dl[i].data_ptr()), NB, E_, K_, vp(dids[i].data_ptr()),
-                                               vp(dw[i].data_ptr()), sp) == 0
-    torch.cuda.synchronize()
-    ids = dids.cpu().numpy()
     exp_bytes = 2 * FF_ * grb + D_ * drb
-    distinct = [len(np.unique(ids[i])) for i in range(NS)]
 
-    def step(i):  # routing + the batch's expert block, as a serving step runs it
-        s_ = i % NS
-        assert hip.eahmmf_hip_route_topk_async(vp(dl[s_].data_ptr()), NB, E_, K_, vp(dids[s_].data_ptr()),
+    def route(s_, nb):
+        assert hip.eahmmf_hip_route_topk_async(vp(dl[s_].data_ptr()), nb, E_, K_, vp(dids[s_].data_ptr()),
                                                vp(dw[s_].data_ptr()), sp) == 0
+
+    def step(i, nb):  # routing + the batch's expert block, as a serving step runs it
+        s_ = i % NS
+        route(s_, nb)
         rc = hip.eahmmf_hip_moe_grouped_async(ctypes.byref(shape), vp(tables[i % R].data_ptr()), E_,
-                                              vp(dids[s_].data_ptr()), vp(dw[s_].data_ptr()), NB, K_,
+                                              vp(dids[s_].data_ptr()), vp(dw[s_].data_ptr()), nb, K_,
                                               vp(dx[s_].data_ptr()), vp(dy[s_].data_ptr()), sp)
         assert rc == 0, b.last_error()
 
-    def timed(steps, warm):
+    def step_per_token(i, nb):  # routing + one single-token launch per token
+        s_ = i % NS
+        route(s_, nb)
+        for t in range(nb):
+            rc = hip.eahmmf_hip_moe_decode_routed_async(ctypes.byref(shape), vp(tables[i % R].data_ptr()), E_,
+                                                        vp(dids[s_, t].data_ptr()), vp(dw[s_, t].data_ptr()), K_,
+                                                        vp(dx[s_, t].data_ptr()), vp(dy[s_, t].data_ptr()), sp)
+            assert rc == 0, b.last_error()
+
+    def timed(fn, nb, steps, warm):
         for i in range(warm):
-            step(i)
+            fn(i, nb)
         torch.cuda.synchronize()
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         e0.record(stream)
         for i in range(steps):
-            step(i)
+            fn(i, nb)
         e1.record(stream)
         torch.cuda.synchronize()
         return e0.elapsed_time(e1) * 1e-3 / steps
 
+    for i in range(NS):
+        route(i, NBMAX)
+    torch.cuda.synchronize()
+    ids_all = dids.cpu().numpy()
+    distinct = [len(np.unique(ids_all[i, :NB])) for i in range(NS)]
     steps = args.steps if args.steps else 100
-    t_api = timed(steps, args.warmup if args.warmup else 5)
+    t_api = timed(step, NB, steps, args.warmup if args.warmup else 5)
     fused_prev = hip.eahmmf_hip_set_fused(0)
-    t_mfma = timed(max(10, steps // 4), 2)
+    t_grouped = timed(step, NB, max(10, steps // 4), 2)
     mfma_prev = hip.eahmmf_hip_set_grouped_mfma(0)
-    t_valu = timed(max(10, steps // 4), 2)
+    dot_prev = hip.eahmmf_hip_set_grouped_dot_max(0)
+    t_valu = timed(step, NB, max(10, steps // 4), 2)
+    hip.eahmmf_hip_set_grouped_dot_max(dot_prev)
     hip.eahmmf_hip_set_grouped_mfma(mfma_prev)
+    sweep = []
+    for nb in (1, 2, 4, 8, 16, 32):
+        hip.eahmmf_hip_set_fused(0)
+        tg = timed(step, nb, 20, 3)
+        hip.eahmmf_hip_set_fused(1)
+        tp = timed(step_per_token, nb, 20, 3)
+        sweep.append({"tokens": nb, "grouped_ms": round(tg * 1e3, 4), "per_token_launches_ms": round(tp * 1e3, 4),
+                      "distinct_experts_mean": round(float(np.mean([len(np.unique(ids_all[i, :nb])) for i in range(NS)])), 1)})
     hip.eahmmf_hip_set_fused(fused_prev)
     assert hip.eahmmf_hip_device_flags() == 0
     read_bytes = NB * K_ * exp_bytes  # each token's experts, read per token
@@ -224,14 +248,15 @@ def bench_c5_batch(args, torch, b, hip):
         "config": {"workload": "16 decode tokens (one per sequence) through one MoE layer, D=4096 FF=1536 "
                                "128 experts top-8, Q4_K gate/up + Q6_K down, routing on device, "
                                "eahmmf_hip_moe_grouped_async", "layer_replicas": R,
-                   "bytes_read_per_step": read_bytes, "distinct_experts_mean": round(float(np.mean(distinct)), 1),
+                   "bytes_read_if_per_token": read_bytes, "distinct_experts_mean": round(float(np.mean(distinct)), 1),
                    "distinct_expert_bytes_per_step": int(distinct_bytes)},
         "pct_of_hbm_peak": round(100 * gbs / HBM_PEAK_GBS, 2),
-        "bytes_read_GB_s": round(read_bytes / t_api / 1e9, 2),
         "expert_only_batch_tokens_per_s_94_layers": round(NB / (94 * t_api), 1),
-        "grouped_kernels_forced": {"matrix_core_ms": round(t_mfma * 1e3, 4), "vector_alu_ms": round(t_valu * 1e3, 4),
-                                   "what": "the same step with eahmmf_hip_set_fused(0) (grouping on the device, "
-                                           "each distinct expert read once)"}}), flush=True)
+        "grouped_block_ms": round(t_grouped * 1e3, 4), "grouped_vector_alu_only_ms": round(t_valu * 1e3, 4),
+        "batch_sweep": sweep,
+        "what": "ms per layer-step including routing; grouped = eahmmf_hip_moe_grouped_async with the single-token "
+                "kernel off (integer-dot kernels for every expert), per_token_launches = one single-launch "
+                "expert block per token (eahmmf_hip_moe_decode_routed_async)"}), flush=True)
 
 
 def bench_c5(args, torch, b, hip):

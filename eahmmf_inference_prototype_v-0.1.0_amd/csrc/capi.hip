@@ -49,8 +49,10 @@ struct DeviceBuf {
     size_t cap = 0;
 };
 
-// Largest batch eahmmf_hip_moe_grouped_async runs as per-token fused launches.
-constexpr int kFusedBatchMax = 32;
+// Largest batch eahmmf_hip_moe_grouped_async runs as per-token fused launches
+// (from 4 tokens the grouped block, which streams each distinct routed expert
+// once, is faster).
+constexpr int kFusedBatchMax = 3;
 
 // Bulk staging ring: kRingSlots pinned slots of kRingChunk bytes each.
 constexpr int kRingSlots = 4;
@@ -608,12 +610,13 @@ int eahmmf_hip_moe_grouped_async(const eahmmf_hip_moe_shape* shape, const eahmmf
                -1;
     DevCtx* c = ctx_for_current_device();
     if (!c) return -2;
-    // A decode batch of a few sequences runs as one fused launch per token
-    // (ids and weights as given): at one or two tokens per routed expert the
-    // grouped kernels' per-expert pipeline costs more than reading each
-    // token's experts on its own.  Measured for 1..32 tokens at D=2048/FF=768
-    // and D=4096/FF=1536 (top-8 of 128): per token 12.2 / 30.4 us each; at 32
-    // tokens 374 / 971 us against 433 / 1520 us for the grouped block.
+    // A decode batch of up to three sequences runs as one fused launch per
+    // token (ids and weights as given): the grouped block's fixed cost
+    // (grouping, activation levels, three more launches) outweighs the shared
+    // expert reads below four tokens.  Measured at D=4096/FF=1536, top-8 of
+    // 128, routing included: 1 / 2 / 4 / 8 / 16 / 32 tokens take 0.043 /
+    // 0.075 / 0.139 / 0.267 / 0.507 / 1.0 ms as per-token launches and
+    // 0.100 / 0.117 / 0.136 / 0.190 / 0.309 / 0.525 ms as the grouped block.
     if (nb <= kFusedBatchMax && fused_enabled() && fused_supported(s, k, 0)) {
         if (!grow_fused(c, s, k)) return -2;
         for (int t = 0; t < nb; t++) {

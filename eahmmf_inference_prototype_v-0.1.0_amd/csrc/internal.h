@@ -139,12 +139,15 @@ hipError_t launch_down_wave(const MoeShape& s, const ExpertEntry* table, int E, 
 // a negative argument only queries.  Returns the previous value.
 int set_grouped_wave_max(int tmax);
 // Integer-dot matmuls for experts holding tmin..tmax tokens, tmax <= 32
-// (kernels_grouped_dot.hip): gate/up from x rows to h's int8 levels
-// (hq [P][3][FF], hsc [P][3][FF/64], hs32 [P][FF/32]), down from those levels.
+// (kernels_grouped_dot.hip).  levels: rows of n values as int8 levels
+// (q [rows][3][n], sc [rows][3][n/64], s32 [rows][n/32]).  gate/up from the
+// tokens' x levels to h [P][FF] fp32, down from h's levels.
 bool grouped_dot_gate_up_ok(const MoeShape& s);
 bool grouped_dot_down_ok(const MoeShape& s);
+hipError_t launch_levels_rows(const float* src, int ld, int rows, int n, int8_t* q, float* sc, float* s32,
+                              hipStream_t st);
 hipError_t launch_gate_up_dot(const MoeShape& s, const ExpertEntry* table, int E, const int* offs, const int* tok,
-                              const float* x, int ldx, int8_t* hq, float* hsc, float* hs32, int tmin, int tmax,
+                              const int8_t* xq, const float* xsc, const float* xs32, float* h, int tmin, int tmax,
                               hipStream_t st);
 hipError_t launch_down_dot(const MoeShape& s, const ExpertEntry* table, int E, const int* offs, const int8_t* hq,
                            const float* hsc, const float* hs32, float* yp, int tmin, int tmax, hipStream_t st);

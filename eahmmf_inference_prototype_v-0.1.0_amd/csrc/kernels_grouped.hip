@@ -345,8 +345,9 @@ size_t grouped_scratch_bytes(const MoeShape& s, int nb, int k, int n_expert) {
                         al(P * s.FF * 4) + al(P * s.D * 4);
     // fp16 hi/lo activations and sub-block sums for the matrix-core path
     const size_t mf = 2 * al(P * s.D * 2) + 2 * al(P * (s.D / 32) * 2) + al(P * 4) + 2 * al(P * s.FF * 2) + al(P * 4);
-    // h as int8 levels (+ scales, 32-value sums) for the integer-dot path
-    const size_t dt = al(P * 3 * s.FF) + al(P * 3 * (s.FF / 64 + 1) * 4) + al(P * (s.FF / 32) * 4);
+    // x and h as int8 levels (+ scales, 32-value sums) for the integer-dot path
+    const size_t dt = al(P * 3 * s.FF) + al(P * 3 * (s.FF / 64 + 1) * 4) + al(P * (s.FF / 32) * 4) +
+                      al((size_t)nb * 3 * s.D) + al((size_t)nb * 3 * (s.D / 64 + 1) * 4) + al((size_t)nb * (s.D / 32) * 4);
     return base + mf + dt;
 }
 
@@ -380,7 +381,10 @@ hipError_t launch_moe_grouped(const MoeShape& s, const ExpertEntry* table, int n
     float* hsc = reinterpret_cast<float*>(b); b += al(P * 4);
     int8_t* dq = reinterpret_cast<int8_t*>(b); b += al(P * 3 * s.FF);
     float* dsc = reinterpret_cast<float*>(b); b += al(P * 3 * (s.FF / 64 + 1) * 4);
-    float* ds32 = reinterpret_cast<float*>(b);
+    float* ds32 = reinterpret_cast<float*>(b); b += al(P * (s.FF / 32) * 4);
+    int8_t* xq = reinterpret_cast<int8_t*>(b); b += al((size_t)nb * 3 * s.D);
+    float* xqs = reinterpret_cast<float*>(b); b += al((size_t)nb * 3 * (s.D / 64 + 1) * 4);
+    float* xq32 = reinterpret_cast<float*>(b);
     const bool mf_gu = g_grouped_mfma && grouped_mfma_gate_up_ok(s);
     const bool mf_dn = g_grouped_mfma && grouped_mfma_down_ok(s);
     // Group sizes by path: 1..dmax the integer-dot kernels, then the per-wave
@@ -397,7 +401,8 @@ hipError_t launch_moe_grouped(const MoeShape& s, const ExpertEntry* table, int n
     group_pairs_kernel<<<1, kGroupThreads, lds, st>>>(ids, w, nb, k, n_expert, cnt, offs, tok, pw, pos);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    if (dot && (e = launch_gate_up_dot(s, table, n_expert, offs, tok, x, ldx, dq, dsc, ds32, 1, dmax, st)) != hipSuccess)
+    if (dot && ((e = launch_levels_rows(x, ldx, nb, s.D, xq, xqs, xq32, st)) != hipSuccess ||
+                (e = launch_gate_up_dot(s, table, n_expert, offs, tok, xq, xqs, xq32, h, 1, dmax, st)) != hipSuccess))
         return e;
     if (nb >= rest) {
         if (mf_gu) {
@@ -423,7 +428,9 @@ hipError_t launch_moe_grouped(const MoeShape& s, const ExpertEntry* table, int n
             if ((e = hipGetLastError()) != hipSuccess) return e;
         }
     }
-    if (dot && (e = launch_down_dot(s, table, n_expert, offs, dq, dsc, ds32, yp, 1, dmax, st)) != hipSuccess) return e;
+    if (dot && ((e = launch_levels_rows(h, s.FF, (int)P, s.FF, dq, dsc, ds32, st)) != hipSuccess ||
+                (e = launch_down_dot(s, table, n_expert, offs, dq, dsc, ds32, yp, 1, dmax, st)) != hipSuccess))
+        return e;
     if (nb >= rest) {
         if (mf_dn) {
             if ((e = launch_prep_rows(offs, n_expert, nullptr, h, s.FF, s.FF, (int)P, hh, hl, nullptr, nullptr, hsc,

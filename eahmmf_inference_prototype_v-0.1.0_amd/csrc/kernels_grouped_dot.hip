@@ -12,73 +12,35 @@
 // codes are exact small integers, so the only rounding is in the fp32 scale
 // products.
 //
-//   gate/up  one workgroup per (expert, 64 FF rows) and the expert's n
-//            tokens: the work is n x 64 rows of gate and up, split into units
-//            (token, row part) - 4/n parts per token when n <= 4, else one -
-//            and unit u is taken by wave u % 4.  A lane owns one 64-value
-//            segment of the unit's token (its levels in registers, formed by
-//            the lane itself from x); a row is G = D/64 lanes, 64/G rows per
-//            step, gate and up rows of the same row back to back.  The
-//            workgroup's 64 values of h = silu(g) * u are one 64-value
-//            segment of h per token, turned into levels in the workgroup and
-//            stored as such.
-//   down     one workgroup per (expert, 64 D rows), the same split; a lane
-//            owns one segment of the token's h levels (loaded as stored), a
-//            row is G' = the power of two >= FF/64 lanes.
-// Weight bytes are loaded straight into registers kDotAhead steps ahead of
-// their dot; a row read by several tokens' waves of a workgroup is served
-// from the CU's cache after the first.
+//   levels   levels_rows_kernel: each token's x as int8 levels, once.
+//   gate/up  one wave per (expert, 16 FF rows, pair of the expert's tokens):
+//            the pair's levels in registers, a lane holding one 64-value
+//            segment of each; a row is G = D/64 lanes, 64/G rows per step,
+//            gate and up rows of the same rows in alternate steps; every
+//            decoded segment is dotted against both tokens.  h = silu(g) * u
+//            is stored in fp32, then turned into levels (levels_rows_kernel).
+//   down     one wave per (expert, 64 D rows, pair of tokens) from h's
+//            levels, a row is G' = the power of two >= FF/64 lanes.
+// Work items this small keep the launch balanced: a wave streams about
+// 4 GB/s when the whole chip streams, so an item's time is set by its bytes,
+// and the last items to start end soon after the rest.
+// Weight bytes: a step's rows (64 segments' worth, contiguous in memory) are
+// copied by the wave with LDS DMA (16-byte global_load_lds, coalesced) into
+// the next of its kDotSlots LDS slots, kDotSlots - 1 steps ahead of their
+// dot; each wait is an explicit vmcnt over the wave's own copies, so nothing
+// the compiler schedules drains the copies in flight.  A row read by several
+// tokens' waves of a workgroup is served from the CU's cache after the first.
 #include "internal.h"
 #include "kquant_seg64.h"
 
 namespace eahmmf {
 
-constexpr int kDotRows = 64;      // output rows per workgroup (one 64-value h segment for gate/up)
-constexpr int kDotAhead = 3;      // steps of weight bytes in flight ahead of the dot (ring of 4)
+constexpr int kDotRows = 64;      // down rows per workgroup
+constexpr int kGuRowsDot = 16;    // gate/up rows per workgroup
+constexpr int kDotSlots = 4;      // LDS slots per gate/up wave: kDotSlots - 1 steps' bytes in flight
+constexpr int kDownSlots = 4;     // the same for a down wave
+constexpr int kDotMaxNI = 5;      // 1 KB DMA instructions per step (a step holds at most 4352 bytes)
 constexpr int kDotMaxTok = 32;    // tokens an expert may hold on this path
-
-// Levels of the 64 values at v (16-byte aligned), formed by one lane alone:
-// the same three-level scheme as quantize8.
-__device__ __forceinline__ void lane_levels(const float* v, XSeg& xs) {
-    float r[64];
-#pragma unroll
-    for (int i = 0; i < 16; i++) {
-        const float4 a = reinterpret_cast<const float4*>(v)[i];
-        r[4 * i] = a.x;
-        r[4 * i + 1] = a.y;
-        r[4 * i + 2] = a.z;
-        r[4 * i + 3] = a.w;
-    }
-    float amax = 0.f, s0 = 0.f, s1 = 0.f;
-#pragma unroll
-    for (int i = 0; i < 64; i++) {
-        amax = fmaxf(amax, fabsf(r[i]));
-        if (i < 32) s0 += r[i]; else s1 += r[i];
-    }
-    xs.sum32[0] = s0;
-    xs.sum32[1] = s1;
-    const float l1 = amax * (1.0f / 127.0f);
-    const float l2 = l1 * (1.0f / 254.0f), l3 = l2 * (1.0f / 254.0f);
-    const float lsc[kLevels] = {l1, l2, l3};
-#pragma unroll
-    for (int lv = 0; lv < kLevels; lv++) {
-        const float inv = lsc[lv] > 0.f ? __builtin_amdgcn_rcpf(lsc[lv]) : 0.f;
-#pragma unroll
-        for (int d = 0; d < 16; d++) {
-            uint32_t packed = 0u;
-#pragma unroll
-            for (int b = 0; b < 4; b++) {
-                const int i = 4 * d + b;
-                float qf = __builtin_rintf(r[i] * inv);
-                qf = fminf(127.f, fmaxf(-127.f, qf));
-                r[i] = __builtin_fmaf(-qf, lsc[lv], r[i]);
-                packed |= ((uint32_t)(int)qf & 0xFFu) << (8 * b);
-            }
-            xs.q[lv][d] = (int32_t)packed;
-        }
-        xs.s[lv] = lsc[lv];
-    }
-}
 
 // Stored levels of one 64-value segment (rows of n values: level lv at
 // q + lv*n, scales sc[lv*(n/64) + seg], sums s32[2*seg], s32[2*seg+1]).
@@ -104,118 +66,206 @@ __device__ __forceinline__ void load_levels(const int8_t* q, const float* sc, co
 // The units of a workgroup: n tokens x parts, parts = 4 / n for n <= 4.
 __device__ __forceinline__ int dot_parts(int n) { return n >= 4 ? 1 : (n == 3 ? 1 : 4 / n); }
 
-// gate/up of expert blockIdx.y, FF rows [64*blockIdx.x, +64), for the
-// expert's tokens (groups of tmin..tmax tokens; others leave at once).  x
-// [nb][ldx] fp32 rows, tok[p] the token at group position p.  Output: the
-// levels of h segment blockIdx.x of every position p of the group,
-// hq [P][3][FF] int8, hsc [P][3][FF/64], hs32 [P][FF/32].
-template <int T, int G>
-__global__ __launch_bounds__(256) void gate_up_dot_kernel(MoeShape s, const ExpertEntry* __restrict__ table,
-                                                          const int* __restrict__ offs, const int* __restrict__ tok,
-                                                          const float* __restrict__ x, int ldx,
-                                                          int8_t* __restrict__ hq, float* __restrict__ hsc,
-                                                          float* __restrict__ hs32, int tmin, int tmax) {
-    constexpr int RPS = 64 / G;  // rows per step
-    __shared__ float hb[kDotMaxTok][kDotRows];
-    const int e = blockIdx.y;
-    const int p0 = offs[e], n = offs[e + 1] - p0;
-    if (n <= 0 || n < tmin || n > tmax) return;
-    const int wave = threadIdx.x >> 6, l = threadIdx.x & 63;
-    const int parts = dot_parts(n), units = n * parts, rows_u = kDotRows / parts;
-    const int seg = l % G, sub = l / G;
-    const int c0 = blockIdx.x * kDotRows;
-    const ExpertEntry ent = table[e];
-    for (int u = wave; u < units; u += 4) {
-        const int t = u / parts, r0 = c0 + (u % parts) * rows_u;
-        XSeg xs;
-        lane_levels(x + (size_t)tok[p0 + t] * ldx + seg * 64, xs);
-        // step j: row r0 + (j >> 1) * RPS + sub of gate (j even) or up (j odd)
-        const int nsteps = 2 * rows_u / RPS;  // a multiple of 4 (rows_u >= 16, RPS <= 4)
-        auto rowp = [&](int j) -> const uint8_t* {
-            const int r = r0 + (j >> 1) * RPS + sub;
-            return (j & 1) ? ent.up + (size_t)r * s.up_rb : ent.gate + (size_t)r * s.gate_rb;
-        };
-        // Every step issues its load (the last steps reload the last row): a
-        // load skipped on some path leaves the compiler unable to count the
-        // loads issued after a ring slot's, and it then waits for all of them.
-        RawSeg<T> ring[kDotAhead + 1];
-#pragma unroll
-        for (int a = 0; a < kDotAhead; a++) ring[a].load(rowp(a), seg);
-        float gv = 0.f;
-        for (int j0 = 0; j0 < nsteps; j0 += kDotAhead + 1) {
-#pragma unroll
-            for (int v = 0; v <= kDotAhead; v++) {
-                const int j = j0 + v;
-                ring[(v + kDotAhead) % (kDotAhead + 1)].load(rowp(min(j + kDotAhead, nsteps - 1)), seg);
-                const float d = group_sum<G>(ring[v].decode(seg).dot(xs));
-                if (v & 1) {
-                    if (seg == G - 1) hb[t][r0 - c0 + (j >> 1) * RPS + sub] = gv / (1.0f + expf(-gv)) * d;
-                } else {
-                    gv = d;
-                }
-            }
-        }
-    }
-    __syncthreads();
-    // levels of h segment blockIdx.x for every token: eight lanes per token
-    const int FF = s.FF;
-    for (int t0 = wave * 8; t0 < n; t0 += 32) {
-        const int t = t0 + (l >> 3), part = l & 7;
-        const bool act = t < n;
+// Levels of nb rows of n values (n % 64 == 0): row r of src (stride ld)
+// -> q [nb][3][n], sc [nb][3][n/64], s32 [nb][n/32].  One workgroup per row,
+// eight threads per 64-value segment.
+__global__ __launch_bounds__(256) void levels_rows_kernel(const float* __restrict__ src, int ld, int n,
+                                                          int8_t* __restrict__ q, float* __restrict__ sc,
+                                                          float* __restrict__ s32) {
+    const int r = blockIdx.x, nseg = n / 64;
+    const float* row = src + (size_t)r * ld;
+    for (int base = 0; base < nseg; base += 32) {
+        const int seg = base + (int)threadIdx.x / 8, part = threadIdx.x % 8;
+        const bool act = seg < nseg;
         float v[8];
+        if (act) {
+            const float4 a = *reinterpret_cast<const float4*>(row + seg * 64 + part * 8);
+            const float4 c = *reinterpret_cast<const float4*>(row + seg * 64 + part * 8 + 4);
+            v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w; v[4] = c.x; v[5] = c.y; v[6] = c.z; v[7] = c.w;
+        } else {
 #pragma unroll
-        for (int i = 0; i < 8; i++) v[i] = act ? hb[t][8 * part + i] : 0.f;
-        const size_t p = (size_t)p0 + (act ? t : 0);
-        quantize8(v, blockIdx.x, part, act, hq + p * 3 * FF, FF, hsc + p * 3 * (FF / 64), FF / 64,
-                  hs32 + p * (FF / 32));
+            for (int i = 0; i < 8; i++) v[i] = 0.f;
+        }
+        quantize8(v, seg, part, act, q + (size_t)r * 3 * n, n, sc + (size_t)r * 3 * nseg, nseg, s32 + (size_t)r * (n / 32));
     }
 }
 
-// down of expert blockIdx.y, D rows [64*blockIdx.x, +64): yp[p][r] =
-// down_r . h[p] for the group's positions p, from h's stored levels.
-template <int T, int G>
-__global__ __launch_bounds__(256) void down_dot_kernel(MoeShape s, const ExpertEntry* __restrict__ table,
-                                                       const int* __restrict__ offs, const int8_t* __restrict__ hq,
-                                                       const float* __restrict__ hsc, const float* __restrict__ hs32,
-                                                       float* __restrict__ yp, int tmin, int tmax) {
-    constexpr int RPS = 64 / G;
+// The levels just loaded stay put: complete their loads here rather than at
+// their first use in a step loop (where the compiler's wait would recur every
+// step and drain the copies in flight).
+__device__ __forceinline__ void pin_levels(XSeg& xs) {
+#pragma unroll
+    for (int lv = 0; lv < kLevels; lv++) {
+#pragma unroll
+        for (int i = 0; i < 16; i++) pin(xs.q[lv][i]);
+        pin(xs.s[lv]);
+    }
+    pin(xs.sum32[0]);
+    pin(xs.sum32[1]);
+}
+
+// DMA of one step's bytes [src, src + bytes) into an LDS slot: NI
+// instructions of 64 lanes x 16 bytes from src rounded down to 16 (the slot
+// holds the bytes at offset src & 15; chunks past the end repeat the last).
+template <int NI>
+__device__ __forceinline__ void issue_step(const uint8_t* src, int bytes, uint8_t* slot, int lane) {
+    const uintptr_t a = (uintptr_t)src, base = a & ~(uintptr_t)15;
+    const int nc = (int)((a + (uintptr_t)bytes + 15 - base) / 16);
+#pragma unroll
+    for (int i = 0; i < NI; i++) lds_dma16(base + (uintptr_t)min(i * 64 + lane, nc - 1) * 16, slot + i * 1024);
+}
+
+// Wait for step j's copies: S - 1 later steps are in flight except
+// at the end of a unit (run-time count there).
+template <int NI, int S>
+__device__ __forceinline__ void wait_step(int j, int nsteps) {
+    if (j + S - 1 < nsteps)
+        wait_vm_upto<NI * (S - 1)>();
+    else
+        wait_vm_n(NI * (nsteps - 1 - j));
+}
+
+// A wave's tokens are taken two at a time (a pass): the two tokens' levels
+// sit in registers and every decoded segment is dotted against both.
+struct XPair {
+    XSeg a, b;
+};
+
+__device__ __forceinline__ void load_pair(const int8_t* q, const float* sc, const float* s32, size_t ra, size_t rb,
+                                          int n, int seg, bool two, XPair& x) {
+    load_levels(q + ra * 3 * n, sc + ra * 3 * (n / 64), s32 + ra * (n / 32), n, seg, x.a);
+    if (two) load_levels(q + rb * 3 * n, sc + rb * 3 * (n / 64), s32 + rb * (n / 32), n, seg, x.b);
+    pin_levels(x.a);
+    pin_levels(x.b);
+}
+
+// gate/up of expert blockIdx.y, FF rows [kGuRowsDot*blockIdx.x, +kGuRowsDot),
+// for tokens 2*blockIdx.z and 2*blockIdx.z + 1 of the expert's group (groups
+// of tmin..tmax tokens; other workgroups leave at once), from the tokens'
+// activation levels (xq/xsc/xs32, levels_rows_kernel over x): h [P][FF]
+// fp32.  One wave; dynamic LDS: kDotSlots slots of NI KB.
+template <int T, int G, int NI>
+__global__ __launch_bounds__(64) void gate_up_dot_kernel(MoeShape s, const ExpertEntry* __restrict__ table,
+                                                         const int* __restrict__ offs, const int* __restrict__ tok,
+                                                         const int8_t* __restrict__ xq, const float* __restrict__ xsc,
+                                                         const float* __restrict__ xs32, float* __restrict__ h,
+                                                         int tmin, int tmax) {
+    constexpr int RPS = 64 / G;  // rows per step
+    constexpr int SLOT = NI * 1024;
+    constexpr int NSTEPS = 2 * kGuRowsDot / RPS;  // gate and up steps of the rows: a multiple of 4
+    extern __shared__ __align__(16) uint8_t ring[];
+    __shared__ float hb[2][kGuRowsDot];
     const int e = blockIdx.y;
     const int p0 = offs[e], n = offs[e + 1] - p0;
-    if (n <= 0 || n < tmin || n > tmax) return;
-    const int wave = threadIdx.x >> 6, l = threadIdx.x & 63;
-    const int parts = dot_parts(n), units = n * parts, rows_u = kDotRows / parts;
-    const int FF = s.FF, nseg = FF / 64;
+    const int t0 = 2 * (int)blockIdx.z;
+    if (n <= 0 || n < tmin || n > tmax || t0 >= n) return;
+    const bool two = t0 + 1 < n;  // wave-uniform
+    const int l = threadIdx.x;
     const int seg = l % G, sub = l / G;
-    const bool on = seg < nseg;
-    const int c0 = blockIdx.x * kDotRows;
-    const uint8_t* dbase = table[e].down;
-    for (int u = wave; u < units; u += 4) {
-        const int t = u / parts, r0 = c0 + (u % parts) * rows_u;
-        const size_t p = (size_t)p0 + t;
-        XSeg xs = {};
-        if (on) load_levels(hq + p * 3 * FF, hsc + p * 3 * nseg, hs32 + p * (FF / 32), FF, seg, xs);
-        const int nsteps = rows_u / RPS;  // >= 1
-        // unconditional loads (see gate_up_dot_kernel); lanes past the row's
-        // segments read segment 0 and contribute 0
-        const int lseg = on ? seg : 0;
-        auto rowp = [&](int j) -> const uint8_t* {
-            return dbase + (size_t)(r0 + min(j, nsteps - 1) * RPS + sub) * s.down_rb;
-        };
-        RawSeg<T> ring[kDotAhead + 1];
+    const int D = s.D, FF = s.FF, c0 = blockIdx.x * kGuRowsDot;
+    const ExpertEntry ent = table[e];
+    const int rb = s.gate_rb, bytes = RPS * rb;  // gate and up share type and shape
+    // the matrix of a step by integer arithmetic: a select between the two
+    // pointers is lowered to an indexed load from a scratch copy of the
+    // entry, and its wait would drain the copies in flight
+    const uintptr_t gate = (uintptr_t)ent.gate, up_minus_gate = (uintptr_t)ent.up - gate;
+    // step j: rows c0 + (j >> 1) * RPS .. + RPS - 1 of gate (j even) or up (j odd)
+    auto stepsrc = [&](int j) -> const uint8_t* {
+        return (const uint8_t*)(gate + ((j & 1) ? up_minus_gate : (uintptr_t)0) +
+                                (uintptr_t)(c0 + (j >> 1) * RPS) * (uintptr_t)rb);
+    };
 #pragma unroll
-        for (int a = 0; a < kDotAhead; a++) ring[a].load(rowp(a), lseg);
-        for (int j0 = 0; j0 < nsteps; j0 += kDotAhead + 1) {
+    for (int j = 0; j < kDotSlots - 1; j++) issue_step<NI>(stepsrc(j), bytes, ring + j * SLOT, l);
+    XPair x;
+    load_pair(xq, xsc, xs32, (size_t)tok[p0 + t0], (size_t)tok[p0 + (two ? t0 + 1 : t0)], D, seg, two, x);
+    float ga = 0.f, gb = 0.f;
+    for (int j0 = 0; j0 < NSTEPS; j0 += kDotSlots) {
 #pragma unroll
-            for (int v = 0; v <= kDotAhead; v++) {
-                const int j = j0 + v;
-                if (j >= nsteps) break;
-                ring[(v + kDotAhead) % (kDotAhead + 1)].load(rowp(j + kDotAhead), lseg);
-                const float dd = ring[v].decode(lseg).dot(xs);
-                const float d = group_sum<G>(on ? dd : 0.f);
-                if (seg == G - 1) yp[p * s.D + r0 + j * RPS + sub] = d;
+        for (int v = 0; v < kDotSlots; v++) {
+            const int j = j0 + v;
+            if (j + kDotSlots - 1 < NSTEPS)
+                issue_step<NI>(stepsrc(j + kDotSlots - 1), bytes, ring + ((v + kDotSlots - 1) % kDotSlots) * SLOT, l);
+            wait_step<NI, kDotSlots>(j, NSTEPS);
+            RawSeg<T> raw;
+            raw.template load<LdsLd>(ring + v * SLOT + ((uintptr_t)stepsrc(j) & 15) + sub * rb, seg);
+            const SegCodes<T> c = raw.decode(seg);
+            const float da = group_sum<G>(c.dot(x.a));
+            const float db = two ? group_sum<G>(c.dot(x.b)) : 0.f;
+            const int row = (j >> 1) * RPS + sub;
+            if (v & 1) {
+                if (seg == G - 1) {
+                    hb[0][row] = ga / (1.0f + expf(-ga)) * da;
+                    hb[1][row] = gb / (1.0f + expf(-gb)) * db;
+                }
+            } else {
+                ga = da;
+                gb = db;
             }
         }
     }
+    if (l < kGuRowsDot) {
+        h[(size_t)(p0 + t0) * FF + c0 + l] = hb[0][l];
+        if (two) h[(size_t)(p0 + t0 + 1) * FF + c0 + l] = hb[1][l];
+    }
+}
+
+// down of expert blockIdx.y, D rows [64*blockIdx.x, +64), for tokens
+// 2*blockIdx.z and 2*blockIdx.z + 1 of the group: yp[p][r] = down_r . h[p]
+// from h's levels.  One wave.  The outputs are gathered in LDS and stored at
+// the end (a global store inside the step loop would count against the
+// copies' vmcnt).
+template <int T, int G, int NI>
+__global__ __launch_bounds__(64) void down_dot_kernel(MoeShape s, const ExpertEntry* __restrict__ table,
+                                                      const int* __restrict__ offs, const int8_t* __restrict__ hq,
+                                                      const float* __restrict__ hsc, const float* __restrict__ hs32,
+                                                      float* __restrict__ yp, int tmin, int tmax) {
+    constexpr int RPS = 64 / G;
+    constexpr int SLOT = NI * 1024;
+    constexpr int NSTEPS = kDotRows / RPS;
+    extern __shared__ __align__(16) uint8_t ring[];
+    __shared__ float yb[2][kDotRows];
+    const int e = blockIdx.y;
+    const int p0 = offs[e], n = offs[e + 1] - p0;
+    const int t0 = 2 * (int)blockIdx.z;
+    if (n <= 0 || n < tmin || n > tmax || t0 >= n) return;
+    const bool two = t0 + 1 < n;
+    const int l = threadIdx.x;
+    const int FF = s.FF, nseg = FF / 64;
+    const int seg = l % G, sub = l / G;
+    const bool on = seg < nseg;
+    const int lseg = on ? seg : 0;  // lanes past the row's segments read segment 0 and contribute 0
+    const int c0 = blockIdx.x * kDotRows;
+    const uint8_t* dbase = table[e].down;
+    const int rb = s.down_rb, bytes = RPS * rb;
+    auto stepsrc = [&](int j) -> const uint8_t* { return dbase + (size_t)(c0 + j * RPS) * rb; };
+#pragma unroll
+    for (int j = 0; j < kDownSlots - 1 && j < NSTEPS; j++) issue_step<NI>(stepsrc(j), bytes, ring + j * SLOT, l);
+    const size_t pa = (size_t)p0 + t0, pb = (size_t)p0 + (two ? t0 + 1 : t0);
+    XPair x = {};
+    if (on) load_pair(hq, hsc, hs32, pa, pb, FF, seg, two, x);
+    pin_levels(x.a);
+    pin_levels(x.b);
+    for (int j0 = 0; j0 < NSTEPS; j0 += kDownSlots) {
+#pragma unroll
+        for (int v = 0; v < kDownSlots; v++) {
+            const int j = j0 + v;
+            if (j >= NSTEPS) break;
+            if (j + kDownSlots - 1 < NSTEPS)
+                issue_step<NI>(stepsrc(j + kDownSlots - 1), bytes, ring + ((v + kDownSlots - 1) % kDownSlots) * SLOT, l);
+            wait_step<NI, kDownSlots>(j, NSTEPS);
+            RawSeg<T> raw;
+            raw.template load<LdsLd>(ring + v * SLOT + ((uintptr_t)stepsrc(j) & 15) + sub * rb, lseg);
+            const SegCodes<T> c = raw.decode(lseg);
+            const float da = group_sum<G>(on ? c.dot(x.a) : 0.f);
+            const float db = two ? group_sum<G>(on ? c.dot(x.b) : 0.f) : 0.f;
+            if (seg == G - 1) {
+                yb[0][j * RPS + sub] = da;
+                yb[1][j * RPS + sub] = db;
+            }
+        }
+    }
+    yp[pa * s.D + c0 + l] = yb[0][l];
+    if (two) yp[pb * s.D + c0 + l] = yb[1][l];
 }
 
 // ---------------------------------------------------------------------------
@@ -235,18 +285,45 @@ bool grouped_dot_gate_up_ok(const MoeShape& s) {
 
 bool grouped_dot_down_ok(const MoeShape& s) {
     const bool fmt = s.down_type == kQ4_K || s.down_type == kQ5_K || s.down_type == kQ6_K || s.down_type == kQ8_0;
-    return fmt && s.FF % 64 == 0 && s.FF / 64 <= 64 && s.FF / 64 >= 4 && s.D % kDotRows == 0;
+    return fmt && s.FF % 64 == 0 && s.FF / 64 <= 64 && s.FF / 64 >= 5 && s.D % kDotRows == 0;
 }
+
+// 1 KB DMA instructions for a step of `bytes` bytes starting anywhere in a
+// 16-byte chunk, plus the 2 bytes a realigned LDS read may touch past them.
+static int step_ni(int bytes) { return (15 + bytes + 2 + 1023) / 1024; }
+
+// gate/up: a step is always 64 segments (16 super-blocks or 64 Q8_0 blocks)
+template <int T> constexpr int gu_ni() { return T == kQ4_K || T == kQ5_K ? 3 : (T == kQ6_K ? 4 : 5); }
 
 template <int T>
 static hipError_t gate_up_dot_g(const MoeShape& s, dim3 g, const ExpertEntry* table, const int* offs, const int* tok,
-                                const float* x, int ldx, int8_t* hq, float* hsc, float* hs32, int tmin, int tmax,
+                                const int8_t* xq, const float* xsc, const float* xs32, float* h, int tmin, int tmax,
                                 hipStream_t st) {
-    switch (s.D / 64) {
-        case 16: gate_up_dot_kernel<T, 16><<<g, 256, 0, st>>>(s, table, offs, tok, x, ldx, hq, hsc, hs32, tmin, tmax); break;
-        case 32: gate_up_dot_kernel<T, 32><<<g, 256, 0, st>>>(s, table, offs, tok, x, ldx, hq, hsc, hs32, tmin, tmax); break;
-        case 64: gate_up_dot_kernel<T, 64><<<g, 256, 0, st>>>(s, table, offs, tok, x, ldx, hq, hsc, hs32, tmin, tmax); break;
+    constexpr int NI = gu_ni<T>();
+    const int G = s.D / 64;
+    if (step_ni(64 / G * s.gate_rb) > NI) return hipErrorInvalidValue;
+    const size_t lds = (size_t)kDotSlots * NI * 1024;
+    switch (G) {
+        case 16: gate_up_dot_kernel<T, 16, NI><<<g, 64, lds, st>>>(s, table, offs, tok, xq, xsc, xs32, h, tmin, tmax); break;
+        case 32: gate_up_dot_kernel<T, 32, NI><<<g, 64, lds, st>>>(s, table, offs, tok, xq, xsc, xs32, h, tmin, tmax); break;
+        case 64: gate_up_dot_kernel<T, 64, NI><<<g, 64, lds, st>>>(s, table, offs, tok, xq, xsc, xs32, h, tmin, tmax); break;
         default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+// down: a step is RPS rows of FF/64 segments, 3/4 .. 1 of 64 segments' bytes;
+// copies sized for 3 KB when that suffices, else the format's 64-segment size
+template <int T, int G>
+static hipError_t down_dot_gn(const MoeShape& s, dim3 g, const ExpertEntry* table, const int* offs, const int8_t* hq,
+                              const float* hsc, const float* hs32, float* yp, int tmin, int tmax, hipStream_t st) {
+    constexpr int NIMAX = gu_ni<T>();
+    const int ni = step_ni(64 / G * s.down_rb);
+    if (ni > NIMAX) return hipErrorInvalidValue;
+    if (ni <= 3) {
+        down_dot_kernel<T, G, 3><<<g, 64, (size_t)kDownSlots * 3 * 1024, st>>>(s, table, offs, hq, hsc, hs32, yp, tmin, tmax);
+    } else {
+        down_dot_kernel<T, G, NIMAX><<<g, 64, (size_t)kDownSlots * NIMAX * 1024, st>>>(s, table, offs, hq, hsc, hs32, yp, tmin, tmax);
     }
     return hipGetLastError();
 }
@@ -255,34 +332,39 @@ template <int T>
 static hipError_t down_dot_g(const MoeShape& s, dim3 g, const ExpertEntry* table, const int* offs, const int8_t* hq,
                              const float* hsc, const float* hs32, float* yp, int tmin, int tmax, hipStream_t st) {
     switch (pow2_at_least(s.FF / 64)) {
-        case 4: down_dot_kernel<T, 4><<<g, 256, 0, st>>>(s, table, offs, hq, hsc, hs32, yp, tmin, tmax); break;
-        case 8: down_dot_kernel<T, 8><<<g, 256, 0, st>>>(s, table, offs, hq, hsc, hs32, yp, tmin, tmax); break;
-        case 16: down_dot_kernel<T, 16><<<g, 256, 0, st>>>(s, table, offs, hq, hsc, hs32, yp, tmin, tmax); break;
-        case 32: down_dot_kernel<T, 32><<<g, 256, 0, st>>>(s, table, offs, hq, hsc, hs32, yp, tmin, tmax); break;
-        case 64: down_dot_kernel<T, 64><<<g, 256, 0, st>>>(s, table, offs, hq, hsc, hs32, yp, tmin, tmax); break;
+        case 8: return down_dot_gn<T, 8>(s, g, table, offs, hq, hsc, hs32, yp, tmin, tmax, st);
+        case 16: return down_dot_gn<T, 16>(s, g, table, offs, hq, hsc, hs32, yp, tmin, tmax, st);
+        case 32: return down_dot_gn<T, 32>(s, g, table, offs, hq, hsc, hs32, yp, tmin, tmax, st);
+        case 64: return down_dot_gn<T, 64>(s, g, table, offs, hq, hsc, hs32, yp, tmin, tmax, st);
         default: return hipErrorInvalidValue;
     }
+}
+
+hipError_t launch_levels_rows(const float* src, int ld, int rows, int n, int8_t* q, float* sc, float* s32,
+                              hipStream_t st) {
+    if (rows <= 0 || n % 64 || ld % 4) return hipErrorInvalidValue;
+    levels_rows_kernel<<<(unsigned)rows, 256, 0, st>>>(src, ld, n, q, sc, s32);
     return hipGetLastError();
 }
 
 hipError_t launch_gate_up_dot(const MoeShape& s, const ExpertEntry* table, int E, const int* offs, const int* tok,
-                              const float* x, int ldx, int8_t* hq, float* hsc, float* hs32, int tmin, int tmax,
+                              const int8_t* xq, const float* xsc, const float* xs32, float* h, int tmin, int tmax,
                               hipStream_t st) {
-    if (!grouped_dot_gate_up_ok(s) || tmax > kDotMaxTok || ldx % 4) return hipErrorInvalidValue;
-    const dim3 g((unsigned)(s.FF / kDotRows), (unsigned)E);
+    if (!grouped_dot_gate_up_ok(s) || tmax > kDotMaxTok || tmax < 1) return hipErrorInvalidValue;
+    const dim3 g((unsigned)(s.FF / kGuRowsDot), (unsigned)E, (unsigned)((tmax + 1) / 2));
     switch (s.gate_type) {
-        case kQ4_K: return gate_up_dot_g<kQ4_K>(s, g, table, offs, tok, x, ldx, hq, hsc, hs32, tmin, tmax, st);
-        case kQ5_K: return gate_up_dot_g<kQ5_K>(s, g, table, offs, tok, x, ldx, hq, hsc, hs32, tmin, tmax, st);
-        case kQ6_K: return gate_up_dot_g<kQ6_K>(s, g, table, offs, tok, x, ldx, hq, hsc, hs32, tmin, tmax, st);
-        case kQ8_0: return gate_up_dot_g<kQ8_0>(s, g, table, offs, tok, x, ldx, hq, hsc, hs32, tmin, tmax, st);
+        case kQ4_K: return gate_up_dot_g<kQ4_K>(s, g, table, offs, tok, xq, xsc, xs32, h, tmin, tmax, st);
+        case kQ5_K: return gate_up_dot_g<kQ5_K>(s, g, table, offs, tok, xq, xsc, xs32, h, tmin, tmax, st);
+        case kQ6_K: return gate_up_dot_g<kQ6_K>(s, g, table, offs, tok, xq, xsc, xs32, h, tmin, tmax, st);
+        case kQ8_0: return gate_up_dot_g<kQ8_0>(s, g, table, offs, tok, xq, xsc, xs32, h, tmin, tmax, st);
         default: return hipErrorInvalidValue;
     }
 }
 
 hipError_t launch_down_dot(const MoeShape& s, const ExpertEntry* table, int E, const int* offs, const int8_t* hq,
                            const float* hsc, const float* hs32, float* yp, int tmin, int tmax, hipStream_t st) {
-    if (!grouped_dot_down_ok(s) || tmax > kDotMaxTok) return hipErrorInvalidValue;
-    const dim3 g((unsigned)(s.D / kDotRows), (unsigned)E);
+    if (!grouped_dot_down_ok(s) || tmax > kDotMaxTok || tmax < 1) return hipErrorInvalidValue;
+    const dim3 g((unsigned)(s.D / kDotRows), (unsigned)E, (unsigned)((tmax + 1) / 2));
     switch (s.down_type) {
         case kQ4_K: return down_dot_g<kQ4_K>(s, g, table, offs, hq, hsc, hs32, yp, tmin, tmax, st);
         case kQ5_K: return down_dot_g<kQ5_K>(s, g, table, offs, hq, hsc, hs32, yp, tmin, tmax, st);

@@ -566,7 +566,7 @@ def test_grouped_vs_oracle(torch_dev, binding, hip, grouped_mode, name, types, D
 def test_grouped_async_device_routing(torch_dev, binding, hip, grouped_mode, nb, E, k, skew):
     """Routing on the device (route_topk), grouping on the device, Zipf-skewed
     expert popularity: y of every token matches the oracle on the same ids
-    (up to 32 tokens as per-token single-launch blocks, above as the grouped
+    (up to 3 tokens as per-token single-launch blocks, above as the grouped
     block)."""
     torch = torch_dev
     D, FF = 512, 256
