@@ -16,7 +16,8 @@
 //      scanned per expert, expert totals across experts, giving
 //        offs[e]      first position of expert e's group
 //        tok[p], pw[p] token and router weight at position p
-//        pos[t*k+j]   position of (token t, slot j), -1 for an invalid id
+//        pos[t*k+r]   position of token t's r-th pair in ascending expert id
+//                     (-1 past its valid pairs)
 //   2. grouped gate/up: h[p][r] = silu(gate_r . x_tok[p]) * (up_r . x_tok[p]);
 //      on the matrix cores for Q4_K/Q5_K (kernels_grouped_mfma.hip), else one
 //      wave per (expert, FF row) with the group's tokens in tiles of 8.
@@ -110,15 +111,39 @@ __global__ __launch_bounds__(kGroupThreads) void group_pairs_kernel(const int* _
         const int t = c * 64 + lane;
         if (t < nb) {
             const unsigned long long below = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
-            for (int j = 0; j < k; j++) {
-                const int e = ids[(size_t)t * k + j];
-                int p = -1;
-                if (e >= 0 && e < E) {
-                    p = offs[e] + cnt[(size_t)c * E + e] + __popcll(mask[e] & below);
-                    tok[p] = t;
-                    pw[p] = w[(size_t)t * k + j];
+            int ej[kMaxSlots], pj[kMaxSlots];
+#pragma unroll
+            for (int j = 0; j < kMaxSlots; j++) {
+                ej[j] = 0;
+                pj[j] = -1;
+                if (j < k) {
+                    const int e = ids[(size_t)t * k + j];
+                    if (e >= 0 && e < E) {
+                        const int p = offs[e] + cnt[(size_t)c * E + e] + __popcll(mask[e] & below);
+                        tok[p] = t;
+                        pw[p] = w[(size_t)t * k + j];
+                        ej[j] = e;
+                        pj[j] = p;
+                    }
                 }
-                pos[(size_t)t * k + j] = p;
+            }
+            // the token's positions in ascending expert id (equal ids in slot
+            // order), invalid slots last: the combine's summation order
+            int nvalid = 0;
+#pragma unroll
+            for (int j = 0; j < kMaxSlots; j++) nvalid += pj[j] >= 0 ? 1 : 0;
+#pragma unroll
+            for (int j = 0; j < kMaxSlots; j++) {
+                if (j >= k) break;
+                int r = 0;
+#pragma unroll
+                for (int i = 0; i < kMaxSlots; i++) {
+                    if (pj[j] >= 0)
+                        r += (i != j && pj[i] >= 0 && (ej[i] < ej[j] || (ej[i] == ej[j] && i < j))) ? 1 : 0;
+                    else
+                        r += (i < j && i < k && pj[i] < 0) ? 1 : 0;
+                }
+                pos[(size_t)t * k + (pj[j] >= 0 ? r : nvalid + r)] = pj[j];
             }
         }
     }
@@ -234,62 +259,33 @@ __global__ __launch_bounds__(256) void grouped_down_kernel(MoeShape s, const Exp
     }
 }
 
-// y[t][d] = sum over the token's valid pairs, ascending expert id, of
-// w * yp[pos][d].  One thread per (token, 4 consecutive d).  The token's
-// slots are read once into registers; a slot's place in the sum is its rank
-// (ids are distinct per token; equal ids keep slot order), so the fma chain
-// runs in ascending id with no data-dependent indexing.
-__global__ __launch_bounds__(256) void grouped_combine_kernel(const int* __restrict__ ids, const int* __restrict__ pos,
-                                                              const float* __restrict__ pw, int nb, int k, int D,
-                                                              const float* __restrict__ yp, float* __restrict__ y,
-                                                              int ldy) {
+// y[t][d] = sum over the token's valid pairs, ascending expert id (the order
+// of pos), of w * yp[pos][d].  One thread per (token, 4 consecutive d).
+__global__ __launch_bounds__(256) void grouped_combine_kernel(const int* __restrict__ pos, const float* __restrict__ pw,
+                                                              int nb, int k, int D, const float* __restrict__ yp,
+                                                              float* __restrict__ y, int ldy) {
     const int q = blockIdx.x * blockDim.x + threadIdx.x;
     const int per_tok = D / 4;
     if (q >= nb * per_tok) return;
     const int t = q / per_tok, d = (q % per_tok) * 4;
-    int pj[kMaxSlots], ej[kMaxSlots];
-#pragma unroll
-    for (int j = 0; j < kMaxSlots; j++) {
-        pj[j] = j < k ? pos[(size_t)t * k + j] : -1;
-        ej[j] = j < k ? ids[(size_t)t * k + j] : 0;
-    }
     float4 v[kMaxSlots];
     float wv[kMaxSlots];
-    int rank[kMaxSlots];
+    bool ok[kMaxSlots];
 #pragma unroll
-    for (int j = 0; j < kMaxSlots; j++) {
-        const bool ok = pj[j] >= 0;
-        v[j] = ok ? *reinterpret_cast<const float4*>(yp + (size_t)pj[j] * D + d) : make_float4(0.f, 0.f, 0.f, 0.f);
-        wv[j] = ok ? pw[pj[j]] : 0.f;
-        int r = 0;
-#pragma unroll
-        for (int i = 0; i < kMaxSlots; i++)
-            r += (i != j && pj[i] >= 0 && (ej[i] < ej[j] || (ej[i] == ej[j] && i < j))) ? 1 : 0;
-        rank[j] = ok ? r : -1;
+    for (int r = 0; r < kMaxSlots; r++) {
+        const int p = r < k ? pos[(size_t)t * k + r] : -1;
+        ok[r] = p >= 0;
+        v[r] = ok[r] ? *reinterpret_cast<const float4*>(yp + (size_t)p * D + d) : make_float4(0.f, 0.f, 0.f, 0.f);
+        wv[r] = ok[r] ? pw[p] : 0.f;
     }
     float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
     for (int r = 0; r < kMaxSlots; r++) {
-        if (r >= k) break;
-        bool any = false;
-        float w = 0.f;
-        float4 x = make_float4(0.f, 0.f, 0.f, 0.f);
-#pragma unroll
-        for (int j = 0; j < kMaxSlots; j++) {
-            const bool sel = rank[j] == r;
-            any |= sel;
-            w = sel ? wv[j] : w;
-            x.x = sel ? v[j].x : x.x;
-            x.y = sel ? v[j].y : x.y;
-            x.z = sel ? v[j].z : x.z;
-            x.w = sel ? v[j].w : x.w;
-        }
-        if (any) {
-            acc.x = __builtin_fmaf(w, x.x, acc.x);
-            acc.y = __builtin_fmaf(w, x.y, acc.y);
-            acc.z = __builtin_fmaf(w, x.z, acc.z);
-            acc.w = __builtin_fmaf(w, x.w, acc.w);
-        }
+        if (!ok[r]) break;  // the valid pairs come first
+        acc.x = __builtin_fmaf(wv[r], v[r].x, acc.x);
+        acc.y = __builtin_fmaf(wv[r], v[r].y, acc.y);
+        acc.z = __builtin_fmaf(wv[r], v[r].z, acc.z);
+        acc.w = __builtin_fmaf(wv[r], v[r].w, acc.w);
     }
     *reinterpret_cast<float4*>(y + (size_t)t * ldy + d) = acc;
 }
@@ -326,10 +322,11 @@ int set_grouped_wave_max(int tmax) {
 }
 
 // Experts holding at most this many tokens run on the integer-dot kernels
-// (kernels_grouped_dot.hip) in batches of more than kDotWhole tokens; a batch
-// of at most kDotWhole tokens (every expert then holds at most nb tokens: a
-// token's pairs with one expert count once) runs on them whole.
-int g_dot_max = 4;
+// (kernels_grouped_dot.hip) in batches of more than kDotWhole tokens (none by
+// default: there the few small groups would run as a long tail of their own);
+// a batch of at most kDotWhole tokens (every expert then holds at most nb
+// tokens: a token's pairs with one expert count once) runs on them whole.
+int g_dot_max = 0;
 constexpr int kDotWhole = 32;
 
 int set_grouped_dot_max(int tmax) {
@@ -455,7 +452,7 @@ hipError_t launch_moe_grouped(const MoeShape& s, const ExpertEntry* table, int n
         }
     }
     const size_t nthr = (size_t)nb * (s.D / 4);
-    grouped_combine_kernel<<<(unsigned)((nthr + 255) / 256), 256, 0, st>>>(ids, pos, pw, nb, k, s.D, yp, y, ldy);
+    grouped_combine_kernel<<<(unsigned)((nthr + 255) / 256), 256, 0, st>>>(pos, pw, nb, k, s.D, yp, y, ldy);
     return hipGetLastError();
 }
 

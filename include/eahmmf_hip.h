@@ -285,7 +285,7 @@ int eahmmf_hip_set_grouped_mfma(int enable);
  * queries.  Returns the previous value.  No counterpart in the reference. */
 int eahmmf_hip_set_grouped_wave_max(int max_tokens);
 /* In a grouped block of more than 32 tokens, expert groups of at most
- * max_tokens tokens (default 4; 0: none) run on the integer-dot kernels (each
+ * max_tokens tokens (default 0: none) run on the integer-dot kernels (each
  * weight row streamed once and dotted in int32 against int8 levels of each of
  * the group's tokens); a block of at most 32 tokens runs on them whole unless
  * max_tokens is 0.  A negative argument only queries.  Returns the previous
