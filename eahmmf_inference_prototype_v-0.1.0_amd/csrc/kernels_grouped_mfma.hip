@@ -176,7 +176,7 @@ __global__ __launch_bounds__(512) void gate_up_mfma_kernel(MoeShape s, const Exp
     auto rload = [&](int b, int i, GuRowSb<T>& r) {
         const uint8_t* sb = drp[i] + (size_t)b * BB;
         const int dkq = dll[i] >> 4;
-        r.hdr = *reinterpret_cast<const uint4*>(sb);
+        r.hdr = gld16(sb);
         if (T == kQ5_K) r.qh = ld8(sb + 16 + dkq * 8);
 #pragma unroll
         for (int g = 0; g < 4; g++) r.q[g] = ld8(sb + QS + 32 * g + dkq * 8);
@@ -362,8 +362,8 @@ __global__ __launch_bounds__(512) void down_mfma_q6k_kernel(MoeShape s, const Ex
         a.ql0 = ld8_a2(blk + 64 * n + kq * 8);
         a.ql1 = ld8_a2(blk + 64 * n + 32 + kq * 8);
         a.qh = ld8_a2(blk + 128 + 32 * n + kq * 8);
-        a.sc0 = (int)(int8_t)blk[192 + 8 * n + (kq >> 1) + 2 * u0];
-        a.sc1 = (int)(int8_t)blk[192 + 8 * n + (kq >> 1) + 2 * (u0 + 1)];
+        a.sc0 = ld_i8(blk + 192 + 8 * n + (kq >> 1) + 2 * u0);
+        a.sc1 = ld_i8(blk + 192 + 8 * n + (kq >> 1) + 2 * (u0 + 1));
     };
     auto dload = [&](int b, float (&d)[4]) {
 #pragma unroll

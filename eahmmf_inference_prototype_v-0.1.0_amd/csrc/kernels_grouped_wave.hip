@@ -1,5 +1,6 @@
 // kernels_grouped_wave.hip - the ragged grouped expert block's matrix-core
-// matmuls for experts holding few tokens (at most 16 * NT: NT 16-token tiles).
+// matmuls for experts holding few tokens (up to 32: one 16-token tile up to
+// 16 tokens, two above).
 //
 // The workgroup-per-row-block kernels of kernels_grouped_mfma.hip decode a
 // 64- or 128-row block's weight fragments once and share them through LDS
@@ -32,7 +33,7 @@ template <int T>
 __device__ __forceinline__ void krow_load(const uint8_t* row, int b, int kq, KRowSb<T>& r) {
     constexpr int QS = T == kQ5_K ? 48 : 16;
     const uint8_t* sb = row + (size_t)b * Fmt<T>::bytes;
-    r.hdr = *reinterpret_cast<const uint4*>(sb);
+    r.hdr = gld16(sb);
     if (T == kQ5_K) r.qh = ld8(sb + 16 + kq * 8);
 #pragma unroll
     for (int g = 0; g < 4; g++) r.q[g] = ld8(sb + QS + 32 * g + kq * 8);
@@ -70,13 +71,11 @@ __device__ __forceinline__ f16x8 krow_mins(const KRowSb<T>& r, int kq) {
 // gate/up of one expert's 16-row strip for its (at most 16 * NT) tokens:
 // h[q][r] = silu(g) * u.  Experts outside [tmin, tmax] tokens leave at once.
 template <int T, int NT>
-__global__ __launch_bounds__(kWaveWaves * 64) void gate_up_wave_kernel(
-    MoeShape s, const ExpertEntry* __restrict__ table, const int* __restrict__ offs, const _Float16* __restrict__ xh,
-    const _Float16* __restrict__ xl, const _Float16* __restrict__ xsh, const _Float16* __restrict__ xsl,
-    const float* __restrict__ xscale, float* __restrict__ h, int tmin, int tmax) {
-    const int e = blockIdx.y;
-    const int p0 = offs[e], p1 = offs[e + 1], n = p1 - p0;
-    if (n < tmin || n > tmax || n <= 0) return;
+__device__ __forceinline__ void gate_up_wave_body(const MoeShape& s, const ExpertEntry* __restrict__ table, int e,
+                                                  int p0, int p1, const _Float16* __restrict__ xh,
+                                                  const _Float16* __restrict__ xl, const _Float16* __restrict__ xsh,
+                                                  const _Float16* __restrict__ xsl, const float* __restrict__ xscale,
+                                                  float* __restrict__ h) {
     const int w = __builtin_amdgcn_readfirstlane(threadIdx.x / 64), l = threadIdx.x % 64;
     const int lr = l & 15, kq = l >> 4;
     const int r0 = (blockIdx.x * kWaveWaves + w) * 16;
@@ -181,6 +180,22 @@ __global__ __launch_bounds__(kWaveWaves * 64) void gate_up_wave_kernel(
     }
 }
 
+// One launch for groups of tmin..tmax tokens: one 16-token tile for groups of
+// at most 16, two above.
+template <int T>
+__global__ __launch_bounds__(kWaveWaves * 64) void gate_up_wave_kernel(
+    MoeShape s, const ExpertEntry* __restrict__ table, const int* __restrict__ offs, const _Float16* __restrict__ xh,
+    const _Float16* __restrict__ xl, const _Float16* __restrict__ xsh, const _Float16* __restrict__ xsl,
+    const float* __restrict__ xscale, float* __restrict__ h, int tmin, int tmax) {
+    const int e = blockIdx.y;
+    const int p0 = offs[e], p1 = offs[e + 1], n = p1 - p0;
+    if (n < tmin || n > tmax || n <= 0) return;
+    if (n <= 16)
+        gate_up_wave_body<T, 1>(s, table, e, p0, p1, xh, xl, xsh, xsl, xscale, h);
+    else
+        gate_up_wave_body<T, 2>(s, table, e, p0, p1, xh, xl, xsh, xsl, xscale, h);
+}
+
 // down (Q6_K) of one expert's 16-row strip: yp[q][r] = down_r . h[q], h as
 // scaled fp16 hi/lo.  A Q6_K 32-value quarter's weights (q - 32) * sc are
 // split into the exact parts 16 * (q - 32) * (sc >> 4) and (q - 32) * (sc & 15).
@@ -195,17 +210,15 @@ __device__ __forceinline__ void q6_load(const uint8_t* row, int c, int kq, Q6Lan
     a.ql0 = ld8_a2(blk + 64 * n + kq * 8);
     a.ql1 = ld8_a2(blk + 64 * n + 32 + kq * 8);
     a.qh = ld8_a2(blk + 128 + 32 * n + kq * 8);
-    a.sc0 = (int)(int8_t)blk[192 + 8 * n + (kq >> 1) + 2 * u0];
-    a.sc1 = (int)(int8_t)blk[192 + 8 * n + (kq >> 1) + 2 * (u0 + 1)];
+    a.sc0 = ld_i8(blk + 192 + 8 * n + (kq >> 1) + 2 * u0);
+    a.sc1 = ld_i8(blk + 192 + 8 * n + (kq >> 1) + 2 * (u0 + 1));
 }
 
 template <int NT>
-__global__ __launch_bounds__(kWaveWaves * 64) void down_wave_q6k_kernel(
-    MoeShape s, const ExpertEntry* __restrict__ table, const int* __restrict__ offs, const _Float16* __restrict__ hh,
-    const _Float16* __restrict__ hl, const float* __restrict__ hscale, float* __restrict__ yp, int tmin, int tmax) {
-    const int e = blockIdx.y;
-    const int p0 = offs[e], p1 = offs[e + 1], n = p1 - p0;
-    if (n < tmin || n > tmax || n <= 0) return;
+__device__ __forceinline__ void down_wave_q6k_body(const MoeShape& s, const ExpertEntry* __restrict__ table, int e,
+                                                   int p0, int p1, const _Float16* __restrict__ hh,
+                                                   const _Float16* __restrict__ hl, const float* __restrict__ hscale,
+                                                   float* __restrict__ yp) {
     const int w = __builtin_amdgcn_readfirstlane(threadIdx.x / 64), l = threadIdx.x % 64;
     const int lr = l & 15, kq = l >> 4;
     const int r0 = (blockIdx.x * kWaveWaves + w) * 16;
@@ -285,6 +298,18 @@ __global__ __launch_bounds__(kWaveWaves * 64) void down_wave_q6k_kernel(
     }
 }
 
+__global__ __launch_bounds__(kWaveWaves * 64) void down_wave_q6k_kernel(
+    MoeShape s, const ExpertEntry* __restrict__ table, const int* __restrict__ offs, const _Float16* __restrict__ hh,
+    const _Float16* __restrict__ hl, const float* __restrict__ hscale, float* __restrict__ yp, int tmin, int tmax) {
+    const int e = blockIdx.y;
+    const int p0 = offs[e], p1 = offs[e + 1], n = p1 - p0;
+    if (n < tmin || n > tmax || n <= 0) return;
+    if (n <= 16)
+        down_wave_q6k_body<1>(s, table, e, p0, p1, hh, hl, hscale, yp);
+    else
+        down_wave_q6k_body<2>(s, table, e, p0, p1, hh, hl, hscale, yp);
+}
+
 // ---------------------------------------------------------------------------
 
 bool grouped_wave_gate_up_ok(const MoeShape& s) { return grouped_mfma_gate_up_ok(s); }
@@ -294,18 +319,10 @@ hipError_t launch_gate_up_wave(const MoeShape& s, const ExpertEntry* table, int 
                                const _Float16* xl, const _Float16* xsh, const _Float16* xsl, const float* xscale,
                                float* h, int tmin, int tmax, hipStream_t st) {
     const dim3 g((unsigned)((s.FF / 16 + kWaveWaves - 1) / kWaveWaves), (unsigned)E);
-    const bool two = tmax > 16;
-    if (s.gate_type == kQ4_K) {
-        if (two)
-            gate_up_wave_kernel<kQ4_K, 2><<<g, kWaveWaves * 64, 0, st>>>(s, table, offs, xh, xl, xsh, xsl, xscale, h, tmin, tmax);
-        else
-            gate_up_wave_kernel<kQ4_K, 1><<<g, kWaveWaves * 64, 0, st>>>(s, table, offs, xh, xl, xsh, xsl, xscale, h, tmin, tmax);
-    } else {
-        if (two)
-            gate_up_wave_kernel<kQ5_K, 2><<<g, kWaveWaves * 64, 0, st>>>(s, table, offs, xh, xl, xsh, xsl, xscale, h, tmin, tmax);
-        else
-            gate_up_wave_kernel<kQ5_K, 1><<<g, kWaveWaves * 64, 0, st>>>(s, table, offs, xh, xl, xsh, xsl, xscale, h, tmin, tmax);
-    }
+    if (s.gate_type == kQ4_K)
+        gate_up_wave_kernel<kQ4_K><<<g, kWaveWaves * 64, 0, st>>>(s, table, offs, xh, xl, xsh, xsl, xscale, h, tmin, tmax);
+    else
+        gate_up_wave_kernel<kQ5_K><<<g, kWaveWaves * 64, 0, st>>>(s, table, offs, xh, xl, xsh, xsl, xscale, h, tmin, tmax);
     return hipGetLastError();
 }
 
@@ -313,10 +330,7 @@ hipError_t launch_down_wave(const MoeShape& s, const ExpertEntry* table, int E, 
                             const _Float16* hl, const float* hscale, float* yp, int tmin, int tmax,
                             hipStream_t st) {
     const dim3 g((unsigned)((s.D / 16 + kWaveWaves - 1) / kWaveWaves), (unsigned)E);
-    if (tmax > 16)
-        down_wave_q6k_kernel<2><<<g, kWaveWaves * 64, 0, st>>>(s, table, offs, hh, hl, hscale, yp, tmin, tmax);
-    else
-        down_wave_q6k_kernel<1><<<g, kWaveWaves * 64, 0, st>>>(s, table, offs, hh, hl, hscale, yp, tmin, tmax);
+    down_wave_q6k_kernel<<<g, kWaveWaves * 64, 0, st>>>(s, table, offs, hh, hl, hscale, yp, tmin, tmax);
     return hipGetLastError();
 }
 

@@ -16,12 +16,21 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 constexpr int kPassTok = 64;  // tokens per pass: four 16-token tiles
 constexpr float kSumScale = 1.0f / 16.0f;  // sub-block sums (32 values) kept below 2^14
 
-struct __attribute__((packed, aligned(2))) Bytes8A2 { uint32_t x, y; };
-__device__ __forceinline__ uint2 ld8_a2(const uint8_t* p) {
-    const Bytes8A2 v = *reinterpret_cast<const Bytes8A2*>(p);
+// Weight bytes are read through global-address-space pointers: a row pointer
+// taken from the expert table is otherwise generic, and generic (flat) loads
+// also count against the LDS counter, so every LDS wait and barrier would
+// drain the weight loads in flight.
+typedef uint32_t __attribute__((ext_vector_type(2))) mf_u32x2;
+typedef uint32_t __attribute__((aligned(2))) mf_u32a2;
+__device__ __forceinline__ uint2 ld8_a2(const uint8_t* p) {  // 2-byte aligned
+    const __attribute__((address_space(1))) mf_u32a2* q = (const __attribute__((address_space(1))) mf_u32a2*)p;
+    return make_uint2(q[0], q[1]);
+}
+__device__ __forceinline__ uint2 ld8(const uint8_t* p) {  // 8-byte aligned
+    const mf_u32x2 v = *(const __attribute__((address_space(1))) mf_u32x2*)p;
     return make_uint2(v.x, v.y);
 }
-__device__ __forceinline__ uint2 ld8(const uint8_t* p) { return *reinterpret_cast<const uint2*>(p); }
+__device__ __forceinline__ int ld_i8(const uint8_t* p) { return (int)*(const __attribute__((address_space(1))) int8_t*)p; }
 
 // Two fp16 values b0, b1 from bytes 2m, 2m+1 of w (each < 256): the byte is
 // placed under the exponent of 1024 (0x64XX = 1024 + XX) and 1024 removed.
@@ -44,8 +53,8 @@ __device__ __forceinline__ f32x4 mfma(f16x8 a, f16x8 b, f32x4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
 }
 
-__device__ __forceinline__ float half_at(const uint8_t* p) {
-    return (float)__builtin_bit_cast(_Float16, *reinterpret_cast<const uint16_t*>(p));
+__device__ __forceinline__ float half_at(const uint8_t* p) {  // a weight row's fp16 scale (global)
+    return (float)__builtin_bit_cast(_Float16, *(const __attribute__((address_space(1))) uint16_t*)p);
 }
 
 }  // namespace eahmmf
