@@ -107,7 +107,7 @@ __global__ __launch_bounds__(256) void prep_rows_kernel(const int* __restrict__ 
 // A fragments (gate and up) into LDS, double-buffered, so each fragment is
 // built once per workgroup and read by every wave; each wave then runs 4 row
 // tiles x (gate, up) x (hi, lo) MFMAs against its own token tile, whose
-// activations stream from global memory one sub-block ahead.  Per
+// activations stream from global memory three sub-blocks ahead.  Per
 // super-block the rows' mins (as A fragments of the min-term MFMA) and their
 // (d, dmin) are staged the same way.  The weight bytes a thread decodes are
 // loaded one super-block ahead.
@@ -216,13 +216,20 @@ __global__ __launch_bounds__(512) void gate_up_mfma_kernel(MoeShape s, const Exp
         sbstage(0, i, rc[i]);
         decode(0, i, rc[i], 0);
     }
-    // activations of the wave's token tile, one sub-block ahead
-    auto xload = [&](int kk, f16x8& bh, f16x8& bl) {
+    // activations of the wave's token tile, kBAhead sub-blocks ahead in a
+    // ring of kBAhead + 1 (a sub-block's compute is shorter than an L2 load:
+    // one sub-block ahead, every sub-block waited for its activations).
+    // Every sub-block issues its load (the last ones reload the last
+    // sub-block) so the compiler's counts of loads in flight stay exact.
+    constexpr int kBAhead = 3;
+    auto xload = [&](int jj, f16x8& bh, f16x8& bl) {
+        const int kk = min(jj, nsub - 1) * 32;
         bh = *reinterpret_cast<const f16x8*>(xh + (size_t)qc * D + kk + kq * 8);
         bl = *reinterpret_cast<const f16x8*>(xl + (size_t)qc * D + kk + kq * 8);
     };
-    f16x8 bh, bl, nbh, nbl;
-    xload(0, bh, bl);
+    f16x8 bh[kBAhead + 1], bl[kBAhead + 1];
+#pragma unroll
+    for (int a = 0; a < kBAhead; a++) xload(a, bh[a], bl[a]);
     lds_barrier();
 
     f32x4 og[kGuRowTiles], ou[kGuRowTiles], ag[kGuRowTiles], au[kGuRowTiles];
@@ -238,23 +245,22 @@ __global__ __launch_bounds__(512) void gate_up_mfma_kernel(MoeShape s, const Exp
         }
 #pragma unroll
         for (int j = 0; j < 8; j++) {
-            const int jj = 8 * b + j, par = j & 1;
-            const bool more = j < 7 || more_sb;
-            if (more) xload((jj + 1) * 32, nbh, nbl);
+            const int jj = 8 * b + j, par = j & 1, slot = j & kBAhead;  // 8 * b + j == j modulo 4
+            xload(jj + kBAhead, bh[(j + kBAhead) & kBAhead], bl[(j + kBAhead) & kBAhead]);
             if (busy) {
 #pragma unroll
                 for (int rt = 0; rt < kGuRowTiles; rt++) {
                     const f16x8 Ag = __builtin_bit_cast(f16x8, L.a[par][0][rt][l]);
                     const f16x8 Au = __builtin_bit_cast(f16x8, L.a[par][1][rt][l]);
-                    ag[rt] = mfma(Ag, bh, ag[rt]);
-                    au[rt] = mfma(Au, bh, au[rt]);
+                    ag[rt] = mfma(Ag, bh[slot], ag[rt]);
+                    au[rt] = mfma(Au, bh[slot], au[rt]);
                 }
 #pragma unroll
                 for (int rt = 0; rt < kGuRowTiles; rt++) {
                     const f16x8 Ag = __builtin_bit_cast(f16x8, L.a[par][0][rt][l]);
                     const f16x8 Au = __builtin_bit_cast(f16x8, L.a[par][1][rt][l]);
-                    ag[rt] = mfma(Ag, bl, ag[rt]);
-                    au[rt] = mfma(Au, bl, au[rt]);
+                    ag[rt] = mfma(Ag, bl[slot], ag[rt]);
+                    au[rt] = mfma(Au, bl[slot], au[rt]);
                 }
                 if (j == 7) {  // end of the super-block: min term, then d / dmin
                     const f16x8 zero8 = {};
@@ -297,8 +303,6 @@ __global__ __launch_bounds__(512) void gate_up_mfma_kernel(MoeShape s, const Exp
                 }
             }
             lds_barrier();
-            bh = nbh;
-            bl = nbl;
         }
     }
     if (!qok) return;
