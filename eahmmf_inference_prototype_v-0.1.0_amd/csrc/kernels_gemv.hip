@@ -189,7 +189,7 @@ __global__ __launch_bounds__(kGemvMaxWaves * 64) void gemv_kernel(GemvArgs a) {
             acc = group_sum<64>(acc);  // the total is in lane 63
             if (lane == 63) {
                 const float v = resid ? rv + acc : acc;
-                g.out(sg)[row] = v;
+                *(__attribute__((address_space(1))) float*)(g.out(sg) + row) = v;  // (a global store, not flat)
                 if (v > best || best_i == 0xFFFFFFFFu) {
                     best = v;
                     best_i = (unsigned)(r0 + r);

@@ -277,12 +277,13 @@ __device__ __forceinline__ void decode_seg_q8_0(const uint8_t* blk, float* w) {
     for (int i = 0; i < 32; i++) w[i] = d * (float)(int8_t)byte_of(q.w[i >> 2], i & 3);
 }
 
+template <class LD = GlobalLd>
 __device__ __forceinline__ void decode_seg_f32(const uint8_t* blk, float* w) {
-    const float4* p = reinterpret_cast<const float4*>(blk);
 #pragma unroll
     for (int i = 0; i < 8; i++) {
-        const float4 v = p[i];
-        w[4 * i] = v.x; w[4 * i + 1] = v.y; w[4 * i + 2] = v.z; w[4 * i + 3] = v.w;
+        const uint4 v = LD::b16(blk + 16 * i);
+        w[4 * i] = __uint_as_float(v.x); w[4 * i + 1] = __uint_as_float(v.y);
+        w[4 * i + 2] = __uint_as_float(v.z); w[4 * i + 3] = __uint_as_float(v.w);
     }
 }
 
@@ -293,7 +294,7 @@ __device__ __forceinline__ void decode_row_seg(const uint8_t* row, int s, float*
     else if constexpr (T == kQ5_K) decode_seg_q5k<LD>(row + (size_t)(s >> 3) * 176, s & 7, w);
     else if constexpr (T == kQ6_K) decode_seg_q6k<LD>(row + (size_t)(s >> 3) * 210, s & 7, w);
     else if constexpr (T == kQ8_0) decode_seg_q8_0<LD>(row + (size_t)s * 34, w);
-    else decode_seg_f32(row + (size_t)s * 128, w);
+    else decode_seg_f32<LD>(row + (size_t)s * 128, w);
 }
 
 // Wave-wide float sum (wave64); every lane receives the total.
