@@ -151,9 +151,10 @@ hipError_t launch_gate_up_dot(const MoeShape& s, const ExpertEntry* table, int E
                               hipStream_t st);
 hipError_t launch_down_dot(const MoeShape& s, const ExpertEntry* table, int E, const int* offs, const int8_t* hq,
                            const float* hsc, const float* hs32, float* yp, int tmin, int tmax, hipStream_t st);
-// Largest expert (in tokens) the integer-dot kernels take in a batch of more
-// than 32 tokens (0: none; batches of at most 32 tokens run on them whole
-// unless this is 0); a negative argument only queries.  Returns the previous value.
+// The integer-dot kernels: 0 off; 1..32 on, and in batches of more than 32
+// tokens also for groups of at most that many tokens; above 32 on for
+// batches of at most 32 tokens only (the default, reported as 33).  A
+// negative argument only queries.  Returns the previous setting.
 int set_grouped_dot_max(int tmax);
 // 1 (default): the grouped block uses the matrix-core matmuls where the formats
 // allow; 0: the vector-ALU kernels only.  A negative argument only queries.

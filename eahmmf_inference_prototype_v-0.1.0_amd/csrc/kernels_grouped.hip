@@ -321,17 +321,23 @@ int set_grouped_wave_max(int tmax) {
     return prev;
 }
 
-// Experts holding at most this many tokens run on the integer-dot kernels
-// (kernels_grouped_dot.hip) in batches of more than kDotWhole tokens (none by
-// default: there the few small groups would run as a long tail of their own);
-// a batch of at most kDotWhole tokens (every expert then holds at most nb
-// tokens: a token's pairs with one expert count once) runs on them whole.
-int g_dot_max = 0;
+// The integer-dot kernels (kernels_grouped_dot.hip) take a batch of at most
+// kDotWhole tokens whole (every expert then holds at most nb tokens: a
+// token's pairs with one expert count once), and in larger batches the
+// groups of at most g_dot_max tokens (none by default: there the few small
+// groups ran as a long tail of their own).  g_dot_on = 0 turns the path off.
 constexpr int kDotWhole = 32;
+int g_dot_on = 1;
+int g_dot_max = 0;
 
 int set_grouped_dot_max(int tmax) {
-    const int prev = g_dot_max;
-    if (tmax >= 0) g_dot_max = tmax > kDotWhole ? kDotWhole : tmax;
+    const int prev = !g_dot_on ? 0 : (g_dot_max > 0 ? g_dot_max : kDotWhole + 1);
+    if (tmax == 0) {
+        g_dot_on = 0;
+    } else if (tmax > 0) {
+        g_dot_on = 1;
+        g_dot_max = tmax > kDotWhole ? 0 : tmax;
+    }
     return prev;
 }
 
@@ -388,8 +394,9 @@ hipError_t launch_moe_grouped(const MoeShape& s, const ExpertEntry* table, int n
     // matrix-core kernels up to wave_max, then the workgroup kernels (or the
     // vector-ALU kernels for everything above dmax).  A group holds at most nb
     // tokens, so launches whose range starts above nb are skipped.
-    const bool dot = g_dot_max > 0 && grouped_dot_gate_up_ok(s) && grouped_dot_down_ok(s);
-    const int dmax = !dot ? 0 : (nb <= kDotWhole ? nb : g_dot_max);
+    const int dmax = !(g_dot_on && grouped_dot_gate_up_ok(s) && grouped_dot_down_ok(s)) ? 0
+                     : (nb <= kDotWhole ? nb : g_dot_max);
+    const bool dot = dmax > 0;
     const int rest = dmax + 1;  // smallest group left to the other kernels
     const int wave_max = g_wave_max;
     const int wg_min = wave_max + 1 > rest ? wave_max + 1 : rest;

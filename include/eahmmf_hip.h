@@ -284,12 +284,13 @@ int eahmmf_hip_set_grouped_mfma(int enable);
  * per-wave kernels, at most 32 (default 32); a negative argument only
  * queries.  Returns the previous value.  No counterpart in the reference. */
 int eahmmf_hip_set_grouped_wave_max(int max_tokens);
-/* In a grouped block of more than 32 tokens, expert groups of at most
- * max_tokens tokens (default 0: none) run on the integer-dot kernels (each
- * weight row streamed once and dotted in int32 against int8 levels of each of
- * the group's tokens); a block of at most 32 tokens runs on them whole unless
- * max_tokens is 0.  A negative argument only queries.  Returns the previous
- * value.  No counterpart in the reference. */
+/* The grouped block's integer-dot kernels (each weight row streamed once and
+ * dotted in int32 against int8 levels of each of the group's tokens): 0
+ * turns them off; any positive value turns them on for blocks of at most 32
+ * tokens, which then run on them whole; 1..32 also sends the groups of at
+ * most that many tokens of larger blocks to them (above 32, the default,
+ * reported as 33: none).  A negative argument only queries.  Returns the
+ * previous setting.  No counterpart in the reference. */
 int eahmmf_hip_set_grouped_dot_max(int max_tokens);
 /* The single-launch expert block's workgroups wait for each other's words
  * (h, per-partition partials).  Every wait is bounded; when one gives up the

@@ -65,6 +65,29 @@ def test_row_bytes(hip, t, ne0):
     assert hip.eahmmf_hip_row_bytes(t, ne0) == oracle.row_bytes(t, ne0)
 
 
+def test_grouped_path_knobs(hip):
+    """The grouped block's kernel-path settings (host state only): the
+    integer-dot path is on for blocks of at most 32 tokens by default
+    (reported as 33), 0 turns it off, 1..32 also routes small groups of larger
+    blocks to it; the per-wave matrix-core split is clamped to 32."""
+    d0, w0, m0 = (hip.eahmmf_hip_set_grouped_dot_max(-1), hip.eahmmf_hip_set_grouped_wave_max(-1),
+                  hip.eahmmf_hip_set_grouped_mfma(-1))
+    try:
+        assert d0 == 33 and w0 == 32 and m0 == 1
+        assert hip.eahmmf_hip_set_grouped_dot_max(0) == 33
+        assert hip.eahmmf_hip_set_grouped_dot_max(-1) == 0
+        assert hip.eahmmf_hip_set_grouped_dot_max(4) == 0
+        assert hip.eahmmf_hip_set_grouped_dot_max(-1) == 4
+        assert hip.eahmmf_hip_set_grouped_dot_max(100) == 4
+        assert hip.eahmmf_hip_set_grouped_dot_max(-1) == 33
+        assert hip.eahmmf_hip_set_grouped_wave_max(99) == 32
+        assert hip.eahmmf_hip_set_grouped_wave_max(-1) == 32
+    finally:
+        hip.eahmmf_hip_set_grouped_dot_max(d0)
+        hip.eahmmf_hip_set_grouped_wave_max(w0)
+        hip.eahmmf_hip_set_grouped_mfma(m0)
+
+
 def test_row_bytes_rejects(hip):
     assert hip.eahmmf_hip_row_bytes(12, 300) == 0
     assert hip.eahmmf_hip_row_bytes(3, 256) == 0
