@@ -499,13 +499,20 @@ def device_blocks(torch, t, nrows, ne0, gen, scale):
     return raw.view(nrows, (ne0 // blck) * nbytes)
 
 
-def c3_model(torch, b, expert_type, n_ctx, seed=3):
-    """The 48-layer Qwen3-30B-A3B-shaped model in HBM: D=2048, 32 query / 4 KV
-    heads of dim 128, 128 experts top-8, FF 768, vocab 151936; experts all
-    expert_type, attention, embedding and output head Q8_0, router F32, norm
-    weights 1.  Weights are generated on the device (random codes with
-    fp16 scales sized for ~0.02 weights) and borrowed by the model."""
-    NL, D_, NH, NKV, HD, E_, K_, FF_, V = 48, 2048, 32, 4, 128, 128, 8, 768, 151936
+QWEN3_30B = dict(n_layer=48, D=2048, n_head=32, n_kv=4, hd=128, n_expert=128, n_used=8, FF=768, n_vocab=151936)
+QWEN3_235B = dict(n_layer=94, D=4096, n_head=64, n_kv=4, hd=128, n_expert=128, n_used=8, FF=1536, n_vocab=151936)
+
+
+def c3_model(torch, b, expert_type, n_ctx, seed=3, shape=QWEN3_30B, types=None):
+    """A Qwen3-MoE-shaped model in HBM (default the 48-layer Qwen3-30B-A3B
+    shape: D=2048, 32 query / 4 KV heads of dim 128, 128 experts top-8, FF
+    768, vocab 151936); experts all expert_type (or types = (gate, up, down)),
+    attention, embedding and output head Q8_0, router F32, norm weights 1.
+    Weights are generated on the device (random codes with fp16 scales sized
+    for ~0.02 weights) and borrowed by the model."""
+    NL, D_, NH, NKV, HD = shape["n_layer"], shape["D"], shape["n_head"], shape["n_kv"], shape["hd"]
+    E_, K_, FF_, V = shape["n_expert"], shape["n_used"], shape["FF"], shape["n_vocab"]
+    gt_, ut_, dt_ = types if types else (expert_type,) * 3
     gen = torch.Generator(device="cuda")
     gen.manual_seed(seed)
     sc = {Q8_0: 3e-4, Q5_K: 5e-5, Q4_K: 1e-4, Q6_K: 1e-5}
@@ -533,9 +540,9 @@ def c3_model(torch, b, expert_type, n_ctx, seed=3):
         add(p + "attn_v.weight", Q8_0, D_, NKV * HD)
         add(p + "attn_output.weight", Q8_0, NH * HD, D_)
         add(p + "ffn_gate_inp.weight", 0, D_, E_, scale=0.02)
-        add(p + "ffn_gate_exps.weight", expert_type, D_, E_ * FF_, ne=[D_, FF_, E_])
-        add(p + "ffn_up_exps.weight", expert_type, D_, E_ * FF_, ne=[D_, FF_, E_])
-        add(p + "ffn_down_exps.weight", expert_type, FF_, E_ * D_, ne=[FF_, D_, E_])
+        add(p + "ffn_gate_exps.weight", gt_, D_, E_ * FF_, ne=[D_, FF_, E_])
+        add(p + "ffn_up_exps.weight", ut_, D_, E_ * FF_, ne=[D_, FF_, E_])
+        add(p + "ffn_down_exps.weight", dt_, FF_, E_ * D_, ne=[FF_, D_, E_])
     torch.cuda.synchronize()
     hp = dict(n_layer=NL, D=D_, n_head=NH, n_kv=NKV, hd=HD, n_expert=E_, n_used=K_, FF=FF_, n_vocab=V, n_ctx=n_ctx,
               eps=1e-6, rope_base=1e6)
@@ -609,6 +616,100 @@ def bench_c3(args, torch, b, hip):
                      "frac": round(r["GB_s"] / HBM_PEAK_GBS, 4), "traffic": None},
         "cpu_baseline": r.get("cpu_baseline"),
         "variants": results}), flush=True)
+
+
+def bench_c5_seqs(args, torch, b, hip):
+    """16 sequences decoded together through the whole 94-layer
+    Qwen3-235B-A22B-shaped model (D=4096, 64 query / 4 KV heads of dim 128,
+    128 experts top-8 FF=1536, Q4_K gate/up + Q6_K down, attention + embedding
+    + output head Q8_0, router F32, vocab 151936; about 155 GB in HBM).  Each
+    sequence is prefilled with its own prompt (lengths 32-256, so the batch is
+    ragged); a timed step is one eahmmf_hip_model_decode_seqs call: one token
+    of every sequence, each at its own position and attending to its own KV
+    rows, all 16 logits rows back on the host, the next tokens picked there
+    (greedy).  Beside it: the same 16 tokens as 16 single-sequence forwards,
+    one after another (what a one-sequence engine does).  value = aggregate
+    decode tokens/s."""
+    NSEQ = 16
+    steps = args.steps if args.steps else 20
+    warm = args.warmup if args.warmup else 3
+    free, _ = torch.cuda.mem_get_info()
+    if free < 200e9:
+        print(f"bench c5seq: needs about 170 GB of free device memory, {free / 1e9:.0f} GB free", file=sys.stderr)
+        sys.exit(3)
+    rng = np.random.default_rng(9)
+    lens = rng.integers(32, 257, NSEQ)
+    n_ctx = int(lens.max()) + warm + steps + 8
+    t0 = time.perf_counter()
+    m, keep, hp = c3_model(torch, b, Q4_K, n_ctx, seed=4, shape=QWEN3_235B, types=(Q4_K, Q4_K, Q6_K))
+    m.set_sequences(NSEQ)
+    t_build = time.perf_counter() - t0
+    t0 = time.perf_counter()
+    last = []
+    for s_ in range(NSEQ):
+        lg = m.eval(rng.integers(0, hp["n_vocab"], int(lens[s_])).astype(np.int32), 0, 64, seq=s_)
+        assert np.isfinite(lg).all(), "non-finite logits after a prefill"
+        last.append(int(np.argmax(lg)))
+    t_prefill = time.perf_counter() - t0
+    toks, pos, seqs = np.array(last, np.int32), lens.astype(np.int32).copy(), np.arange(NSEQ, dtype=np.int32)
+
+    def step():
+        nonlocal toks
+        lg = m.decode_seqs(toks, seqs, pos)
+        toks = np.argmax(lg, axis=1).astype(np.int32)
+        pos[:] += 1
+
+    for _ in range(warm):
+        step()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        step()
+    el = time.perf_counter() - t0
+    # one traced step: distinct routed experts per layer (the expert bytes of a step)
+    m.set_trace(True)
+    m.trace_clear()
+    kv_rows = int(pos.sum()) + NSEQ
+    step()
+    ids, _ = m.trace()
+    m.set_trace(False)
+    ids = ids.reshape(hp["n_layer"], NSEQ, hp["n_used"])
+    distinct = float(np.mean([len(np.unique(ids[l])) for l in range(hp["n_layer"])]))
+    # the same tokens as single-sequence forwards, one after another
+    n_seq_steps = 2
+    t0 = time.perf_counter()
+    for _ in range(n_seq_steps):
+        for s_ in range(NSEQ):
+            lg = m.forward([int(toks[s_])], int(pos[s_]), seq=s_)
+            toks[s_] = int(np.argmax(lg))
+            pos[s_] += 1
+    el_seq = (time.perf_counter() - t0) / n_seq_steps
+    D_, FF_, NL, KD, QD = hp["D"], hp["FF"], hp["n_layer"], hp["n_kv"] * hp["hd"], hp["n_head"] * hp["hd"]
+    q8 = lambda ne0: b.row_bytes(Q8_0, ne0)
+    exp_bytes = 2 * FF_ * b.row_bytes(Q4_K, D_) + D_ * b.row_bytes(Q6_K, FF_)
+    dense = (QD + 2 * KD) * q8(D_) + D_ * q8(QD) + hp["n_expert"] * D_ * 4
+    step_bytes = NL * (dense + distinct * exp_bytes + 2 * kv_rows * KD * 4) + hp["n_vocab"] * q8(D_)
+    ms = el * 1e3 / steps
+    gbs = step_bytes / (ms * 1e-3) / 1e9
+    r = {"metric": "16-sequence decode tokens/s, 94-layer Qwen3-235B-A22B-shaped model (whole model on the device)",
+         "unit": "tokens/s", "value": round(NSEQ * steps / el, 1), "n_gpus": 1, "steps": steps, "warmup": warm,
+         "ms_per_step": round(ms, 3), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+         "dtype": "f32", "data": "synthetic",
+         "config": {"workload": "one decode token of each of 16 sequences per step (eahmmf_hip_model_decode_seqs), "
+                                "94 layers D=4096 64/4 heads hd=128, 128 experts top-8 FF=1536 Q4_K/Q4_K/Q6_K, "
+                                "attention + embedding + output head Q8_0, router F32, vocab 151936",
+                    "prompt_lengths": [int(v) for v in lens]},
+         "step_bytes": int(step_bytes), "distinct_experts_per_layer": round(distinct, 1),
+         "roofline": {"bound": "hbm", "kernel": "whole decode step (all launches)", "achieved": round(gbs, 1),
+                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None},
+         "one_sequence_at_a_time_ms_per_16_tokens": round(el_seq * 1e3, 2),
+         "one_sequence_at_a_time_tokens_per_s": round(NSEQ / el_seq, 1),
+         "prefill_tokens_per_s": round(float(lens.sum()) / t_prefill, 1), "build_s": round(t_build, 1),
+         "what": "step = decode_seqs (16 tokens, logits [16][151936] to the host) + host argmax; step_bytes = "
+                 "dense weights once + distinct routed experts (one traced step) + KV rows read + output head"}
+    m.close()
+    del keep
+    torch.cuda.empty_cache()
+    print(json.dumps(r), flush=True)
 
 
 def bench_c3_experts(args, torch, b, hip):
@@ -974,11 +1075,13 @@ def main():
     ap.add_argument("--c3-cpu-child", type=int, default=0, help=argparse.SUPPRESS)
     ap.add_argument("--c3-cpu-etype", type=int, default=Q5_K, help=argparse.SUPPRESS)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--workload", choices=("c2", "c3", "c3x", "c4", "c5", "c5b16", "stream", "staging", "dropin"), default="c2",
+    ap.add_argument("--workload", choices=("c2", "c3", "c3x", "c4", "c5", "c5b16", "c5seq", "stream", "staging",
+                                           "dropin"), default="c2",
                     help="c2 (default): the headline single-token layer; c3: one decode token through the whole "
                          "48-layer model; c3x: the 48 layers' expert blocks only; "
                          "c4: ragged grouped prefill; c5: single-token layer at the 235B shape; "
-                         "c5b16: a 16-sequence decode batch at the 235B shape; "
+                         "c5b16: a 16-sequence decode batch at the 235B shape (one layer's expert block); "
+                         "c5seq: 16 sequences decoded together through the whole 94-layer 235B-shaped model; "
                          "stream: the achievable HBM read rate (streaming-read kernel); "
                          "staging: making one layer's experts resident from host memory; "
                          "dropin: a C2 layer-token through the drop-in matmul calls")
@@ -1009,7 +1112,7 @@ def main():
     if args.workload != "c2":
         hip_ = b.lib()
         torch.cuda.set_device(0)
-        {"c3": bench_c3, "c3x": bench_c3_experts, "c4": bench_c4, "c5": bench_c5, "c5b16": bench_c5_batch, "stream": bench_stream,
+        {"c3": bench_c3, "c3x": bench_c3_experts, "c4": bench_c4, "c5": bench_c5, "c5b16": bench_c5_batch, "c5seq": bench_c5_seqs, "stream": bench_stream,
          "staging": bench_staging, "dropin": bench_dropin}[args.workload](args, torch, b, hip_)
         return
     hip = b.lib()

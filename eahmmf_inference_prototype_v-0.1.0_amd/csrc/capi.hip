@@ -60,7 +60,7 @@ constexpr size_t kRingChunk = (size_t)32 << 20;
 
 struct DevCtx {
     hipStream_t stream = nullptr;
-    DeviceBuf dx, dy, dy2, dh, dids, dw, dyp, dhx, dgs, dtab, drt;  // device scratch
+    DeviceBuf dx, dy, dy2, dh, dids, dw, dyp, dhx, dgs, dtab, drt, dws;  // device scratch
     DeviceBuf px, py, py2;                // pinned host staging
     unsigned* dsync = nullptr;            // fused-launch error word and ticket counters (zeroed once)
     FusedState fused;                     // the fused kernel's scratch set (dhx, dyp, dsync) and epochs
@@ -290,6 +290,16 @@ void fill_slot(uint8_t* slot, const std::vector<Piece>& ps, size_t total, int nt
     for (std::thread& x : th) x.join();
 }
 
+// The drop-in matmul's launch: on the matrix cores for 2..64 tokens of a
+// K-quant or Q8_0 matrix (workspace grown on demand), else the general kernel.
+hipError_t matmul_launch(DevCtx* c, int type, const uint8_t* w, int ne0, int ne1, size_t rb, int nb, float* out) {
+    const float* x = (const float*)c->dx.p;
+    if (dense_mfma_enabled() && matmul_mfma_ok(type, w, ne0, rb, x, nb, ne0) &&
+        grow_device(c->dws, matmul_mfma_ws_bytes(ne0, ne1, nb)))
+        return launch_matmul_mfma(type, w, ne0, ne1, rb, x, nb, ne0, out, ne1, c->dws.p, c->dws.cap, c->stream);
+    return launch_matmul(type, w, ne0, ne1, rb, x, nb, ne0, out, ne1, c->stream);
+}
+
 }  // namespace
 
 void eahmmf::set_last_error(const char* msg) { set_error("%s", msg); }
@@ -313,8 +323,7 @@ bool eahmmf_hip_matmul(const uint8_t* device_weights, int type, int ne0, int ne1
     if (!c) return false;
     const size_t obytes = (size_t)nb * ne1 * sizeof(float);
     bool ok = grow_device(c->dy, obytes) && grow_pinned(c->py, obytes) && stage_x(c, host_x, nb, ne0, ldx);
-    if (ok) ok = hip_ok(launch_matmul(type, device_weights, ne0, ne1, row_bytes, (const float*)c->dx.p, nb, ne0,
-                                      (float*)c->dy.p, ne1, c->stream), "matmul launch");
+    if (ok) ok = hip_ok(matmul_launch(c, type, device_weights, ne0, ne1, row_bytes, nb, (float*)c->dy.p), "matmul launch");
     if (ok) ok = hip_ok(hipMemcpyAsync(c->py.p, c->dy.p, obytes, hipMemcpyDeviceToHost, c->stream), "hipMemcpyAsync(out)");
     ok = drain(c, ok);
     if (ok) unstage_rows((const float*)c->py.p, nb, ne1, host_out, ldo);
@@ -334,10 +343,8 @@ bool eahmmf_hip_matmul_pair(const uint8_t* gw, int gt, int gne0, int gne1, size_
     const size_t obytes = (size_t)nb * gne1 * sizeof(float);
     bool ok = grow_device(c->dy, obytes) && grow_device(c->dy2, obytes) && grow_pinned(c->py, obytes) &&
               grow_pinned(c->py2, obytes) && stage_x(c, host_x, nb, gne0, ldx);
-    if (ok) ok = hip_ok(launch_matmul(gt, gw, gne0, gne1, grb, (const float*)c->dx.p, nb, gne0, (float*)c->dy.p, gne1,
-                                      c->stream), "gate launch");
-    if (ok) ok = hip_ok(launch_matmul(ut, uw, une0, une1, urb, (const float*)c->dx.p, nb, une0, (float*)c->dy2.p,
-                                      une1, c->stream), "up launch");
+    if (ok) ok = hip_ok(matmul_launch(c, gt, gw, gne0, gne1, grb, nb, (float*)c->dy.p), "gate launch");
+    if (ok) ok = hip_ok(matmul_launch(c, ut, uw, une0, une1, urb, nb, (float*)c->dy2.p), "up launch");
     if (ok) ok = hip_ok(hipMemcpyAsync(c->py.p, c->dy.p, obytes, hipMemcpyDeviceToHost, c->stream), "copy g");
     if (ok) ok = hip_ok(hipMemcpyAsync(c->py2.p, c->dy2.p, obytes, hipMemcpyDeviceToHost, c->stream), "copy u");
     ok = drain(c, ok);
@@ -717,6 +724,8 @@ int eahmmf_hip_set_grouped_wave_max(int max_tokens) { return set_grouped_wave_ma
 
 int eahmmf_hip_set_grouped_dot_max(int max_tokens) { return set_grouped_dot_max(max_tokens); }
 
+int eahmmf_hip_set_dense_mfma(int on) { return set_dense_mfma(on); }
+
 int eahmmf_hip_set_fused(int enable) {
     const int prev = fused_enabled() ? 1 : 0;
     if (enable >= 0) g_fused = enable ? 1 : 0;
@@ -911,7 +920,7 @@ void eahmmf_hip_shutdown(void) {
     if (it == g_ctx.end()) return;
     DevCtx& c = it->second;
     if (c.stream) (void)hipStreamSynchronize(c.stream);
-    for (DeviceBuf* b : {&c.dx, &c.dy, &c.dy2, &c.dh, &c.dids, &c.dw, &c.dyp, &c.dhx, &c.dgs, &c.dtab})
+    for (DeviceBuf* b : {&c.dx, &c.dy, &c.dy2, &c.dh, &c.dids, &c.dw, &c.dyp, &c.dhx, &c.dgs, &c.dtab, &c.drt, &c.dws})
         if (b->p) (void)hipFree(b->p);
     for (DeviceBuf* b : {&c.px, &c.py, &c.py2})
         if (b->p) (void)hipHostFree(b->p);

@@ -40,6 +40,20 @@ hipError_t launch_dequant(int type, const uint8_t* w, int64_t ne0, int64_t nrows
                           hipStream_t st);
 hipError_t launch_matmul(int type, const uint8_t* w, int ne0, int ne1, size_t row_bytes, const float* x, int nb,
                          int ldx, float* out, int ldo, hipStream_t st);
+// The same product on the matrix cores for 2..kMaxMfmaMatmulTokens tokens of
+// Q4_K / Q5_K / Q6_K / Q8_0 rows with ne0 % 256 == 0 (kernels_dense_mfma.hip);
+// ws: device workspace of matmul_mfma_ws_bytes(ne0, ne1, nb) bytes, 256-byte
+// aligned.  launch_matmul_auto takes that path when matmul_mfma_ok, the
+// switch is on and ws is large enough, else launch_matmul.
+constexpr int kMaxMfmaMatmulTokens = 64;
+bool matmul_mfma_ok(int type, const uint8_t* w, int ne0, size_t row_bytes, const float* x, int nb, int ldx);
+size_t matmul_mfma_ws_bytes(int ne0, int ne1, int nb);
+hipError_t launch_matmul_mfma(int type, const uint8_t* w, int ne0, int ne1, size_t row_bytes, const float* x, int nb,
+                              int ldx, float* out, int ldo, void* ws, size_t ws_bytes, hipStream_t st);
+hipError_t launch_matmul_auto(int type, const uint8_t* w, int ne0, int ne1, size_t row_bytes, const float* x, int nb,
+                              int ldx, float* out, int ldo, void* ws, size_t ws_bytes, hipStream_t st);
+bool dense_mfma_enabled();
+int set_dense_mfma(int on);  // returns the previous setting
 
 // Fused single-token decode: h[k][FF] scratch, y[D] = sum_j w_j down_j(silu(gate_j x) * up_j x).
 hipError_t launch_moe_decode(const MoeShape& s, const DecodeSlots& slots, const float* x, float* h, float* y,
@@ -201,6 +215,14 @@ bool attention_supported(int n_head, int n_kv, int hd);
 hipError_t launch_attention(const float* q, const float* k, const float* v, const float* q_norm, const float* k_norm,
                             const float* rope, float* kc, float* vc, float* out, int nb, int n_head, int n_kv, int hd,
                             int p0, float eps, float scale, float* part, unsigned* cnt, hipStream_t st);
+// The same for nb tokens of nb different sequences: token t is at position
+// tpos[t] (device) of the sequence whose cache rows start tseq[t] (device) *
+// seq_stride floats past kc / vc, and attends to that sequence's rows
+// 0 .. tpos[t]; max_pos >= every tpos[t] sizes the splits.
+hipError_t launch_attention_multi(const float* q, const float* k, const float* v, const float* q_norm,
+                                  const float* k_norm, const float* rope, float* kc, float* vc, float* out, int nb,
+                                  int n_head, int n_kv, int hd, const int* tpos, const int* tseq, size_t seq_stride,
+                                  int max_pos, float eps, float scale, float* part, unsigned* cnt, hipStream_t st);
 // Single-token matrix-vector products with fused input and output steps
 // (kernels_gemv.hip).  Up to three weight matrices of one type and row
 // length; out[r] = (resid ? resid[r] : 0) + sum_i W[r][i] * in[i] where

@@ -126,6 +126,12 @@ struct AttnArgs {
     float* part;
     unsigned* cnt;
     int n_head, n_kv, p0, n_split, span;  // span: positions per split
+    // several sequences, one token each (null for one sequence's batch):
+    // token t is at position tpos[t] of the sequence whose cache starts
+    // tseq[t] * seq_stride floats past kc / vc
+    const int* tpos;
+    const int* tseq;
+    size_t seq_stride;
     float eps, scale;
 };
 
@@ -198,20 +204,27 @@ __global__ __launch_bounds__((AttnShape<HD, GRP>::W * 64)) void attention_kernel
     const int t = blockIdx.x / n_kv, kvh = blockIdx.x % n_kv, s = blockIdx.y;
     const int tid = threadIdx.x, w = __builtin_amdgcn_readfirstlane(tid / 64), lane = tid % 64;
     const int h = lane / LPH, g = lane % LPH, d0 = g * DPL;
-    const int np = a.p0 + t + 1;
+    // the token's batch starts at pfirst (its own sequence); the token sits at own
+    const bool multi = a.tpos != nullptr;
+    const int pfirst = multi ? a.tpos[t] : a.p0;
+    const int own = multi ? pfirst : a.p0 + t;
+    const size_t sbase = multi ? (size_t)a.tseq[t] * a.seq_stride : 0;
+    float* const kc = a.kc + sbase;
+    float* const vc = a.vc + sbase;
+    const int np = own + 1;
     const int pos0 = s * a.span, pos1 = min(pos0 + a.span, np);
-    const int old_end = min(pos1, a.p0);  // cached rows end here
-    const int safe = 0;                   // a row that always exists (its data is not used)
+    const int old_end = min(pos1, pfirst);  // cached rows end here
+    const int safe = 0;                     // a row that always exists (its data is not used)
     float* slots = smem + w * 2 * S::SLOT;
     int c0 = pos0 + w * C;
-    if (c0 < pos1) issue_chunk<HD, GRP>(a.kc, a.vc, KD, kvh, c0, old_end, safe, slots, lane);
+    if (c0 < pos1) issue_chunk<HD, GRP>(kc, vc, KD, kvh, c0, old_end, safe, slots, lane);
     // query head (kvh * GRP + h), normed and rotated at the token's position
     float q[DPL];
     {
         const float* src = a.q + (size_t)t * QD + (size_t)(kvh * GRP + h) * HD + d0;
 #pragma unroll
         for (int e = 0; e < DPL; e++) q[e] = src[e];
-        norm_rope<HD, LPH, DPL>(q, a.q_norm, a.rope + (size_t)(a.p0 + t) * HD, a.eps, g);
+        norm_rope<HD, LPH, DPL>(q, a.q_norm, a.rope + (size_t)own * HD, a.eps, g);
     }
     float o[DPL];
 #pragma unroll
@@ -220,8 +233,7 @@ __global__ __launch_bounds__((AttnShape<HD, GRP>::W * 64)) void attention_kernel
     for (int k = 0; c0 < pos1; c0 += W * C, k++) {
         float* cur = slots + (k & 1) * S::SLOT;
         if (c0 + W * C < pos1) {
-            issue_chunk<HD, GRP>(a.kc, a.vc, KD, kvh, c0 + W * C, old_end, safe, slots + ((k + 1) & 1) * S::SLOT,
-                                 lane);
+            issue_chunk<HD, GRP>(kc, vc, KD, kvh, c0 + W * C, old_end, safe, slots + ((k + 1) & 1) * S::SLOT, lane);
             wait_vm_upto<S::NI>();
         } else {
             wait_vm();
@@ -229,7 +241,7 @@ __global__ __launch_bounds__((AttnShape<HD, GRP>::W * 64)) void attention_kernel
         const int nc = min(C, pos1 - c0);
         // the batch's own rows of this chunk: normed, rotated, into the slot
         for (int j = max(0, old_end - c0); j < nc; j++) {
-            const int pos = c0 + j, tt = pos - a.p0;
+            const int pos = c0 + j, tt = multi ? t : pos - a.p0;  // (a single-token batch: its own row)
             float kr[DPL], vr[DPL];
             const float* kp = a.k + (size_t)tt * KD + kvh * HD + d0;
             const float* vp = a.v + (size_t)tt * KD + kvh * HD + d0;
@@ -248,8 +260,8 @@ __global__ __launch_bounds__((AttnShape<HD, GRP>::W * 64)) void attention_kernel
                 if (pos == np - 1) {  // this token's own row: one block stores it
 #pragma unroll
                     for (int e = 0; e < DPL; e++) {
-                        a.kc[(size_t)pos * KD + kvh * HD + d0 + e] = kr[e];
-                        a.vc[(size_t)pos * KD + kvh * HD + d0 + e] = vr[e];
+                        kc[(size_t)pos * KD + kvh * HD + d0 + e] = kr[e];
+                        vc[(size_t)pos * KD + kvh * HD + d0 + e] = vr[e];
                     }
                 }
             }
@@ -439,10 +451,29 @@ hipError_t launch_attention(const float* q, const float* k, const float* v, cons
                             const float* rope, float* kc, float* vc, float* out, int nb, int n_head, int n_kv, int hd,
                             int p0, float eps, float scale, float* part, unsigned* cnt, hipStream_t st) {
     if (!attention_supported(n_head, n_kv, hd) || nb <= 0 || p0 < 0) return hipErrorInvalidValue;
-    AttnArgs a{q, k, v, q_norm, k_norm, rope, kc, vc, out, part, cnt, n_head, n_kv, p0, 0, 0, eps, scale};
+    AttnArgs a{q, k, v, q_norm, k_norm, rope, kc, vc, out, part, cnt, n_head, n_kv, p0, 0, 0, nullptr, nullptr, 0,
+               eps, scale};
     // splits of at least kMinSplitPos positions, at most kMaxSplit (the
     // merge reads one record per split in a single round)
     const int n_pos = p0 + nb;  // of the last token
+    int n_split = (n_pos + kMinSplitPos - 1) / kMinSplitPos;
+    if (n_split > kMaxSplit) n_split = kMaxSplit;
+    a.span = (n_pos + n_split - 1) / n_split;
+    a.n_split = (n_pos + a.span - 1) / a.span;
+    clear_stale_error();
+    const bool ok = hd == 64 ? attn_dispatch<64>(a, n_head / n_kv, nb, st) : attn_dispatch<128>(a, n_head / n_kv, nb, st);
+    if (!ok) return hipErrorInvalidValue;
+    return hipGetLastError();
+}
+
+hipError_t launch_attention_multi(const float* q, const float* k, const float* v, const float* q_norm,
+                                  const float* k_norm, const float* rope, float* kc, float* vc, float* out, int nb,
+                                  int n_head, int n_kv, int hd, const int* tpos, const int* tseq, size_t seq_stride,
+                                  int max_pos, float eps, float scale, float* part, unsigned* cnt, hipStream_t st) {
+    if (!attention_supported(n_head, n_kv, hd) || nb <= 0 || max_pos < 0 || !tpos || !tseq) return hipErrorInvalidValue;
+    AttnArgs a{q, k, v, q_norm, k_norm, rope, kc, vc, out, part, cnt, n_head, n_kv, 0, 0, 0, tpos, tseq, seq_stride,
+               eps, scale};
+    const int n_pos = max_pos + 1;  // positions of the longest sequence, its new token included
     int n_split = (n_pos + kMinSplitPos - 1) / kMinSplitPos;
     if (n_split > kMaxSplit) n_split = kMaxSplit;
     a.span = (n_pos + n_split - 1) / n_split;

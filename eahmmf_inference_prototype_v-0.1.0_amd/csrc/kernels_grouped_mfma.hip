@@ -30,20 +30,6 @@
 
 namespace eahmmf {
 
-// Workgroup barrier for LDS hand-offs only.  __syncthreads() carries a
-// workgroup release fence, which on this target waits for every outstanding
-// vector-memory operation, loads included (s_waitcnt vmcnt(0)), and so would
-// stall on the next chunk's prefetch at every barrier.  This one waits for
-// this wave's LDS operations (lgkmcnt 0; vmcnt and expcnt left at their
-// maxima), then meets the other waves; global data is consumed only through
-// its own registers, so no global ordering is needed here.
-__device__ __forceinline__ void lds_barrier() {
-    __atomic_signal_fence(__ATOMIC_SEQ_CST);
-    __builtin_amdgcn_s_waitcnt(0xC07F);
-    __builtin_amdgcn_s_barrier();
-    __atomic_signal_fence(__ATOMIC_SEQ_CST);
-}
-
 // ---------------------------------------------------------------------------
 // Activation rows -> scaled fp16 hi/lo (+ 32-value sums).  One workgroup per
 // position q < offs[E]; the row is src + (tok ? tok[q] : q) * ld, n values.

@@ -53,6 +53,20 @@ __device__ __forceinline__ f32x4 mfma(f16x8 a, f16x8 b, f32x4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
 }
 
+// Workgroup barrier for LDS hand-offs only.  __syncthreads() carries a
+// workgroup release fence, which on this target waits for every outstanding
+// vector-memory operation, loads included (s_waitcnt vmcnt(0)), and so would
+// stall on the next chunk's prefetch at every barrier.  This one waits for
+// this wave's LDS operations (lgkmcnt 0; vmcnt and expcnt left at their
+// maxima), then meets the other waves; global data is consumed only through
+// its own registers, so no global ordering is needed here.
+__device__ __forceinline__ void lds_barrier() {
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __builtin_amdgcn_s_waitcnt(0xC07F);
+    __builtin_amdgcn_s_barrier();
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+
 __device__ __forceinline__ float half_at(const uint8_t* p) {  // a weight row's fp16 scale (global)
     return (float)__builtin_bit_cast(_Float16, *(const __attribute__((address_space(1))) uint16_t*)p);
 }

@@ -16,6 +16,8 @@
 // waits once per forward, for the logits, the trace and the error words.
 #include <math.h>
 #include <stdarg.h>
+
+#include <algorithm>
 #include <stdio.h>
 #include <string.h>
 
@@ -72,11 +74,18 @@ struct Model {
     float *rope, *kc, *vc, *x, *h, *xn, *q, *k, *v, *att, *tmp, *rl, *logits, *part;
     unsigned long long* key;  // argmax key of the greedy loop
     int *toks, *ids, *bad, *gen;
+    // sequences: KV cache [n_layer][n_seq][n_ctx][KD]; a decode step over
+    // several sequences takes token t at position tpos[t] of sequence tseq[t]
+    // (device arrays beside toks) and leaves logits [t][V] (lg_rows rows)
+    int n_seq = 1, lg_rows = 1;
+    int *tpos, *tseq;
+    void* ws = nullptr;  // workspace of the batched matrix-core matmuls
+    size_t ws_bytes = 0;
     float* wts;
     unsigned* cnt;
     // pinned host staging
     int* h_toks = nullptr;
-    float* h_logits = nullptr;
+    float* h_logits = nullptr;  // [lg_rows][V]
     int* h_ids = nullptr;
     float* h_w = nullptr;
     unsigned* h_status = nullptr;  // [0] before, [1] after; [2] bad-token flag
@@ -165,8 +174,25 @@ void release(Model* m) {
     delete m;
 }
 
-bool mm(const Tens& w, const float* x, int nb, int ldx, float* out, int ldo, hipStream_t st, const char* what) {
-    return ok(launch_matmul(w.type, w.p, (int)w.ne0, (int)w.ne1, w.rb, x, nb, ldx, out, ldo, st), what);
+bool mm(Model* m, const Tens& w, const float* x, int nb, int ldx, float* out, int ldo, hipStream_t st,
+        const char* what) {
+    return ok(launch_matmul_auto(w.type, w.p, (int)w.ne0, (int)w.ne1, w.rb, x, nb, ldx, out, ldo, m->ws, m->ws_bytes,
+                                 st),
+              what);
+}
+
+// Workspace for the batched matmuls of every matrix the model multiplies
+// with nb = 2..kMaxBatch tokens.
+size_t mm_ws_bytes(const Model* m) {
+    size_t need = 0;
+    auto fit = [&](const Tens& w) {
+        for (int nb = 2; nb <= kMaxBatch && nb <= kMaxMfmaMatmulTokens; nb++)
+            if (w.ne0 % 256 == 0) need = std::max(need, matmul_mfma_ws_bytes((int)w.ne0, (int)w.ne1, nb));
+    };
+    for (const LayerDev& L : m->L)
+        for (const Tens* w : {&L.wq, &L.wk, &L.wv, &L.wo, &L.router}) fit(*w);
+    fit(m->out);
+    return need;
 }
 
 // out = W in with the input formed in the kernel (kernels_gemv.hip).
@@ -204,12 +230,24 @@ bool gemv_qkv(Model* m, const LayerDev& L, GemvArgs g, hipStream_t st) {
     return gemv1(L.wk, g, m->k, nullptr, st, "k projection") && gemv1(L.wv, g, m->v, nullptr, st, "v projection");
 }
 
-bool attention(Model* m, int l, int nb, int p0, hipStream_t st) {
+size_t seq_floats(const Model* m) { return (size_t)m->n_ctx * m->KD; }
+
+// nb tokens of sequence `seq` at p0..
+bool attention(Model* m, int l, int nb, int p0, int seq, hipStream_t st) {
     const LayerDev& L = m->L[l];
-    float* kc = m->kc + (size_t)l * m->n_ctx * m->KD;
-    float* vc = m->vc + (size_t)l * m->n_ctx * m->KD;
-    return ok(launch_attention(m->q, m->k, m->v, L.q_norm, L.k_norm, m->rope, kc, vc, m->att, nb, m->n_head, m->n_kv,
-                               m->hd, p0, m->eps, m->scale, m->part, m->cnt, st),
+    const size_t off = ((size_t)l * m->n_seq + seq) * seq_floats(m);
+    return ok(launch_attention(m->q, m->k, m->v, L.q_norm, L.k_norm, m->rope, m->kc + off, m->vc + off, m->att, nb,
+                               m->n_head, m->n_kv, m->hd, p0, m->eps, m->scale, m->part, m->cnt, st),
+              "attention");
+}
+
+// one token each of nb sequences (m->tpos / m->tseq), positions up to max_pos
+bool attention_seqs(Model* m, int l, int nb, int max_pos, hipStream_t st) {
+    const LayerDev& L = m->L[l];
+    const size_t off = (size_t)l * m->n_seq * seq_floats(m);
+    return ok(launch_attention_multi(m->q, m->k, m->v, L.q_norm, L.k_norm, m->rope, m->kc + off, m->vc + off, m->att,
+                                     nb, m->n_head, m->n_kv, m->hd, m->tpos, m->tseq, seq_floats(m), max_pos, m->eps,
+                                     m->scale, m->part, m->cnt, st),
               "attention");
 }
 
@@ -220,13 +258,13 @@ bool attention(Model* m, int l, int nb, int p0, hipStream_t st) {
 //   QKV(r or h + y, norm) -> attention -> O-proj (+ r) -> h
 //   -> router(norm h; block 0 stores the normalized h) -> expert block -> y
 // amax: the output head also tracks the argmax key when set.
-bool enqueue_decode(Model* m, int p0, bool want_logits, unsigned long long* amax) {
+bool enqueue_decode(Model* m, int p0, int seq, bool want_logits, unsigned long long* amax) {
     hipStream_t st = m->st;
     for (int l = 0; l < m->n_layer; l++) {
         const LayerDev& L = m->L[l];
         GemvArgs g = l == 0 ? gemv_in(m->x, nullptr, L.attn_norm, m->eps) : gemv_in(m->h, m->tmp, L.attn_norm, m->eps);
         if (l > 0) g.x_sum_out = m->x;
-        if (!gemv_qkv(m, L, g, st) || !attention(m, l, 1, p0, st) ||
+        if (!gemv_qkv(m, L, g, st) || !attention(m, l, 1, p0, seq, st) ||
             !gemv1(L.wo, gemv_in(m->att, nullptr, nullptr, 0.f), m->h, m->x, st, "output projection"))
             return false;
         GemvArgs gr = gemv_in(m->h, nullptr, L.ffn_norm, m->eps);
@@ -244,8 +282,11 @@ bool enqueue_decode(Model* m, int p0, bool want_logits, unsigned long long* amax
 }
 
 // A batch of nb > 1 tokens: per-step kernels over the batch (norm, the
-// matmul kernel, attention, add, routing + the grouped expert block).
-bool enqueue_batch(Model* m, int nb, int p0, bool want_logits) {
+// matmul kernel, attention, add, routing + the grouped expert block).  The
+// tokens are nb consecutive positions p0.. of sequence seq, or (seqs) one
+// token of each of nb sequences (m->tpos / m->tseq, positions up to
+// max_pos), whose logits all come out ([nb][V]).
+bool enqueue_batch(Model* m, int nb, int p0, int seq, bool want_logits, bool seqs = false, int max_pos = 0) {
     hipStream_t st = m->st;
     const int D = m->D;
     for (int l = 0; l < m->n_layer; l++) {
@@ -253,13 +294,14 @@ bool enqueue_batch(Model* m, int nb, int p0, bool want_logits) {
         int* ids = m->ids + (size_t)l * kMaxBatch * m->K;
         float* wts = m->wts + (size_t)l * kMaxBatch * m->K;
         if (!ok(launch_rmsnorm(m->x, L.attn_norm, m->xn, nb, D, m->eps, st), "attn rmsnorm") ||
-            !mm(L.wq, m->xn, nb, D, m->q, m->QD, st, "q matmul") ||
-            !mm(L.wk, m->xn, nb, D, m->k, m->KD, st, "k matmul") ||
-            !mm(L.wv, m->xn, nb, D, m->v, m->KD, st, "v matmul") || !attention(m, l, nb, p0, st) ||
-            !mm(L.wo, m->att, nb, m->QD, m->tmp, D, st, "output matmul") ||
+            !mm(m, L.wq, m->xn, nb, D, m->q, m->QD, st, "q matmul") ||
+            !mm(m, L.wk, m->xn, nb, D, m->k, m->KD, st, "k matmul") ||
+            !mm(m, L.wv, m->xn, nb, D, m->v, m->KD, st, "v matmul") ||
+            !(seqs ? attention_seqs(m, l, nb, max_pos, st) : attention(m, l, nb, p0, seq, st)) ||
+            !mm(m, L.wo, m->att, nb, m->QD, m->tmp, D, st, "output matmul") ||
             !ok(launch_add(m->x, m->tmp, (size_t)nb * D, st), "residual add") ||
             !ok(launch_rmsnorm(m->x, L.ffn_norm, m->xn, nb, D, m->eps, st), "ffn rmsnorm") ||
-            !mm(L.router, m->xn, nb, D, m->rl, m->E, st, "router matmul"))
+            !mm(m, L.router, m->xn, nb, D, m->rl, m->E, st, "router matmul"))
             return false;
         if (eahmmf_hip_route_topk_async(m->rl, nb, m->E, m->K, ids, wts, st) != 0 ||
             eahmmf_hip_moe_grouped_async(&L.shape, L.table, m->E, ids, wts, nb, m->K, m->xn, m->tmp, st) != 0)
@@ -267,6 +309,9 @@ bool enqueue_batch(Model* m, int nb, int p0, bool want_logits) {
         if (!ok(launch_add(m->x, m->tmp, (size_t)nb * D, st), "residual add")) return false;
     }
     if (!want_logits) return true;
+    if (seqs)
+        return ok(launch_rmsnorm(m->x, m->out_norm, m->xn, nb, D, m->eps, st), "output rmsnorm") &&
+               mm(m, m->out, m->xn, nb, D, m->logits, m->V, st, "output head");
     return gemv1(m->out, gemv_in(m->x + (size_t)(nb - 1) * D, nullptr, m->out_norm, m->eps), m->logits, nullptr, st,
                  "output head");
 }
@@ -274,13 +319,13 @@ bool enqueue_batch(Model* m, int nb, int p0, bool want_logits) {
 // Enqueues one forward of nb tokens at positions p0...: ids from toks (device)
 // or, when key is set (nb = 1), the argmax held in the key, which the
 // embedding step clears and also stores in hist when given.
-bool enqueue_forward(Model* m, const int* toks, unsigned long long* key, int* hist, int nb, int p0, bool want_logits,
-                     unsigned long long* amax) {
+bool enqueue_forward(Model* m, const int* toks, unsigned long long* key, int* hist, int nb, int p0, int seq,
+                     bool want_logits, unsigned long long* amax) {
     if (!ok(launch_embed(m->tok.type, m->tok.p, m->tok.rb, (int)m->tok.ne1, m->D, toks, key, hist, nb, m->x, m->bad,
                          m->st),
             "embed"))
         return false;
-    return nb == 1 ? enqueue_decode(m, p0, want_logits, amax) : enqueue_batch(m, nb, p0, want_logits);
+    return nb == 1 ? enqueue_decode(m, p0, seq, want_logits, amax) : enqueue_batch(m, nb, p0, seq, want_logits);
 }
 
 // Queues the error-word and bad-token reads, waits, and judges the forward.
@@ -322,8 +367,9 @@ bool queue_trace_read(Model* m) {
            ok(hipMemcpyAsync(m->h_w, m->wts, n * sizeof(float), hipMemcpyDeviceToHost, m->st), "read trace");
 }
 
-int forward(Model* m, const int* toks, int nb, int p0, float* logits) {
+int forward(Model* m, const int* toks, int nb, int p0, int seq, float* logits) {
     if (nb < 1 || nb > kMaxBatch) return fail("batch size %d outside 1..%d", nb, kMaxBatch), -1;
+    if (seq < 0 || seq >= m->n_seq) return fail("sequence %d outside 0..%d", seq, m->n_seq - 1), -1;
     if (p0 < 0 || p0 + nb > m->n_ctx) return fail("context overflow (%d > %d)", p0 + nb, m->n_ctx), -1;
     for (int t = 0; t < nb; t++)
         if (toks[t] < 0 || toks[t] >= (int)m->tok.ne1) return fail("token id %d out of range", toks[t]), -1;
@@ -331,7 +377,7 @@ int forward(Model* m, const int* toks, int nb, int p0, float* logits) {
     memcpy(m->h_toks, toks, sizeof(int) * nb);
     bool e = begin(m) &&
              ok(hipMemcpyAsync(m->toks, m->h_toks, sizeof(int) * nb, hipMemcpyHostToDevice, m->st), "copy tokens") &&
-             enqueue_forward(m, m->toks, nullptr, nullptr, nb, p0, logits != nullptr, nullptr);
+             enqueue_forward(m, m->toks, nullptr, nullptr, nb, p0, seq, logits != nullptr, nullptr);
     if (e && logits)
         e = ok(hipMemcpyAsync(m->h_logits, m->logits, sizeof(float) * m->V, hipMemcpyDeviceToHost, m->st),
                "read logits");
@@ -339,6 +385,40 @@ int forward(Model* m, const int* toks, int nb, int p0, float* logits) {
     if (!finish(m, e)) return -3;
     if (logits) memcpy(logits, m->h_logits, sizeof(float) * m->V);
     if (m->trace) record_trace(m, nb);
+    return 0;
+}
+
+// One token of each of n distinct sequences; logits [n][V] when given.
+int decode_seqs(Model* m, int n, const int* toks, const int* seqs, const int* pos, float* logits) {
+    if (n < 1 || n > m->n_seq) return fail("sequence count %d outside 1..%d", n, m->n_seq), -1;
+    int max_pos = 0;
+    for (int t = 0; t < n; t++) {
+        if (toks[t] < 0 || toks[t] >= (int)m->tok.ne1) return fail("token id %d out of range", toks[t]), -1;
+        if (seqs[t] < 0 || seqs[t] >= m->n_seq) return fail("sequence %d outside 0..%d", seqs[t], m->n_seq - 1), -1;
+        if (pos[t] < 0 || pos[t] >= m->n_ctx) return fail("context overflow (%d > %d)", pos[t] + 1, m->n_ctx), -1;
+        for (int u = 0; u < t; u++)
+            if (seqs[u] == seqs[t]) return fail("sequence %d given twice in one step", seqs[t]), -1;
+        max_pos = pos[t] > max_pos ? pos[t] : max_pos;
+    }
+    DeviceGuard g(m->dev);
+    // tokens, positions and sequences staged together (m->tpos / m->tseq follow m->toks)
+    memcpy(m->h_toks, toks, sizeof(int) * n);
+    memcpy(m->h_toks + kMaxBatch, pos, sizeof(int) * n);
+    memcpy(m->h_toks + 2 * kMaxBatch, seqs, sizeof(int) * n);
+    bool e = begin(m) &&
+             ok(hipMemcpyAsync(m->toks, m->h_toks, sizeof(int) * 3 * kMaxBatch, hipMemcpyHostToDevice, m->st),
+                "copy tokens") &&
+             ok(launch_embed(m->tok.type, m->tok.p, m->tok.rb, (int)m->tok.ne1, m->D, m->toks, nullptr, nullptr, n,
+                             m->x, m->bad, m->st),
+                "embed") &&
+             enqueue_batch(m, n, 0, 0, logits != nullptr, true, max_pos);
+    if (e && logits)
+        e = ok(hipMemcpyAsync(m->h_logits, m->logits, sizeof(float) * n * m->V, hipMemcpyDeviceToHost, m->st),
+               "read logits");
+    if (e && m->trace) e = queue_trace_read(m);
+    if (!finish(m, e)) return -3;
+    if (logits) memcpy(logits, m->h_logits, sizeof(float) * n * m->V);
+    if (m->trace) record_trace(m, n);
     return 0;
 }
 
@@ -442,10 +522,10 @@ void* eahmmf_hip_model_create(const eahmmf_hip_model_desc* d) {
     m->att = (float*)dalloc(m, (size_t)B * m->QD * 4, false);
     m->tmp = (float*)dalloc(m, (size_t)B * D * 4, false);
     m->rl = (float*)dalloc(m, (size_t)B * E * 4, false);
-    m->logits = (float*)dalloc(m, (size_t)m->V * 4, false);
+    m->logits = (float*)dalloc(m, (size_t)m->V * 4, false);  // one row until more sequences are set
     m->part = (float*)dalloc(m, attention_part_floats(B, m->n_head, m->hd, m->n_ctx) * 4, false);
     m->cnt = (unsigned*)dalloc(m, (size_t)B * m->n_kv * 4, true);
-    m->toks = (int*)dalloc(m, (size_t)B * 4, false);
+    m->toks = (int*)dalloc(m, (size_t)3 * B * 4, false);  // tokens, then positions, then sequences
     m->ids = (int*)dalloc(m, (size_t)m->n_layer * B * Kk * 4, true);
     m->wts = (float*)dalloc(m, (size_t)m->n_layer * B * Kk * 4, true);
     m->bad = (int*)dalloc(m, 4, true);
@@ -453,10 +533,14 @@ void* eahmmf_hip_model_create(const eahmmf_hip_model_desc* d) {
     if (!m->rope || !m->kc || !m->vc || !m->x || !m->xn || !m->h || !m->key || !m->q || !m->k || !m->v || !m->att || !m->tmp || !m->rl ||
         !m->logits || !m->part || !m->cnt || !m->toks || !m->ids || !m->wts || !m->bad || !m->gen)
         return release(m), nullptr;
+    m->tpos = m->toks + B;
+    m->tseq = m->toks + 2 * B;
+    m->ws_bytes = mm_ws_bytes(m);
+    if (m->ws_bytes && !(m->ws = dalloc(m, m->ws_bytes, false))) return release(m), nullptr;
     if (!ok(hipMemcpy(m->rope, rope.data(), rope.size() * sizeof(float), hipMemcpyHostToDevice), "copy rope"))
         return release(m), nullptr;
     const size_t trn = (size_t)m->n_layer * B * Kk;
-    if (!ok(hipHostMalloc((void**)&m->h_toks, B * sizeof(int), 0), "hipHostMalloc") ||
+    if (!ok(hipHostMalloc((void**)&m->h_toks, 3 * B * sizeof(int), 0), "hipHostMalloc") ||
         !ok(hipHostMalloc((void**)&m->h_logits, (size_t)m->V * sizeof(float), 0), "hipHostMalloc") ||
         !ok(hipHostMalloc((void**)&m->h_ids, trn * sizeof(int), 0), "hipHostMalloc") ||
         !ok(hipHostMalloc((void**)&m->h_w, trn * sizeof(float), 0), "hipHostMalloc") ||
@@ -467,7 +551,66 @@ void* eahmmf_hip_model_create(const eahmmf_hip_model_desc* d) {
 
 int eahmmf_hip_model_forward(void* model, const int* toks, int nb, int p0, float* logits) {
     if (!model || !toks) return fail("null argument"), -1;
-    return forward(static_cast<Model*>(model), toks, nb, p0, logits);
+    return forward(static_cast<Model*>(model), toks, nb, p0, 0, logits);
+}
+
+int eahmmf_hip_model_set_sequences(void* model, int n_seq) {
+    Model* m = static_cast<Model*>(model);
+    if (!m) return fail("null model"), -1;
+    if (n_seq < 1 || n_seq > kMaxBatch) return fail("sequence count %d outside 1..%d", n_seq, kMaxBatch), -1;
+    DeviceGuard g(m->dev);
+    if (!ok(hipStreamSynchronize(m->st), "model stream")) return -3;
+    const size_t kvn = (size_t)m->n_layer * n_seq * seq_floats(m);
+    float* kc = (float*)dalloc(m, kvn * sizeof(float), true);
+    float* vc = kc ? (float*)dalloc(m, kvn * sizeof(float), true) : nullptr;
+    float* lg = nullptr;
+    float* hlg = nullptr;
+    const int rows = n_seq > m->lg_rows ? n_seq : m->lg_rows;
+    if (vc && rows > m->lg_rows) {
+        lg = (float*)dalloc(m, (size_t)rows * m->V * 4, false);
+        if (lg && !ok(hipHostMalloc((void**)&hlg, (size_t)rows * m->V * sizeof(float), 0), "hipHostMalloc"))
+            hlg = nullptr;
+    }
+    // drops device allocations made here or replaced (they are in m->owned)
+    auto drop = [m](void* p) {
+        if (!p) return;
+        for (size_t i = 0; i < m->owned.size(); i++)
+            if (m->owned[i] == p) {
+                m->owned.erase(m->owned.begin() + i);
+                break;
+            }
+        (void)hipFree(p);
+    };
+    if (!kc || !vc || (rows > m->lg_rows && (!lg || !hlg))) {
+        drop(kc);
+        drop(vc);
+        drop(lg);
+        return -3;  // dalloc / hipHostMalloc set the message; the model is as it was
+    }
+    drop(m->kc);
+    drop(m->vc);
+    m->kc = kc;
+    m->vc = vc;
+    if (lg) {
+        drop(m->logits);
+        (void)hipHostFree(m->h_logits);
+        m->logits = lg;
+        m->h_logits = hlg;
+        m->lg_rows = rows;
+    }
+    m->n_seq = n_seq;
+    return 0;
+}
+
+int eahmmf_hip_model_forward_seq(void* model, int seq, const int* toks, int nb, int p0, float* logits) {
+    if (!model || !toks) return fail("null argument"), -1;
+    return forward(static_cast<Model*>(model), toks, nb, p0, seq, logits);
+}
+
+int eahmmf_hip_model_decode_seqs(void* model, int n, const int* toks, const int* seqs, const int* pos,
+                                 float* logits) {
+    if (!model || !toks || !seqs || !pos) return fail("null argument"), -1;
+    return decode_seqs(static_cast<Model*>(model), n, toks, seqs, pos, logits);
 }
 
 int eahmmf_hip_model_eval(void* model, const int* toks, int n, int p0, int n_batch, float* logits) {
@@ -476,7 +619,7 @@ int eahmmf_hip_model_eval(void* model, const int* toks, int n, int p0, int n_bat
     Model* m = static_cast<Model*>(model);
     for (int i = 0; i < n; i += n_batch) {
         const int nb = n - i < n_batch ? n - i : n_batch;
-        const int rc = forward(m, toks + i, nb, p0 + i, i + nb == n ? logits : nullptr);
+        const int rc = forward(m, toks + i, nb, p0 + i, 0, i + nb == n ? logits : nullptr);
         if (rc) return rc;
     }
     return 0;
@@ -506,7 +649,7 @@ int eahmmf_hip_model_generate_greedy(void* model, int first, int p0, int n, int*
     // step i - 1, stored as output i - 1) and leaves its argmax in the key
     for (int i = 0; e && i < n; i++) {
         e = enqueue_forward(m, i == 0 ? m->toks : nullptr, i == 0 ? nullptr : m->key, i == 0 ? nullptr : m->gen + i - 1,
-                            1, p0 + i, true, m->key);
+                            1, p0 + i, 0, true, m->key);
         if (e && m->trace) {
             // the trace of this step is read before the next step overwrites it
             e = queue_trace_read(m) && ok(hipStreamSynchronize(m->st), "model stream");

@@ -28,7 +28,8 @@ EXPORTS = (
     "eahmmf_hip_moe_layer_decode_noalloc", "eahmmf_hip_expf_ref_async", "eahmmf_hip_moe_decode_resident",
     "eahmmf_hip_model_create", "eahmmf_hip_model_forward", "eahmmf_hip_model_eval", "eahmmf_hip_model_generate_greedy",
     "eahmmf_hip_model_set_trace", "eahmmf_hip_model_trace", "eahmmf_hip_model_trace_clear", "eahmmf_hip_model_stream",
-    "eahmmf_hip_model_free", "eahmmf_hip_moe_layer_decode_xn_async", "eahmmf_hip_set_grouped_wave_max",
+    "eahmmf_hip_model_free", "eahmmf_hip_model_set_sequences", "eahmmf_hip_model_forward_seq",
+    "eahmmf_hip_model_decode_seqs", "eahmmf_hip_set_dense_mfma", "eahmmf_hip_moe_layer_decode_xn_async", "eahmmf_hip_set_grouped_wave_max",
     "eahmmf_hip_set_grouped_dot_max",
 )
 
@@ -141,6 +142,10 @@ def load(path=LIB_PATH):
         "eahmmf_hip_model_trace_clear": (None, [vp]),
         "eahmmf_hip_model_stream": (vp, [vp]),
         "eahmmf_hip_model_free": (None, [vp]),
+        "eahmmf_hip_model_set_sequences": (c_int, [vp, c_int]),
+        "eahmmf_hip_model_forward_seq": (c_int, [vp, c_int, vp, c_int, c_int, vp]),
+        "eahmmf_hip_model_decode_seqs": (c_int, [vp, c_int, vp, vp, vp, vp]),
+        "eahmmf_hip_set_dense_mfma": (c_int, [c_int]),
         "eahmmf_hip_dequantize": (c_int, [vp, c_int, c_i64, c_i64, c_sz, vp, vp]),
         "eahmmf_hip_row_bytes": (c_sz, [c_int, c_i64]),
         "eahmmf_hip_quantize_rows": (c_i64, [c_int, vp, c_i64, c_i64, vp]),
@@ -245,22 +250,50 @@ class DeviceModel:
         if rc != 0:
             raise RuntimeError(f"{what} ({rc}): {last_error()}")
 
-    def forward(self, toks, p0, logits=True):
-        """Engine::forward: tokens at p0..; the last token's logits (or None)."""
+    def forward(self, toks, p0, logits=True, seq=0):
+        """Engine::forward on sequence ``seq``: tokens at p0..; the last
+        token's logits (or None)."""
         import numpy as np
         t = np.ascontiguousarray(toks, dtype=np.int32)
         out = np.empty(self.n_vocab, np.float32) if logits else None
-        self._check(self._lib.eahmmf_hip_model_forward(self.h, t.ctypes.data, len(t), int(p0),
-                                                       out.ctypes.data if logits else None), "forward")
+        self._check(self._lib.eahmmf_hip_model_forward_seq(self.h, int(seq), t.ctypes.data, len(t), int(p0),
+                                                           out.ctypes.data if logits else None), "forward")
         return out
 
-    def eval(self, toks, p0, n_batch):
-        """Engine::eval: chunks of n_batch from p0; the last token's logits."""
+    def eval(self, toks, p0, n_batch, seq=0):
+        """Engine::eval on sequence ``seq``: chunks of n_batch from p0; the
+        last token's logits."""
         import numpy as np
         t = np.ascontiguousarray(toks, dtype=np.int32)
         out = np.empty(self.n_vocab, np.float32)
-        self._check(self._lib.eahmmf_hip_model_eval(self.h, t.ctypes.data, len(t), int(p0), int(n_batch),
-                                                    out.ctypes.data), "eval")
+        if seq == 0:
+            self._check(self._lib.eahmmf_hip_model_eval(self.h, t.ctypes.data, len(t), int(p0), int(n_batch),
+                                                        out.ctypes.data), "eval")
+            return out
+        if not 1 <= int(n_batch) <= 64 or len(t) == 0:
+            raise ValueError("n_batch outside 1..64 or empty input")
+        nb = int(n_batch)
+        for i in range(0, len(t), nb):
+            lg = self.forward(t[i:i + nb], int(p0) + i, logits=i + nb >= len(t), seq=seq)
+        return lg
+
+    def set_sequences(self, n_seq):
+        """n_seq independent sequences (KV rows of their own), all empty."""
+        self._check(self._lib.eahmmf_hip_model_set_sequences(self.h, int(n_seq)), "set_sequences")
+
+    def decode_seqs(self, toks, seqs, pos, logits=True):
+        """One decode step of several sequences in one batch: token toks[i]
+        at position pos[i] of sequence seqs[i]; logits [n][n_vocab] (or None)."""
+        import numpy as np
+        t = np.ascontiguousarray(toks, dtype=np.int32)
+        s = np.ascontiguousarray(seqs, dtype=np.int32)
+        p = np.ascontiguousarray(pos, dtype=np.int32)
+        if not len(t) == len(s) == len(p):
+            raise ValueError("toks, seqs and pos differ in length")
+        out = np.empty((len(t), self.n_vocab), np.float32) if logits else None
+        self._check(self._lib.eahmmf_hip_model_decode_seqs(self.h, len(t), t.ctypes.data, s.ctypes.data,
+                                                           p.ctypes.data, out.ctypes.data if logits else None),
+                    "decode_seqs")
         return out
 
     def generate_greedy(self, first, p0, n):

@@ -292,6 +292,12 @@ int eahmmf_hip_set_grouped_wave_max(int max_tokens);
  * reported as 33: none).  A negative argument only queries.  Returns the
  * previous setting.  No counterpart in the reference. */
 int eahmmf_hip_set_grouped_dot_max(int max_tokens);
+/* Matrix-core path of the batched matmuls (the drop-in eahmmf_hip_matmul /
+ * _pair at 2..64 tokens and the model's projections and output head at
+ * batch 2..64) for Q4_K, Q5_K, Q6_K and Q8_0 rows of a multiple of 256
+ * values: 1 on (default), 0 the general kernel.  Returns the previous
+ * setting.  No counterpart in the reference (a switch for A/B checks). */
+int eahmmf_hip_set_dense_mfma(int on);
 /* The single-launch expert block's workgroups wait for each other's words
  * (h, per-partition partials).  Every wait is bounded; when one gives up the
  * launch writes NaN where the missing words were needed and records its
@@ -370,6 +376,28 @@ int eahmmf_hip_model_eval(void* model, const int* toks, int n, int p0, int n_bat
  * receives the n argmax tokens; last_logits (may be null) the final logits.
  * One synchronisation at the end.  Same return codes as forward. */
 int eahmmf_hip_model_generate_greedy(void* model, int first, int p0, int n, int* out_toks, float* last_logits);
+/* Sequences (the reference's Engine keeps one: a single KV cache
+ * [n_layer][n_ctx][KD] written at p0 + t, qwen3moe.cpp:791, 910-913, 969-971).
+ * Sets the model to n_seq (1..64) independent sequences, each with its own KV
+ * rows [n_layer][n_seq][n_ctx][KD]; every cache row is cleared (all sequences
+ * start empty).  Sequence 0 is the one forward / eval / generate_greedy use.
+ * Synchronous; 0, -1 bad count, -3 out of device memory (the model is then
+ * unchanged). */
+int eahmmf_hip_model_set_sequences(void* model, int n_seq);
+/* Engine::forward (qwen3moe.cpp:910-913) on sequence seq: nb tokens at
+ * positions p0 .. p0+nb-1 of that sequence; same arguments and return codes
+ * as eahmmf_hip_model_forward, plus -1 for seq outside 0..n_seq-1. */
+int eahmmf_hip_model_forward_seq(void* model, int seq, const int* toks, int nb, int p0, float* logits);
+/* One decode step of n (1..n_seq) different sequences, batched: token toks[i]
+ * at position pos[i] of sequence seqs[i]; each token attends to its own
+ * sequence's rows 0..pos[i] and its row is written there.  Equals n calls of
+ * Engine::forward(&toks[i], 1, pos[i], ...) each on its own sequence's
+ * engine, in one pass whose matmuls and expert block see all n tokens.
+ * logits (may be null): [n][n_vocab], row i for toks[i].  -1 for a sequence
+ * given twice, outside 0..n_seq-1, pos outside 0..n_ctx-1 or a bad token;
+ * otherwise as eahmmf_hip_model_forward. */
+int eahmmf_hip_model_decode_seqs(void* model, int n, const int* toks, const int* seqs, const int* pos,
+                                 float* logits);
 /* Routing trace (Engine::trace_routing): when on, every forward appends, per
  * layer and token, the n_used expert ids and weights in routing order. */
 int eahmmf_hip_model_set_trace(void* model, int on);

@@ -58,6 +58,11 @@ def test_invalid_arguments_fail_without_touching_the_device(binding, hip):
     bad = (binding.Copy * 1)(binding.Copy(None, x.ctypes.data, 16))
     assert hip.eahmmf_hip_h2d_batch(bad, 1) == -1
     assert "null pointer" in hip.eahmmf_hip_last_error().decode()
+    # the model's sequence entry points: a null model is rejected up front
+    assert hip.eahmmf_hip_model_set_sequences(None, 2) == -1
+    assert hip.eahmmf_hip_model_forward_seq(None, 0, ids.ctypes.data, 1, 0, None) == -1
+    assert hip.eahmmf_hip_model_decode_seqs(None, 1, ids.ctypes.data, ids.ctypes.data, ids.ctypes.data, None) == -1
+    assert "null" in hip.eahmmf_hip_last_error().decode()
 
 
 @pytest.mark.parametrize("t,ne0", [(0, 64), (8, 96), (12, 2048), (13, 768), (14, 768), (14, 1536)])
@@ -86,6 +91,12 @@ def test_grouped_path_knobs(hip):
         hip.eahmmf_hip_set_grouped_dot_max(d0)
         hip.eahmmf_hip_set_grouped_wave_max(w0)
         hip.eahmmf_hip_set_grouped_mfma(m0)
+
+
+def test_dense_mfma_switch(hip):
+    assert hip.eahmmf_hip_set_dense_mfma(0) == 1  # on by default
+    assert hip.eahmmf_hip_set_dense_mfma(1) == 0
+    assert hip.eahmmf_hip_set_dense_mfma(1) == 1
 
 
 def test_row_bytes_rejects(hip):

@@ -245,6 +245,64 @@ def test_long_context_against_oracle(torch_dev, binding, shape):
         m.close()
 
 
+# Several sequences in one model (eahmmf_hip_model_set_sequences /
+# forward_seq / decode_seqs): each sequence against an oracle engine of its
+# own (the reference's Engine holds one sequence), prompts of different
+# lengths -- one past a 64-position split, so the batched decode step mixes
+# one-split and several-split tokens -- then decode steps over every
+# sequence in one batch (in shuffled order), over a ragged subset, and a
+# single-sequence step; logits at 1e-4 absolute as above, greedy tokens
+# exactly.
+
+@pytest.mark.parametrize("shape", [
+    dict(D=256, NH=4, NKV=2, HD=64, attn=gt.F32, lens=[37, 5, 150, 1]),
+    dict(D=256, NH=16, NKV=2, HD=128, attn=gt.Q8_0, lens=[70, 3, 12, 9, 130, 2]),
+], ids=["hd64-grp2-4seq", "hd128-grp8-6seq"])
+def test_sequences_against_oracle(torch_dev, binding, shape):
+    import oracle
+    lens = shape["lens"]
+    S = len(lens)
+    spec = small_spec(7, shape["D"], shape["NH"], shape["NKV"], shape["HD"], 8, 2, 128, 512, 2, 200, shape["attn"])
+    rng = np.random.default_rng(5)
+    m = binding.DeviceModel(hp_of(spec), spec.tensors)
+    try:
+        m.set_sequences(S)
+        orc = [oracle.OracleModel(spec) for _ in range(S)]
+        last, pos = [], list(lens)
+        for s, n in enumerate(lens):
+            prompt = rng.integers(0, spec.n_vocab, n).astype(np.int32)
+            lg, lo = m.eval(prompt, 0, 32, seq=s), orc[s].eval(prompt, 0, 32)
+            np.testing.assert_allclose(lg, lo, rtol=0, atol=1e-4)
+            last.append(lo)
+        order = rng.permutation(S)
+        subset = [int(v) for v in order[: S // 2 + 1]][::-1]
+        for seqs in ([int(v) for v in order], list(range(S)), subset, [S - 1]):
+            toks = [int(np.argmax(last[s])) for s in seqs]
+            lg = m.decode_seqs(toks, seqs, [pos[s] for s in seqs])
+            for i, s in enumerate(seqs):
+                lo = orc[s].forward([toks[i]], pos[s])
+                np.testing.assert_allclose(lg[i], lo, rtol=0, atol=1e-4, err_msg=f"sequence {s}")
+                assert int(np.argmax(lg[i])) == int(np.argmax(lo))
+                last[s] = lo
+                pos[s] += 1
+        # sequence 0 through the one-sequence entry points still sees its own rows
+        t = int(np.argmax(last[0]))
+        np.testing.assert_allclose(m.forward([t], pos[0]), orc[0].forward([t], pos[0]), rtol=0, atol=1e-4)
+        # argument checks: a sequence twice, outside the set, a position past the context
+        for toks, seqs, p in (([1, 2], [0, 0], [5, 6]), ([1], [S], [0]), ([1], [0], [spec.n_ctx])):
+            with pytest.raises(RuntimeError):
+                m.decode_seqs(toks, seqs, p)
+        with pytest.raises(RuntimeError):
+            m.forward([1], 0, seq=S)
+        # a new set of sequences starts empty
+        m.set_sequences(2)
+        prompt = rng.integers(0, spec.n_vocab, 9).astype(np.int32)
+        fresh = oracle.OracleModel(spec)
+        np.testing.assert_allclose(m.eval(prompt, 0, 4, seq=1), fresh.eval(prompt, 0, 4), rtol=0, atol=1e-4)
+    finally:
+        m.close()
+
+
 def test_model_from_gguf_file(tmp_path, torch_dev, binding):
     """The tiny model loaded from a GGUF file through the binding's reader
     gives the reference's baseline logits (as Engine::load + eval)."""

@@ -82,6 +82,10 @@ MATMUL_CASES = [
     (Q4_K, 2048, 768, 1), (Q4_K, 2048, 768, 3), (Q6_K, 768, 2048, 1), (Q6_K, 768, 2048, 8), (Q5_K, 2048, 64, 13),
     (Q8_0, 2048, 96, 5), (Q8_0, 128, 256, 2), (Q8_0, 96, 17, 3), (Q6_K, 1536, 40, 64), (Q4_K, 4096, 33, 9),
     (Q5_K, 256, 256, 4),
+    # the matrix-core path at its edges: 16 splits of the K range (few rows),
+    # ragged token tiles (17, 33), 64 tokens, rows not a multiple of 64
+    (Q4_K, 4096, 512, 16), (Q5_K, 2048, 100, 33), (Q6_K, 4096, 130, 17), (Q8_0, 8192, 70, 64),
+    (Q8_0, 4096, 1000, 2), (Q6_K, 256, 4100, 48),
 ]
 
 
@@ -100,6 +104,18 @@ def test_matmul_vs_oracle(torch_dev, hip, t, ne0, ne1, nb):
     assert ok, hip.eahmmf_hip_last_error()
     close(out[:, :ne1], oracle.matmul(t, w, ne0, x))
     assert np.all(out[:, ne1:] == 7.0)  # padding untouched
+
+
+@pytest.mark.parametrize("t,ne0,ne1,nb", [(Q4_K, 2048, 96, 5), (Q5_K, 4096, 40, 16), (Q6_K, 1536, 70, 33),
+                                          (Q8_0, 2048, 130, 8)])
+def test_matmul_general_kernel_vs_oracle(torch_dev, hip, t, ne0, ne1, nb):
+    """The general (vector-ALU) matmul kernel, with the matrix-core path
+    switched off, on shapes the matrix-core path would otherwise take."""
+    prev = hip.eahmmf_hip_set_dense_mfma(0)
+    try:
+        test_matmul_vs_oracle(torch_dev, hip, t, ne0, ne1, nb)
+    finally:
+        hip.eahmmf_hip_set_dense_mfma(prev)
 
 
 @pytest.mark.parametrize("t,pad", [(Q4_K, 48), (Q6_K, 6), (Q8_0, 2), (Q5_K, 16)])
