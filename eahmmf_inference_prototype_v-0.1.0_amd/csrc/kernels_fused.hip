@@ -276,22 +276,43 @@ __device__ bool quantize_words(const uint64_t* src, int n, unsigned epoch, unsig
     return good;
 }
 
-// The activation levels of segment g (64 values) held by one lane.
+// The activation levels of segment g (64 values) held by one lane.  All
+// fifteen LDS reads are in flight together: one asm statement takes every
+// loaded register, so the compiler cannot pair each read with its uses (it
+// did, waiting for one or two reads at a time, which made a phase-B task
+// twelve dependent LDS round trips long).
+using u32x4 = unsigned __attribute__((ext_vector_type(4)));
 __device__ __forceinline__ void load_xseg(XSeg& xs, const int8_t* q, int qstride, const float* sc, int scstride,
                                           const float* s32, int g) {
+    u32x4 v[kLevels][4];
+    float f[kLevels + 2];
 #pragma unroll
     for (int lv = 0; lv < kLevels; lv++) {
-        const uint4* xp = reinterpret_cast<const uint4*>(q + lv * qstride + g * 64);
+        const u32x4* xp = reinterpret_cast<const u32x4*>(q + lv * qstride + g * 64);
+#pragma unroll
+        for (int c = 0; c < 4; c++) v[lv][c] = xp[c];
+        f[lv] = sc[lv * scstride + g];
+    }
+    f[kLevels] = s32[2 * g];
+    f[kLevels + 1] = s32[2 * g + 1];
+    static_assert(kLevels == 3, "one operand per loaded register below");
+    asm volatile(""
+                 : "+v"(v[0][0]), "+v"(v[0][1]), "+v"(v[0][2]), "+v"(v[0][3]), "+v"(v[1][0]), "+v"(v[1][1]),
+                   "+v"(v[1][2]), "+v"(v[1][3]), "+v"(v[2][0]), "+v"(v[2][1]), "+v"(v[2][2]), "+v"(v[2][3]),
+                   "+v"(f[0]), "+v"(f[1]), "+v"(f[2]), "+v"(f[3]), "+v"(f[4]));
+#pragma unroll
+    for (int lv = 0; lv < kLevels; lv++) {
 #pragma unroll
         for (int c = 0; c < 4; c++) {
-            const uint4 v = xp[c];
-            xs.q[lv][4 * c] = (int)v.x; xs.q[lv][4 * c + 1] = (int)v.y;
-            xs.q[lv][4 * c + 2] = (int)v.z; xs.q[lv][4 * c + 3] = (int)v.w;
+            xs.q[lv][4 * c] = (int)v[lv][c].x;
+            xs.q[lv][4 * c + 1] = (int)v[lv][c].y;
+            xs.q[lv][4 * c + 2] = (int)v[lv][c].z;
+            xs.q[lv][4 * c + 3] = (int)v[lv][c].w;
         }
-        xs.s[lv] = sc[lv * scstride + g];
+        xs.s[lv] = f[lv];
     }
-    xs.sum32[0] = s32[2 * g];
-    xs.sum32[1] = s32[2 * g + 1];
+    xs.sum32[0] = f[kLevels];
+    xs.sum32[1] = f[kLevels + 1];
 }
 
 // Routing, step 1 (wave 0): the expert table into LDS and every candidate's
@@ -736,13 +757,37 @@ __device__ void fused_body(const FusedArgs& a, FusedLds& L) {
         return r;
     };
 
+    // What phase B and the combine read from the kernel arguments, loaded by
+    // each wave before the barrier that starts phase B and held in scalar
+    // registers: the compiler otherwise reloads them where they are used,
+    // and after the barrier those loads miss and wait (two dependent round
+    // trips ahead of the first phase-B task).
+    struct Late {
+        const FusedArgs& a;
+        unsigned epoch, flags;
+        int rows_round, stride_b, D, np;
+        uint64_t* ypart;
+        float* y;
+        unsigned* sync;
+        __device__ __forceinline__ void load() {
+            epoch = a.epoch;
+            flags = a.flags;
+            rows_round = a.rows_round;
+            stride_b = a.stride_b;
+            D = a.D;
+            np = a.np;
+            ypart = a.ypart;
+            y = a.y;
+            sync = a.sync;
+            asm volatile(""
+                         : "+s"(epoch), "+s"(flags), "+s"(rows_round), "+s"(stride_b), "+s"(D), "+s"(np), "+s"(ypart),
+                           "+s"(y), "+s"(sync));
+        }
+    } late{a};
     SegCodes<DT> pre[NPD];  // B waves: their first phase-B tasks, decoded
     BTask tb[NPD];          // and where those tasks are
-    // A waves: the round-0 task after the B waves' (task (8 - 4) NPD + wave),
-    // decoded once the passes are done, while h is on its way
+    // A waves: the round-0 tasks after the B waves' (from (8 - 4) NPD + wave)
     const int task_a = (kWaves - kAWaves) * NPD + wave;
-    SegCodes<DT> pre_a;
-    BTask tb_a;
     if (wave < kAWaves) {
         // ---- 2A. this wave's passes through its LDS ring.  Every load the
         // compiler issued is retired first: the copies below are invisible to
@@ -783,17 +828,13 @@ __device__ void fused_body(const FusedArgs& a, FusedLds& L) {
             // every lane's reads of this slot have returned (their values are used above)
             if (pp + NPA < npass) issue(pp + NPA);
         }
-        if (task_a < n_tasks0) {
-            wait_lds(&L.b_landed, (unsigned)(kWaves - kAWaves));  // the staged down rows
-            tb_a = btask(task_a, rr0, 0);
-            RawSeg<DT> raw;
-            raw.template load<LdsLd>(tb_a.row, tb_a.sg);
-            pre_a = raw.decode(tb_a.sg);
-            pre_a.pin_all();  // decoded here, not after the barrier
-        }
+        late.load();
         // ---- 4A. the partition's h as int8 levels, once every word carries
         // this launch's epoch (it overwrites the activation levels: every A
-        // wave has read its own first)
+        // wave has read its own first).  The A waves decode their phase-B
+        // tasks after the barrier: h is on the critical path, and a decode
+        // ahead of the first poll (or between the poll and the barrier)
+        // delayed phase B by the decode's length.
         wait_lds(&L.xs_read, (unsigned)kAWaves);
         if (!quantize_words(a.hx + p * ep * FF, ep * FF, a.epoch, a.sync, spin_limit_of(a.flags), &L.b.hq[0][0], kMaxHP,
                             &L.b.hsc[0][0], kMaxHP / 64, L.b.hs32, tid, kAThreads))
@@ -817,6 +858,7 @@ __device__ void fused_body(const FusedArgs& a, FusedLds& L) {
             pre[i] = raw.decode(tb[i].sg);
             pre[i].pin_all();  // decoded here, not after the barrier
         }
+        late.load();
     }
     __syncthreads();  // the h levels and the first phase-B codes are ready
 
@@ -829,8 +871,8 @@ __device__ void fused_body(const FusedArgs& a, FusedLds& L) {
     // a lane is one row, so the h levels of the task are read by all lanes at
     // one address.
     const int nrows = r_end - r_begin;
-    for (int r0 = 0; r0 < nrows; r0 += a.rows_round) {
-        const int rr = min(a.rows_round, nrows - r0);
+    for (int r0 = 0; r0 < nrows; r0 += late.rows_round) {
+        const int rr = min(late.rows_round, nrows - r0);
         if (r0 > 0) {
             // this wave's copies of the round (issued a round ago) have
             // landed; after the barrier everyone's have, and the previous
@@ -841,8 +883,8 @@ __device__ void fused_body(const FusedArgs& a, FusedLds& L) {
         {
             // the next round's copies go out now, into the stage the previous
             // round has finished with (the second round's: the A rings)
-            const int r1 = r0 + a.rows_round;
-            if (r1 < nrows) stage_round(r1, min(a.rows_round, nrows - r1));
+            const int r1 = r0 + late.rows_round;
+            if (r1 < nrows) stage_round(r1, min(late.rows_round, nrows - r1));
         }
         auto finish = [&](const BTask& t, const SegCodes<DT>& k) {
             XSeg hs;  // the same address in every lane: one LDS broadcast per read
@@ -858,8 +900,7 @@ __device__ void fused_body(const FusedArgs& a, FusedLds& L) {
                     if (wave - kAWaves + (kWaves - kAWaves) * i < n_tasks0) finish(tb[i], pre[i]);
                 first = (kWaves - kAWaves) * NPD + wave;
             } else {
-                if (task_a < n_tasks0) finish(tb_a, pre_a);
-                first = task_a + kWaves;
+                first = task_a;
             }
         }
         for (int task = first; task < n_tasks(rr); task += kWaves) {
@@ -889,14 +930,15 @@ __device__ void fused_body(const FusedArgs& a, FusedLds& L) {
                     for (int u = 0; u < segB; u++) v += pr[u];
                 }
             }
-            store_word(&a.ypart[p * D + r_begin + r0 + r], epoch_word(poisoned ? __builtin_nanf("") : v, a.epoch),
+            store_word(&late.ypart[p * late.D + r_begin + r0 + r], epoch_word(poisoned ? __builtin_nanf("") : v, late.epoch),
                        true);
         }
     }
 
     // ---- 5. workgroup q of partition q % np adds chunk q's partials into y
-    if (p == q % np)
-        for (int r = r_begin + tid; r < r_end; r += kThreads) a.y[r] = reduce_row(a.ypart, D, r, np, a.epoch, a.sync, spin_limit_of(a.flags));
+    if (p == q % late.np)
+        for (int r = r_begin + tid; r < r_end; r += kThreads)
+            late.y[r] = reduce_row(late.ypart, late.D, r, late.np, late.epoch, late.sync, spin_limit_of(late.flags));
 }
 
 template <int LA, int GT, int UT, int DT>

@@ -27,6 +27,8 @@
 //      w * yp[pos] (fma), the reference's accumulation order.
 // Expert weights are read once per (expert, row) however many tokens the
 // group holds.
+#include <mutex>
+
 #include "internal.h"
 #include "kquant.h"
 
@@ -354,6 +356,65 @@ size_t grouped_scratch_bytes(const MoeShape& s, int nb, int k, int n_expert) {
     return base + mf + dt;
 }
 
+// A second stream per device on which the per-wave matrix-core kernels (the
+// small groups) run beside the workgroup kernels (the large groups) of the
+// same matmul: the two write disjoint rows of h / yp, and each alone leaves
+// the CUs waiting on memory latency (one 8-wave workgroup per CU for the
+// workgroup kernels).  Fork: an event on the caller's stream that the side
+// stream waits for; join: an event on the side stream that the caller's
+// stream waits for.  Both streams keep the default priority.  Kept per device
+// until the process ends.
+struct SideStream {
+    hipStream_t st = nullptr;
+    hipEvent_t fork = nullptr, join = nullptr;
+};
+static std::mutex g_side_mu;
+static SideStream g_side[64];
+
+static SideStream* side_stream() {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return nullptr;
+    std::lock_guard<std::mutex> g(g_side_mu);
+    SideStream& ss = g_side[dev];
+    if (!ss.st) {
+        hipStream_t st = nullptr;
+        hipEvent_t a = nullptr, b = nullptr;
+        if (hipStreamCreateWithFlags(&st, hipStreamNonBlocking) != hipSuccess) return nullptr;
+        if (hipEventCreateWithFlags(&a, hipEventDisableTiming) != hipSuccess ||
+            hipEventCreateWithFlags(&b, hipEventDisableTiming) != hipSuccess) {
+            if (a) (void)hipEventDestroy(a);
+            (void)hipStreamDestroy(st);
+            return nullptr;
+        }
+        ss.st = st;
+        ss.fork = a;
+        ss.join = b;
+    }
+    return &ss;
+}
+
+// Runs small(side) and large(st) concurrently when a side stream exists
+// (else both on st, in order), then joins: work queued on st afterwards waits
+// for both.
+template <class Small, class Large>
+static hipError_t fork_join(hipStream_t st, bool any_small, bool any_large, Small small, Large large) {
+    SideStream* ss = any_small && any_large ? side_stream() : nullptr;
+    hipError_t e;
+    if (!ss) {
+        if (any_small && (e = small(st)) != hipSuccess) return e;
+        if (any_large && (e = large(st)) != hipSuccess) return e;
+        return hipSuccess;
+    }
+    if ((e = hipEventRecord(ss->fork, st)) != hipSuccess || (e = hipStreamWaitEvent(ss->st, ss->fork, 0)) != hipSuccess)
+        return e;
+    const hipError_t es = small(ss->st);
+    // the join is recorded whatever the launch returned, so st never waits on a stale event
+    if ((e = hipEventRecord(ss->join, ss->st)) != hipSuccess) return e;
+    const hipError_t el = large(st);
+    if ((e = hipStreamWaitEvent(st, ss->join, 0)) != hipSuccess) return e;
+    return es != hipSuccess ? es : el;
+}
+
 bool grouped_supported(const MoeShape& s, int nb, int k, int n_expert) {
     return moe_shape_ok(s) && nb > 0 && k > 0 && k <= kMaxSlots && n_expert > 0 && n_expert <= kGroupMaxE &&
            s.D % 32 == 0 && s.FF % 32 == 0 && s.D % 4 == 0;
@@ -413,12 +474,15 @@ hipError_t launch_moe_grouped(const MoeShape& s, const ExpertEntry* table, int n
             if ((e = launch_prep_rows(offs, n_expert, tok, x, ldx, s.D, (int)P, xh, xl, xsh, xsl, xsc, st)) !=
                 hipSuccess)
                 return e;
-            if (wave_max >= rest && (e = launch_gate_up_wave(s, table, n_expert, offs, xh, xl, xsh, xsl, xsc, h, rest,
-                                                             wave_max, st)) != hipSuccess)
-                return e;
-            if (nb >= wg_min && (e = launch_gate_up_mfma(s, table, n_expert, offs, nb, xh, xl, xsh, xsl, xsc, h,
-                                                         wg_min, st)) != hipSuccess)
-                return e;
+            e = fork_join(
+                st, wave_max >= rest, nb >= wg_min,
+                [&](hipStream_t q) {
+                    return launch_gate_up_wave(s, table, n_expert, offs, xh, xl, xsh, xsl, xsc, h, rest, wave_max, q);
+                },
+                [&](hipStream_t q) {
+                    return launch_gate_up_mfma(s, table, n_expert, offs, nb, xh, xl, xsh, xsl, xsc, h, wg_min, q);
+                });
+            if (e != hipSuccess) return e;
         } else {
             const dim3 ga((unsigned)((s.FF + 3) / 4), (unsigned)n_expert);
             switch (s.gate_type) {
@@ -440,12 +504,11 @@ hipError_t launch_moe_grouped(const MoeShape& s, const ExpertEntry* table, int n
             if ((e = launch_prep_rows(offs, n_expert, nullptr, h, s.FF, s.FF, (int)P, hh, hl, nullptr, nullptr, hsc,
                                       st)) != hipSuccess)
                 return e;
-            if (wave_max >= rest &&
-                (e = launch_down_wave(s, table, n_expert, offs, hh, hl, hsc, yp, rest, wave_max, st)) != hipSuccess)
-                return e;
-            if (nb >= wg_min &&
-                (e = launch_down_mfma(s, table, n_expert, offs, nb, hh, hl, hsc, yp, wg_min, st)) != hipSuccess)
-                return e;
+            e = fork_join(
+                st, wave_max >= rest, nb >= wg_min,
+                [&](hipStream_t q) { return launch_down_wave(s, table, n_expert, offs, hh, hl, hsc, yp, rest, wave_max, q); },
+                [&](hipStream_t q) { return launch_down_mfma(s, table, n_expert, offs, nb, hh, hl, hsc, yp, wg_min, q); });
+            if (e != hipSuccess) return e;
         } else {
             const dim3 gd((unsigned)((s.D + 3) / 4), (unsigned)n_expert);
             switch (s.down_type) {
