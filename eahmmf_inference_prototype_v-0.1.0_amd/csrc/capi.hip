@@ -158,12 +158,26 @@ bool matmul_args_ok(const uint8_t* w, int type, int ne0, int ne1, size_t row_byt
 }
 
 // host x[nb][ldx] (first ne0 of each row) -> device dense [nb][ne0]
+// Up to this many bytes a synchronous call's staging copies run as a copy
+// kernel on the call's stream (launch_copy_words), above it on a copy engine.
+constexpr size_t kKernelCopyMax = (size_t)1 << 20;
+
+// Queues dst0 <- src0 and dst1 <- src1 (bytes multiples of 4; bytes1 may be 0)
+// between pinned staging and device buffers on the context's stream.
+bool queue_copies(DevCtx* c, void* d0, const void* s0, size_t b0, void* d1, const void* s1, size_t b1,
+                  hipMemcpyKind kind, const char* what) {
+    if (b0 + b1 <= kKernelCopyMax && ((b0 | b1) & 3) == 0)
+        return hip_ok(launch_copy_words(d0, s0, b0, d1, s1, b1, c->stream), what);
+    return hip_ok(hipMemcpyAsync(d0, s0, b0, kind, c->stream), what) &&
+           (b1 == 0 || hip_ok(hipMemcpyAsync(d1, s1, b1, kind, c->stream), what));
+}
+
 bool stage_x(DevCtx* c, const float* host_x, int nb, int ne0, int ldx) {
     const size_t bytes = (size_t)nb * ne0 * sizeof(float);
     if (!grow_pinned(c->px, bytes) || !grow_device(c->dx, bytes)) return false;
     float* px = (float*)c->px.p;
     for (int t = 0; t < nb; t++) memcpy(px + (size_t)t * ne0, host_x + (size_t)t * ldx, sizeof(float) * ne0);
-    return hip_ok(hipMemcpyAsync(c->dx.p, px, bytes, hipMemcpyHostToDevice, c->stream), "hipMemcpyAsync(x)");
+    return queue_copies(c, c->dx.p, px, bytes, nullptr, nullptr, 0, hipMemcpyHostToDevice, "stage x");
 }
 
 void unstage_rows(const float* dense, int nb, int n, float* host, int ld) {
@@ -197,15 +211,6 @@ bool grow_fused(DevCtx* c, const MoeShape& s, int k) {
     c->fused.ypart = (uint64_t*)c->dyp.p;
     c->fused.ypart_words = c->dyp.cap / sizeof(uint64_t);
     return true;
-}
-
-// Synchronous entry points read the fused kernel's error word with their
-// output: one 4-byte copy queued behind the output's, into pinned staging
-// next to it, so no extra synchronisation is needed.
-bool queue_flag_read(DevCtx* c, void* host_slot) {
-    return hip_ok(hipMemcpyAsync(host_slot, c->dsync + kSyncFlagWord, sizeof(unsigned), hipMemcpyDeviceToHost,
-                                 c->stream),
-                  "hipMemcpyAsync(error word)");
 }
 
 // After the drain: an error word equal to the call's own launch epoch means
@@ -290,10 +295,28 @@ void fill_slot(uint8_t* slot, const std::vector<Piece>& ps, size_t total, int nt
     for (std::thread& x : th) x.join();
 }
 
-// The drop-in matmul's launch: on the matrix cores for 2..64 tokens of a
-// K-quant or Q8_0 matrix (workspace grown on demand), else the general kernel.
+// A single token (the reference's decode calls, nb = 1) runs on the decode
+// matrix-vector kernel (kernels_gemv.hip: rows DMA'd into LDS, the input held
+// once per block in LDS, DPP reductions) where it takes the shape; its direct
+// row reads want 16-byte aligned matrices.
+bool gemv_ok(int type, const uint8_t* w, int ne0, size_t rb) {
+    return gemv_supported(type, ne0, rb) && ((uintptr_t)w & 15u) == 0;
+}
+
+// The drop-in matmul's launch: the matrix-vector kernel for one token, the
+// matrix cores for 2..64 tokens of a K-quant or Q8_0 matrix (workspace grown
+// on demand), else the general kernel.
 hipError_t matmul_launch(DevCtx* c, int type, const uint8_t* w, int ne0, int ne1, size_t rb, int nb, float* out) {
     const float* x = (const float*)c->dx.p;
+    if (nb == 1 && gemv_ok(type, w, ne0, rb)) {
+        GemvArgs g{};
+        g.x = x;
+        g.seg[0] = GemvSeg{w, out, nullptr, ne1};
+        g.nseg = 1;
+        g.ne0 = ne0;
+        g.rb = (int)rb;
+        return launch_gemv(type, g, c->stream);
+    }
     if (dense_mfma_enabled() && matmul_mfma_ok(type, w, ne0, rb, x, nb, ne0) &&
         grow_device(c->dws, matmul_mfma_ws_bytes(ne0, ne1, nb)))
         return launch_matmul_mfma(type, w, ne0, ne1, rb, x, nb, ne0, out, ne1, c->dws.p, c->dws.cap, c->stream);
@@ -324,7 +347,7 @@ bool eahmmf_hip_matmul(const uint8_t* device_weights, int type, int ne0, int ne1
     const size_t obytes = (size_t)nb * ne1 * sizeof(float);
     bool ok = grow_device(c->dy, obytes) && grow_pinned(c->py, obytes) && stage_x(c, host_x, nb, ne0, ldx);
     if (ok) ok = hip_ok(matmul_launch(c, type, device_weights, ne0, ne1, row_bytes, nb, (float*)c->dy.p), "matmul launch");
-    if (ok) ok = hip_ok(hipMemcpyAsync(c->py.p, c->dy.p, obytes, hipMemcpyDeviceToHost, c->stream), "hipMemcpyAsync(out)");
+    if (ok) ok = queue_copies(c, c->py.p, c->dy.p, obytes, nullptr, nullptr, 0, hipMemcpyDeviceToHost, "copy out");
     ok = drain(c, ok);
     if (ok) unstage_rows((const float*)c->py.p, nb, ne1, host_out, ldo);
     return ok;
@@ -343,10 +366,21 @@ bool eahmmf_hip_matmul_pair(const uint8_t* gw, int gt, int gne0, int gne1, size_
     const size_t obytes = (size_t)nb * gne1 * sizeof(float);
     bool ok = grow_device(c->dy, obytes) && grow_device(c->dy2, obytes) && grow_pinned(c->py, obytes) &&
               grow_pinned(c->py2, obytes) && stage_x(c, host_x, nb, gne0, ldx);
-    if (ok) ok = hip_ok(matmul_launch(c, gt, gw, gne0, gne1, grb, nb, (float*)c->dy.p), "gate launch");
-    if (ok) ok = hip_ok(matmul_launch(c, ut, uw, une0, une1, urb, nb, (float*)c->dy2.p), "up launch");
-    if (ok) ok = hip_ok(hipMemcpyAsync(c->py.p, c->dy.p, obytes, hipMemcpyDeviceToHost, c->stream), "copy g");
-    if (ok) ok = hip_ok(hipMemcpyAsync(c->py2.p, c->dy2.p, obytes, hipMemcpyDeviceToHost, c->stream), "copy u");
+    if (ok && nb == 1 && gt == ut && grb == urb && gemv_ok(gt, gw, gne0, grb) && gemv_ok(ut, uw, une0, urb)) {
+        // one matrix-vector launch for both (the input staged in LDS once)
+        GemvArgs g{};
+        g.x = (const float*)c->dx.p;
+        g.seg[0] = GemvSeg{gw, (float*)c->dy.p, nullptr, gne1};
+        g.seg[1] = GemvSeg{uw, (float*)c->dy2.p, nullptr, une1};
+        g.nseg = 2;
+        g.ne0 = gne0;
+        g.rb = (int)grb;
+        ok = hip_ok(launch_gemv(gt, g, c->stream), "gate/up launch");
+    } else {
+        if (ok) ok = hip_ok(matmul_launch(c, gt, gw, gne0, gne1, grb, nb, (float*)c->dy.p), "gate launch");
+        if (ok) ok = hip_ok(matmul_launch(c, ut, uw, une0, une1, urb, nb, (float*)c->dy2.p), "up launch");
+    }
+    if (ok) ok = queue_copies(c, c->py.p, c->dy.p, obytes, c->py2.p, c->dy2.p, obytes, hipMemcpyDeviceToHost, "copy g/u");
     ok = drain(c, ok);
     if (ok) {
         unstage_rows((const float*)c->py.p, nb, gne1, host_g, ldg);
@@ -410,10 +444,11 @@ bool eahmmf_hip_moe_decode(const eahmmf_hip_expert* experts, const float* w, int
         }
     }
     unsigned* flag = (unsigned*)((uint8_t*)c->py.p + flag_at);
-    if (ok) ok = hip_ok(hipMemcpyAsync(c->py.p, c->dy.p, ybytes, hipMemcpyDeviceToHost, c->stream), "copy y");
-    if (ok && fused) {
+    if (ok) {
+        // y, and for a fused launch its error word into the staging next to y
         *flag = 0;
-        ok = queue_flag_read(c, flag);
+        ok = queue_copies(c, c->py.p, c->dy.p, ybytes, flag, c->dsync + kSyncFlagWord, fused ? sizeof(unsigned) : 0,
+                          hipMemcpyDeviceToHost, "copy y");
     }
     ok = drain(c, ok);
     if (!ok) return false;

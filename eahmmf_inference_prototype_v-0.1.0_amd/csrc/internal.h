@@ -252,5 +252,9 @@ bool gemv_supported(int type, int ne0, size_t rb);
 hipError_t launch_gemv(int type, GemvArgs a, hipStream_t st);
 
 hipError_t launch_add(float* x, const float* y, size_t n, hipStream_t st);
+// Copies two regions of 4-byte words (sizes multiples of 4) in one kernel;
+// either side may be pinned host memory (kernels_basic.hip).
+hipError_t launch_copy_words(void* d0, const void* s0, size_t bytes0, void* d1, const void* s1, size_t bytes1,
+                             hipStream_t st);
 
 }  // namespace eahmmf

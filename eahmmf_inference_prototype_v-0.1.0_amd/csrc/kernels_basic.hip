@@ -97,4 +97,31 @@ hipError_t launch_matmul(int type, const uint8_t* w, int ne0, int ne1, size_t ro
     return hipGetLastError();
 }
 
+// Small copies between pinned host staging and device buffers as a kernel
+// (the GPU reads and writes pinned host memory directly): for the few KB a
+// synchronous entry point moves per call this starts sooner than a copy
+// engine transfer.  Two regions of 4-byte words per launch.
+__global__ __launch_bounds__(256) void copy_words_kernel(uint32_t* d0, const uint32_t* s0, size_t n0, uint32_t* d1,
+                                                         const uint32_t* s1, size_t n1) {
+    const size_t stride = (size_t)gridDim.x * blockDim.x;
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n0 + n1; i += stride) {
+        if (i < n0)
+            d0[i] = s0[i];
+        else
+            d1[i - n0] = s1[i - n0];
+    }
+}
+
+hipError_t launch_copy_words(void* d0, const void* s0, size_t bytes0, void* d1, const void* s1, size_t bytes1,
+                             hipStream_t st) {
+    if ((bytes0 | bytes1) & 3) return hipErrorInvalidValue;
+    const size_t n = (bytes0 + bytes1) / 4;
+    if (n == 0) return hipSuccess;
+    clear_stale_error();
+    const size_t blocks = (n + 255) / 256;
+    copy_words_kernel<<<(unsigned)(blocks < 64 ? blocks : 64), 256, 0, st>>>(
+        (uint32_t*)d0, (const uint32_t*)s0, bytes0 / 4, (uint32_t*)d1, (const uint32_t*)s1, bytes1 / 4);
+    return hipGetLastError();
+}
+
 }  // namespace eahmmf
