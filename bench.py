@@ -550,67 +550,78 @@ def c3_model(torch, b, expert_type, n_ctx, seed=3, shape=QWEN3_30B, types=None):
     return m, keep, hp
 
 
-def c3_token_bytes(b, hp, expert_type, n_pos):
+def c3_token_bytes(b, hp, expert_type, n_pos, types=None):
     """Algorithmic HBM bytes of one decode token at n_pos cached positions:
     every dense weight once (Q, K, V, output projections, router, output
-    head), the 8 routed experts' three matrices per layer, the K and V rows of
-    n_pos positions per layer (fp32) plus the new row, one embedding row."""
+    head), the 8 routed experts' three matrices per layer (all expert_type,
+    or types = (gate, up, down)), the K and V rows of n_pos positions per
+    layer (fp32) plus the new row, one embedding row."""
     D_, FF_, NL, KD, QD = hp["D"], hp["FF"], hp["n_layer"], hp["n_kv"] * hp["hd"], hp["n_head"] * hp["hd"]
+    gt_, ut_, dt_ = types if types else (expert_type,) * 3
     q8 = lambda ne0: b.row_bytes(Q8_0, ne0)
     dense = (QD + 2 * KD) * q8(D_) + D_ * q8(QD) + hp["n_expert"] * D_ * 4
-    experts = hp["n_used"] * (2 * FF_ * b.row_bytes(expert_type, D_) + D_ * b.row_bytes(expert_type, FF_))
+    experts = hp["n_used"] * (FF_ * (b.row_bytes(gt_, D_) + b.row_bytes(ut_, D_)) + D_ * b.row_bytes(dt_, FF_))
     kv = 2 * (n_pos + 1) * KD * 4
     return NL * (dense + experts + kv) + hp["n_vocab"] * q8(D_) + q8(D_)
+
+
+def c3_decode(torch, b, et, types, CTX, steps, warm, rng):
+    """Builds the 48-layer model (experts et, or types = (gate, up, down)),
+    prefills CTX - warm positions (batches of 64), decodes warm tokens, then
+    times one eahmmf_hip_model_generate_greedy call of `steps` tokens (one
+    host wait at its end).  Returns its figures and frees the model."""
+    t0 = time.perf_counter()
+    m, keep, hp = c3_model(torch, b, et, CTX + warm + steps + 1, types=types)
+    t_build = time.perf_counter() - t0
+    prompt = rng.integers(0, hp["n_vocab"], CTX - warm).astype(np.int32)
+    t0 = time.perf_counter()
+    lg = m.eval(prompt, 0, 64)
+    t_prefill = time.perf_counter() - t0
+    assert np.isfinite(lg).all(), "non-finite logits after the prefill"
+    first = int(np.argmax(lg))
+    toks, lg = m.generate_greedy(first, CTX - warm, warm)
+    t0 = time.perf_counter()
+    toks, lg = m.generate_greedy(int(toks[-1]), CTX, steps)
+    el = time.perf_counter() - t0
+    assert np.isfinite(lg).all(), "non-finite logits after decode"
+    bt = c3_token_bytes(b, hp, et, CTX + steps // 2, types)
+    m.close()
+    del keep
+    torch.cuda.empty_cache()
+    return {"tokens_per_s": round(steps / el, 1), "ms_per_token": round(el * 1e3 / steps, 4),
+            "bytes_per_token": bt, "GB_s": round(bt * steps / el / 1e9, 1),
+            "pct_of_hbm_peak": round(100 * bt * steps / el / 1e9 / HBM_PEAK_GBS, 2),
+            "prefill_tokens_per_s": round(len(prompt) / t_prefill, 1), "build_s": round(t_build, 1)}
 
 
 def bench_c3(args, torch, b, hip):
     """Single-token decode of the full 48-layer Qwen3-30B-A3B-shaped model at
     a 2048-token KV context (every layer on the device: attention with its
     Q8_0 projections, norms, RoPE, KV cache, router, the fused expert block,
-    output head, greedy argmax), for the two expert variants all-Q5_K and
-    all-Q8_0.  The KV cache is filled by a 2048-token prefill (batches of 64);
-    the timed region is one eahmmf_hip_model_generate_greedy call of `steps`
-    tokens (one host wait at its end).  value = tokens/s of the Q5_K variant."""
+    output head, greedy argmax), for the expert variants all-Q5_K, all-Q8_0
+    and the Q4_K_M mix (Q4_K gate/up, Q6_K down).  The KV cache is filled by a
+    2048-token prefill (batches of 64); the timed region is one
+    eahmmf_hip_model_generate_greedy call of `steps` tokens (one host wait at
+    its end).  value = tokens/s of the Q5_K variant."""
     CTX = 2048
     steps = args.steps if args.steps else 64
     warm = args.warmup if args.warmup else 8
     rng = np.random.default_rng(5)
     results = {}
-    for name, et in (("q5_k", Q5_K), ("q8_0", Q8_0)):
-        t0 = time.perf_counter()
-        m, keep, hp = c3_model(torch, b, et, CTX + warm + steps + 1)
-        t_build = time.perf_counter() - t0
-        prompt = rng.integers(0, hp["n_vocab"], CTX - warm).astype(np.int32)
-        t0 = time.perf_counter()
-        lg = m.eval(prompt, 0, 64)
-        t_prefill = time.perf_counter() - t0
-        assert np.isfinite(lg).all(), "non-finite logits after the prefill"
-        first = int(np.argmax(lg))
-        toks, lg = m.generate_greedy(first, CTX - warm, warm)
-        t0 = time.perf_counter()
-        toks, lg = m.generate_greedy(int(toks[-1]), CTX, steps)
-        el = time.perf_counter() - t0
-        assert np.isfinite(lg).all(), "non-finite logits after decode"
-        bt = c3_token_bytes(b, hp, et, CTX + steps // 2)
-        results[name] = {"tokens_per_s": round(steps / el, 1), "ms_per_token": round(el * 1e3 / steps, 4),
-                         "bytes_per_token": bt, "GB_s": round(bt * steps / el / 1e9, 1),
-                         "pct_of_hbm_peak": round(100 * bt * steps / el / 1e9 / HBM_PEAK_GBS, 2),
-                         "prefill_tokens_per_s": round(len(prompt) / t_prefill, 1),
-                         "build_s": round(t_build, 1)}
+    for name, et, types in (("q5_k", Q5_K, None), ("q8_0", Q8_0, None), ("q4_k_m", Q4_K, (Q4_K, Q4_K, Q6_K))):
+        results[name] = c3_decode(torch, b, et, types, CTX, steps, warm, rng)
         if not args.no_cpu_baseline and name == "q5_k":  # the headline variant only (about 2 minutes)
             results[name]["cpu_baseline"] = c3_cpu_baseline(et)
         print(f"# c3 {name}: {results[name]}", file=sys.stderr, flush=True)
-        m.close()
-        del keep
-        torch.cuda.empty_cache()
     r = results["q5_k"]
     print(json.dumps({
         "metric": "decode tokens/s, 48-layer Qwen3-30B-A3B-shaped model, 2048-token KV context", "unit": "tokens/s",
         "value": r["tokens_per_s"], "n_gpus": 1, "steps": steps, "warmup": warm, "ms_per_step": r["ms_per_token"],
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32", "data": "synthetic",
         "config": {"workload": "single-token greedy decode, 48 layers D=2048 32/4 heads hd=128, 128 experts top-8 "
-                               "FF=768, vocab 151936, KV context 2048 (prefilled), experts Q5_K (value) / Q8_0, "
-                               "attention + embedding + output head Q8_0, router F32; everything on the device"},
+                               "FF=768, vocab 151936, KV context 2048 (prefilled), experts Q5_K (value) / Q8_0 / "
+                               "Q4_K_M (Q4_K gate/up, Q6_K down), attention + embedding + output head Q8_0, router "
+                               "F32; everything on the device"},
         "roofline": {"bound": "hbm", "kernel": "whole decode token (all launches)",
                      "achieved": r["GB_s"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(r["GB_s"] / HBM_PEAK_GBS, 4), "traffic": None},
@@ -1075,6 +1086,7 @@ def main():
     ap.add_argument("--c3-cpu-child", type=int, default=0, help=argparse.SUPPRESS)
     ap.add_argument("--c3-cpu-etype", type=int, default=Q5_K, help=argparse.SUPPRESS)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-model", action="store_true", help="default line: skip the whole-model decode figure")
     ap.add_argument("--workload", choices=("c2", "c3", "c3x", "c4", "c5", "c5b16", "c5seq", "stream", "staging",
                                            "dropin"), default="c2",
                     help="c2 (default): the headline single-token layer; c3: one decode token through the whole "
@@ -1220,6 +1232,16 @@ def main():
     sr = stream_rates(torch, hip)
     sr["frac_of_c2_size_cold"] = round(achieved / sr["c2_size_cold_GB_s"], 4)
     out["stream_read"] = sr
+    # the second half of the metric, measured: whole-model single-token decode at the
+    # Qwen3-30B-A3B shape with Q4_K_M experts (every layer on the device, 2048-token
+    # context), after the layer replicas are freed
+    if not args.no_model:
+        del dgate, dup, ddown, tables
+        torch.cuda.empty_cache()
+        r = c3_decode(torch, b, Q4_K, (Q4_K, Q4_K, Q6_K), 2048, 32, 4, np.random.default_rng(5))
+        out["decode_tokens_per_s_q4_k_m_48_layers"] = r["tokens_per_s"]
+        out["decode_q4_k_m"] = dict(r, what="eahmmf_hip_model_generate_greedy, 32 tokens at a 2048-token KV "
+                                    "context, 48 layers (attention, norms, router, fused experts, head on the device)")
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline(args.cpu_tokens)
     print(json.dumps(out), flush=True)
