@@ -372,8 +372,10 @@ def bench_staging(args, torch, b, hip):
     884,736 B each, down Q6_K 1,290,240 B; 391.6 MB) from pageable host
     memory into HBM, (a) the reference's way - per expert three h2d() calls and
     a sync() (ExpertPager::stage_to_vram, eahmmf.h:1009-1013), through
-    eahmmf_hip_h2d/eahmmf_hip_sync - and (b) one eahmmf_hip_h2d_batch of all
-    384 components through the pinned staging ring."""
+    eahmmf_hip_h2d/eahmmf_hip_sync - (b) one eahmmf_hip_h2d_batch of all
+    384 components through the pinned staging ring, and (c) the same batch
+    queued with eahmmf_hip_h2d_batch_async (the caller's thread free once it
+    is queued)."""
     E_, comp = 128, (884_736, 884_736, 1_290_240)
     rng = np.random.default_rng(9)
     host = [[rng.integers(0, 256, n, dtype=np.uint8) for n in comp] for _ in range(E_)]
@@ -409,6 +411,18 @@ def bench_staging(args, torch, b, hip):
         return min(t)
 
     t_ref, t_batch = best(per_expert, 3), best(batch, 3)
+    # (c) the same batch queued asynchronously: how long the caller's thread is
+    # held (the call returns once the batch is queued to the staging thread),
+    # and when the bytes have landed (host wait on the ticket)
+    t_ret, t_land = [], []
+    for _ in range(3):
+        torch.cuda.synchronize()
+        ticket = ctypes.c_uint64(0)
+        t0 = time.perf_counter()
+        assert hip.eahmmf_hip_h2d_batch_async(copies, 3 * E_, ctypes.byref(ticket)) == 0, b.last_error()
+        t_ret.append(time.perf_counter() - t0)
+        assert hip.eahmmf_hip_h2d_batch_wait(ticket.value, None) == 0, b.last_error()
+        t_land.append(time.perf_counter() - t0)
     probe = [(7, 2), (E_ - 1, 0)]  # spot check: two components read back exactly
     for e, c in probe:
         got = dev[e * foot + offs[c]:e * foot + offs[c] + comp[c]].cpu().numpy()
@@ -423,7 +437,12 @@ def bench_staging(args, torch, b, hip):
         "batch_ms": round(t_batch * 1e3, 2),
         "per_expert_h2d_sync": {"GB_s": round(total / t_ref / 1e9, 2), "ms": round(t_ref * 1e3, 2),
                                 "what": "3 x eahmmf_hip_h2d + eahmmf_hip_sync per expert (the reference pager)"},
-        "speedup": round(t_ref / t_batch, 2)}), flush=True)
+        "speedup": round(t_ref / t_batch, 2),
+        "async": {"return_us": round(min(t_ret) * 1e6, 1), "landed_ms": round(min(t_land) * 1e3, 2),
+                  "GB_s": round(total / min(t_land) / 1e9, 2),
+                  "what": "eahmmf_hip_h2d_batch_async of the same 384 copies: time until the call returns "
+                          "(the caller's thread is free from then on) and until eahmmf_hip_h2d_batch_wait says "
+                          "the bytes have landed"}}), flush=True)
 
 
 def bench_dropin(args, torch, b, hip):

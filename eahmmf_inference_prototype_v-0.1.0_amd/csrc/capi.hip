@@ -17,6 +17,8 @@
 #include <string>
 #include <vector>
 #include <algorithm>
+#include <condition_variable>
+#include <deque>
 #include <thread>
 
 #include "../../include/eahmmf_hip.h"
@@ -69,6 +71,7 @@ struct DevCtx {
     uint8_t* ring[kRingSlots] = {};
     hipEvent_t ring_done[kRingSlots] = {};  // recorded after the copies out of each slot
     bool ring_ready = false;
+    int ring_next = 0;  // the slot the next staged batch starts in
 };
 
 // 1: single fused launch where the shape allows it; 0: route + two-kernel path.
@@ -293,6 +296,162 @@ void fill_slot(uint8_t* slot, const std::vector<Piece>& ps, size_t total, int nt
     range(0, std::min(total, per));
     if (done < total) range(done, total);
     for (std::thread& x : th) x.join();
+}
+
+// Every copy has both pointers unless it is empty.
+bool copies_ok(const eahmmf_hip_copy* copies, int n) {
+    if (n < 0 || (n > 0 && !copies)) return set_error("null argument"), false;
+    for (int i = 0; i < n; i++)
+        if (copies[i].bytes && (!copies[i].dev_dst || !copies[i].host_src))
+            return set_error("copy %d: null pointer", i), false;
+    return true;
+}
+
+// The copies of one batch through the ring: per slot, wait until its previous
+// copies have left it, fill it on the CPU, then one DMA per piece on the
+// slot's stream and an event behind them.  Pieces start 256-byte aligned in
+// a slot; small copies share one.
+bool stage_copies(DevCtx* c, const eahmmf_hip_copy* copies, int n) {
+    const int nt = stage_threads();
+    bool ok = true;
+    int slot = c->ring_next;
+    std::vector<Piece> ps;
+    size_t fill = 0;
+    auto flush = [&]() -> bool {
+        if (ps.empty()) return true;
+        if (!hip_ok(hipEventSynchronize(c->ring_done[slot]), "staging wait")) return false;
+        fill_slot(c->ring[slot], ps, fill, nt);
+        for (const Piece& q : ps)
+            if (!hip_ok(hipMemcpyAsync(q.dst, c->ring[slot] + q.at, q.n, hipMemcpyHostToDevice,
+                                       c->copy_stream[slot]),
+                        "staging copy"))
+                return false;
+        if (!hip_ok(hipEventRecord(c->ring_done[slot], c->copy_stream[slot]), "staging record")) return false;
+        slot = (slot + 1) % kRingSlots;
+        ps.clear();
+        fill = 0;
+        return true;
+    };
+    for (int i = 0; ok && i < n; i++) {
+        uint8_t* dst = (uint8_t*)copies[i].dev_dst;
+        const uint8_t* src = (const uint8_t*)copies[i].host_src;
+        for (size_t off = 0; ok && off < copies[i].bytes;) {
+            const size_t m = std::min(copies[i].bytes - off, kRingChunk - fill);
+            ps.push_back(Piece{dst + off, src + off, m, fill});
+            off += m;
+            fill = std::min(kRingChunk, (fill + m + 255) & ~(size_t)255);
+            if (fill == kRingChunk) ok = flush();
+        }
+    }
+    if (ok) ok = flush();
+    c->ring_next = slot;
+    return ok;
+}
+
+// Asynchronous staging (eahmmf_hip_h2d_batch_async): one worker thread per
+// device takes batches in order, stages them through the ring and records a
+// completion event behind every slot's copies (on a join stream that waits
+// for the four slots).  A ticket's batch has landed once its event has
+// completed; completed events are destroyed when the next batch is queued.
+// The worker and the state live until the process ends (the thread is
+// detached and idles on its condition variable).
+constexpr int kMaxDev = 64;
+struct Stager {
+    DevCtx* c = nullptr;
+    int dev = 0;
+    hipStream_t join = nullptr;
+    std::mutex qmu;
+    std::condition_variable qcv, dcv;
+    std::deque<std::pair<uint64_t, std::vector<eahmmf_hip_copy>>> q;
+    uint64_t next = 1, issued = 0;  // tickets handed out; batches whose copies are all queued
+    std::map<uint64_t, hipEvent_t> ev;
+    std::map<uint64_t, std::string> failed;  // the worker's error message per failed batch
+    bool stop = false, running = false;
+};
+Stager* g_stager[kMaxDev] = {};
+
+void stager_main(Stager* st) {
+    (void)hipSetDevice(st->dev);
+    std::unique_lock<std::mutex> lk(st->qmu);
+    for (;;) {
+        st->qcv.wait(lk, [&] { return st->stop || !st->q.empty(); });
+        if (st->q.empty()) break;  // stop
+        auto job = std::move(st->q.front());
+        st->q.pop_front();
+        lk.unlock();
+        hipEvent_t e = nullptr;
+        bool ok = hip_ok(hipEventCreateWithFlags(&e, hipEventDisableTiming), "hipEventCreate(staging)");
+        ok = ok && stage_copies(st->c, job.second.data(), (int)job.second.size());
+        for (int s = 0; ok && s < kRingSlots; s++)
+            ok = hip_ok(hipStreamWaitEvent(st->join, st->c->ring_done[s], 0), "staging join");
+        ok = ok && hip_ok(hipEventRecord(e, st->join), "staging record");
+        lk.lock();
+        if (ok) {
+            st->ev[job.first] = e;
+        } else {
+            st->failed[job.first] = g_last_error;
+            if (e) (void)hipEventDestroy(e);
+        }
+        st->issued = job.first;
+        st->dcv.notify_all();
+    }
+    st->running = false;
+    st->dcv.notify_all();
+}
+
+// Destroys the events of landed batches (caller holds qmu).
+void retire_done(Stager* st) {
+    for (auto it = st->ev.begin(); it != st->ev.end();) {
+        if (hipEventQuery(it->second) == hipSuccess) {
+            (void)hipEventDestroy(it->second);
+            it = st->ev.erase(it);
+        } else {
+            ++it;
+        }
+    }
+}
+
+Stager* stager_for(DevCtx* c) {
+    int dev = 0;
+    if (!hip_ok(hipGetDevice(&dev), "hipGetDevice")) return nullptr;
+    if (dev < 0 || dev >= kMaxDev) return set_error("device %d out of range", dev), nullptr;
+    std::lock_guard<std::mutex> g(g_mu);
+    if (!ensure_ring(c)) return nullptr;
+    Stager*& st = g_stager[dev];
+    if (st && st->running) return st;
+    if (!st) {
+        st = new (std::nothrow) Stager;
+        if (!st) return set_error("out of memory"), nullptr;
+        st->dev = dev;
+    }
+    st->c = c;
+    if (!st->join && !hip_ok(hipStreamCreateWithFlags(&st->join, hipStreamNonBlocking), "hipStreamCreate(join)"))
+        return nullptr;
+    st->stop = false;
+    st->running = true;
+    try {
+        std::thread(stager_main, st).detach();
+    } catch (...) {
+        st->running = false;
+        return set_error("could not start the staging thread"), nullptr;
+    }
+    return st;
+}
+
+// Stops the device's staging worker once its queue is empty (shutdown).
+void stop_stager(int dev) {
+    Stager* st = dev >= 0 && dev < kMaxDev ? g_stager[dev] : nullptr;
+    if (!st) return;
+    std::unique_lock<std::mutex> lk(st->qmu);
+    st->stop = true;
+    st->qcv.notify_all();
+    st->dcv.wait(lk, [&] { return !st->running; });
+    for (auto& kv : st->ev) {
+        (void)hipEventSynchronize(kv.second);
+        (void)hipEventDestroy(kv.second);
+    }
+    st->ev.clear();
+    st->c = nullptr;
 }
 
 // A single token (the reference's decode calls, nb = 1) runs on the decode
@@ -897,59 +1056,72 @@ int eahmmf_hip_mem_info(size_t* free_bytes, size_t* total_bytes) {
 }
 
 int eahmmf_hip_h2d_batch(const eahmmf_hip_copy* copies, int n) {
-    if (n < 0 || (n > 0 && !copies)) return set_error("null argument"), -1;
-    for (int i = 0; i < n; i++)
-        if (copies[i].bytes && (!copies[i].dev_dst || !copies[i].host_src))
-            return set_error("copy %d: null pointer", i), -1;
+    if (!copies_ok(copies, n)) return -1;
     if (n == 0) return 0;
     DevCtx* c = ctx_for_current_device();
-    if (!c || !ensure_ring(c)) return -2;
+    if (!c) return -2;
     // work already queued on the library's stream finishes first
     if (!drain(c, true)) return -2;
-    const int nt = stage_threads();
-    bool ok = true;
-    int slot = 0;
-    std::vector<Piece> ps;
-    size_t fill = 0;
-    // slot: wait until its previous copies have left it, fill it on the CPU,
-    // then one DMA per piece on the staging stream and an event behind them
-    auto flush = [&]() -> bool {
-        if (ps.empty()) return true;
-        if (!hip_ok(hipEventSynchronize(c->ring_done[slot]), "staging wait")) return false;
-        fill_slot(c->ring[slot], ps, fill, nt);
-        for (const Piece& q : ps)
-            if (!hip_ok(hipMemcpyAsync(q.dst, c->ring[slot] + q.at, q.n, hipMemcpyHostToDevice,
-                                       c->copy_stream[slot]),
-                        "staging copy"))
-                return false;
-        if (!hip_ok(hipEventRecord(c->ring_done[slot], c->copy_stream[slot]), "staging record")) return false;
-        slot = (slot + 1) % kRingSlots;
-        ps.clear();
-        fill = 0;
-        return true;
-    };
-    for (int i = 0; ok && i < n; i++) {
-        uint8_t* dst = (uint8_t*)copies[i].dev_dst;
-        const uint8_t* src = (const uint8_t*)copies[i].host_src;
-        for (size_t off = 0; ok && off < copies[i].bytes;) {
-            const size_t m = std::min(copies[i].bytes - off, kRingChunk - fill);
-            ps.push_back(Piece{dst + off, src + off, m, fill});
-            off += m;
-            fill = std::min(kRingChunk, (fill + m + 255) & ~(size_t)255);  // pieces start 256-byte aligned
-            if (fill == kRingChunk) ok = flush();
-        }
-    }
-    if (ok) ok = flush();
-    for (int s = 0; s < kRingSlots; s++) {  // drained on every path
-        const hipError_t e = hipStreamSynchronize(c->copy_stream[s]);
-        if (ok && e != hipSuccess) ok = hip_ok(e, "staging drain");
-    }
-    return ok ? 0 : -2;
+    uint64_t ticket = 0;
+    const int r = eahmmf_hip_h2d_batch_async(copies, n, &ticket);
+    return r != 0 ? r : eahmmf_hip_h2d_batch_wait(ticket, nullptr);
+}
+
+int eahmmf_hip_h2d_batch_async(const eahmmf_hip_copy* copies, int n, uint64_t* ticket) {
+    if (!ticket) return set_error("null ticket"), -1;
+    if (!copies_ok(copies, n)) return -1;
+    DevCtx* c = ctx_for_current_device();
+    if (!c) return -2;
+    Stager* st = stager_for(c);
+    if (!st) return -2;
+    std::lock_guard<std::mutex> lk(st->qmu);
+    retire_done(st);
+    const uint64_t id = st->next++;
+    st->q.emplace_back(id, std::vector<eahmmf_hip_copy>(copies, copies + n));
+    st->qcv.notify_all();
+    *ticket = id;
+    return 0;
+}
+
+int eahmmf_hip_h2d_batch_wait(uint64_t ticket, void* stream) {
+    int dev = 0;
+    if (!hip_ok(hipGetDevice(&dev), "hipGetDevice")) return -2;
+    Stager* st = dev >= 0 && dev < kMaxDev ? g_stager[dev] : nullptr;
+    if (!st || ticket == 0) return set_error("unknown staging ticket"), -1;
+    std::unique_lock<std::mutex> lk(st->qmu);
+    if (ticket >= st->next) return set_error("unknown staging ticket"), -1;
+    st->dcv.wait(lk, [&] { return st->issued >= ticket; });
+    auto f = st->failed.find(ticket);
+    if (f != st->failed.end()) return set_error("staging batch %llu: %s", (unsigned long long)ticket, f->second.c_str()), -2;
+    auto e = st->ev.find(ticket);
+    if (e == st->ev.end()) return 0;  // landed and retired
+    // held under the lock: the event is not retired meanwhile
+    const hipError_t r = stream ? hipStreamWaitEvent((hipStream_t)stream, e->second, 0) : hipEventSynchronize(e->second);
+    return hip_ok(r, "staging wait") ? 0 : -2;
+}
+
+int eahmmf_hip_h2d_batch_query(uint64_t ticket) {
+    int dev = 0;
+    if (!hip_ok(hipGetDevice(&dev), "hipGetDevice")) return -2;
+    Stager* st = dev >= 0 && dev < kMaxDev ? g_stager[dev] : nullptr;
+    if (!st || ticket == 0) return set_error("unknown staging ticket"), -1;
+    std::lock_guard<std::mutex> lk(st->qmu);
+    if (ticket >= st->next) return set_error("unknown staging ticket"), -1;
+    if (st->issued < ticket) return 0;
+    auto f = st->failed.find(ticket);
+    if (f != st->failed.end()) return set_error("staging batch %llu: %s", (unsigned long long)ticket, f->second.c_str()), -2;
+    auto e = st->ev.find(ticket);
+    if (e == st->ev.end()) return 1;
+    const hipError_t r = hipEventQuery(e->second);
+    if (r == hipSuccess) return 1;
+    if (r == hipErrorNotReady) return 0;
+    return hip_ok(r, "staging query") ? 0 : -2;
 }
 
 void eahmmf_hip_shutdown(void) {
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess) return;
+    stop_stager(dev);
     std::lock_guard<std::mutex> g(g_mu);
     auto it = g_ctx.find(dev);
     if (it == g_ctx.end()) return;
@@ -967,6 +1139,10 @@ void eahmmf_hip_shutdown(void) {
         if (c.copy_stream[s]) (void)hipStreamDestroy(c.copy_stream[s]);
     }
     if (c.stream) (void)hipStreamDestroy(c.stream);
+    if (dev >= 0 && dev < kMaxDev && g_stager[dev] && g_stager[dev]->join) {
+        (void)hipStreamDestroy(g_stager[dev]->join);
+        g_stager[dev]->join = nullptr;
+    }
     g_ctx.erase(it);
 }
 

@@ -30,7 +30,8 @@ EXPORTS = (
     "eahmmf_hip_model_set_trace", "eahmmf_hip_model_trace", "eahmmf_hip_model_trace_clear", "eahmmf_hip_model_stream",
     "eahmmf_hip_model_free", "eahmmf_hip_model_set_sequences", "eahmmf_hip_model_forward_seq",
     "eahmmf_hip_model_decode_seqs", "eahmmf_hip_set_dense_mfma", "eahmmf_hip_moe_layer_decode_xn_async", "eahmmf_hip_set_grouped_wave_max",
-    "eahmmf_hip_set_grouped_dot_max",
+    "eahmmf_hip_set_grouped_dot_max", "eahmmf_hip_h2d_batch_async", "eahmmf_hip_h2d_batch_wait",
+    "eahmmf_hip_h2d_batch_query",
 )
 
 
@@ -133,6 +134,9 @@ def load(path=LIB_PATH):
         "eahmmf_hip_expf_ref_async": (c_int, [vp, vp, c_i64, vp]),
         "eahmmf_hip_moe_decode_resident": (c_bool, [ctypes.POINTER(Expert), vp, c_int, vp, vp, vp]),
         "eahmmf_hip_h2d_batch": (c_int, [ctypes.POINTER(Copy), c_int]),
+        "eahmmf_hip_h2d_batch_async": (c_int, [ctypes.POINTER(Copy), c_int, ctypes.POINTER(ctypes.c_uint64)]),
+        "eahmmf_hip_h2d_batch_wait": (c_int, [ctypes.c_uint64, vp]),
+        "eahmmf_hip_h2d_batch_query": (c_int, [ctypes.c_uint64]),
         "eahmmf_hip_model_create": (vp, [ctypes.POINTER(ModelDesc)]),
         "eahmmf_hip_model_forward": (c_int, [vp, vp, c_int, c_int, vp]),
         "eahmmf_hip_model_eval": (c_int, [vp, vp, c_int, c_int, c_int, vp]),

@@ -71,6 +71,19 @@ struct HipDeviceOn : Base {
     // call through the library's pinned staging ring (valid for compute when
     // it returns), for preloading experts instead of one h2d() + sync() each.
     bool h2d_batch(const eahmmf_hip_copy* copies, int n) { return eahmmf_hip_h2d_batch(copies, n) == 0; }
+    // Not in the reference's interface either: the same batch queued to the
+    // library's staging thread (asynchronous prefetch, which the reference
+    // lists as not implemented, README.md:379).  Returns a ticket (0 on
+    // failure); the sources must stay valid until h2d_batch_wait(ticket)
+    // has returned true.  With a stream, work queued on it afterwards waits
+    // on the device for the bytes; without, the host waits until they land.
+    uint64_t h2d_batch_async(const eahmmf_hip_copy* copies, int n) {
+        uint64_t t = 0;
+        return eahmmf_hip_h2d_batch_async(copies, n, &t) == 0 ? t : 0;
+    }
+    bool h2d_batch_wait(uint64_t ticket, void* stream = nullptr) {
+        return eahmmf_hip_h2d_batch_wait(ticket, stream) == 0;
+    }
     bool cpu_readable() const override { return false; }
     size_t total_memory() const override { return total; }
     size_t free_memory() const override {

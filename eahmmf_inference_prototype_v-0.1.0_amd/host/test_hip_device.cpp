@@ -146,6 +146,21 @@ static void check_batch(eahmmf_hip::HipDevice& dev) {
     }
     CHECK(eahmmf_hip_h2d_batch(nullptr, 1) == -1);
     CHECK(eahmmf_hip_h2d_batch(cp.data(), 0) == 0);
+    // the asynchronous form: both halves queued at once, then waited for
+    for (int i = 0; i < n; i++)
+        for (auto& b : host[i]) b = (uint8_t)rng();
+    const uint64_t t0 = dev.h2d_batch_async(cp.data(), n / 2);
+    const uint64_t t1 = dev.h2d_batch_async(cp.data() + n / 2, n - n / 2);
+    CHECK(t0 != 0 && t1 > t0);
+    CHECK(dev.h2d_batch_wait(t1));
+    CHECK(dev.h2d_batch_wait(t0));
+    CHECK(eahmmf_hip_h2d_batch_query(t0) == 1 && eahmmf_hip_h2d_batch_query(t1) == 1);
+    for (int i = 0; i < n; i++) {
+        if (!sizes[i] || !ptrs[i]) continue;
+        std::vector<uint8_t> back(sizes[i]);
+        CHECK(dev.d2h(back.data(), ptrs[i], sizes[i]));
+        CHECK(back == host[i]);
+    }
     for (void* p : ptrs)
         if (p) dev.release(p, 0);
 }

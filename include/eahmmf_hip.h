@@ -260,6 +260,26 @@ typedef struct {
  * experts resident at once.  Single-threaded caller per device.  0 on
  * success, -1 on bad arguments, -2 on a HIP error. */
 int eahmmf_hip_h2d_batch(const eahmmf_hip_copy* copies, int n);
+/* Asynchronous bulk staging (no counterpart in the reference, whose README.md:379
+ * lists asynchronous prefetch as not implemented): queues the same copies to
+ * a per-device worker thread and returns at once with a ticket (> 0) in
+ * *ticket.  The worker stages batches in order through the ring above while
+ * the caller goes on (e.g. computing a layer while the next layer's experts
+ * are made resident).  The host sources must stay valid and unchanged, and
+ * the destinations unused, until the batch has landed.  Unlike the
+ * synchronous form it does not wait for work queued on the library stream.
+ * 0 on success, -1 on bad arguments, -2 on a HIP error. */
+int eahmmf_hip_h2d_batch_async(const eahmmf_hip_copy* copies, int n, uint64_t* ticket);
+/* Waits for batch `ticket`.  With a stream, the host waits only until the
+ * batch's copies are all queued, and the stream waits (on the device) until
+ * they have landed, so work queued on it afterwards sees the bytes; with a
+ * null stream the host waits until they have landed.  0 on success, -1 for a
+ * ticket never handed out, -2 when the batch failed (eahmmf_hip_last_error()
+ * names the cause). */
+int eahmmf_hip_h2d_batch_wait(uint64_t ticket, void* stream);
+/* 1 when batch `ticket` has landed, 0 while it is pending, -1 for a ticket
+ * never handed out, -2 when it failed. */
+int eahmmf_hip_h2d_batch_query(uint64_t ticket);
 
 /* ---- diagnostics / lifetime ------------------------------------------- */
 /* Selects the single-launch fused expert block (1, the default) or the

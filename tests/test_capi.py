@@ -2,6 +2,8 @@
 import os
 import re
 
+import ctypes
+
 import numpy as np
 import pytest
 
@@ -58,6 +60,12 @@ def test_invalid_arguments_fail_without_touching_the_device(binding, hip):
     bad = (binding.Copy * 1)(binding.Copy(None, x.ctypes.data, 16))
     assert hip.eahmmf_hip_h2d_batch(bad, 1) == -1
     assert "null pointer" in hip.eahmmf_hip_last_error().decode()
+    ticket = ctypes.c_uint64(0)
+    assert hip.eahmmf_hip_h2d_batch_async(None, 1, ctypes.byref(ticket)) == -1
+    assert hip.eahmmf_hip_h2d_batch_async(bad, 1, ctypes.byref(ticket)) == -1
+    assert "null pointer" in hip.eahmmf_hip_last_error().decode()
+    assert hip.eahmmf_hip_h2d_batch_async(bad, 1, None) == -1
+    assert "ticket" in hip.eahmmf_hip_last_error().decode()
     # the model's sequence entry points: a null model is rejected up front
     assert hip.eahmmf_hip_model_set_sequences(None, 2) == -1
     assert hip.eahmmf_hip_model_forward_seq(None, 0, ids.ctypes.data, 1, 0, None) == -1

@@ -307,6 +307,49 @@ def test_h2d_batch_round_trip(torch_dev, binding, hip):
         assert np.array_equal(d[:n].cpu().numpy(), h)
 
 
+def test_h2d_batch_async_round_trip(torch_dev, binding, hip):
+    """Asynchronous staging: two batches queued back to back return at once
+    with increasing tickets; one is waited for on a stream (a copy queued on
+    that stream afterwards sees its bytes), the other on the host; both land
+    byte for byte, query then reports them landed, and the synchronous form
+    still works after them."""
+    import ctypes
+    torch = torch_dev
+    rng = np.random.default_rng(12)
+    batches = [[884736, 1290240, 1, 4097, (33 << 20) + 5], [0, 1290240, 32 << 20, 77]]
+    host, dev, tickets = [], [], []
+    for sizes in batches:
+        h = [rng.integers(0, 256, n, dtype=np.uint8) for n in sizes]
+        d = [torch.empty(max(n, 1), dtype=torch.uint8, device="cuda") for n in sizes]
+        cp = (binding.Copy * len(sizes))()
+        for i, n in enumerate(sizes):
+            cp[i] = binding.Copy(d[i].data_ptr(), h[i].ctypes.data, n)
+        t = ctypes.c_uint64(0)
+        assert hip.eahmmf_hip_h2d_batch_async(cp, len(sizes), ctypes.byref(t)) == 0, hip.eahmmf_hip_last_error()
+        host.append(h)
+        dev.append(d)
+        tickets.append(t.value)
+    assert 0 < tickets[0] < tickets[1]
+    assert hip.eahmmf_hip_h2d_batch_query(tickets[1] + 1000) == -1
+    st = torch.cuda.Stream()
+    assert hip.eahmmf_hip_h2d_batch_wait(tickets[0], ctypes.c_void_p(st.cuda_stream)) == 0
+    with torch.cuda.stream(st):
+        got0 = [x.clone() for x in dev[0]]
+    st.synchronize()
+    assert hip.eahmmf_hip_h2d_batch_wait(tickets[1], None) == 0
+    for h, d in zip(host[0], got0):
+        assert np.array_equal(d[:len(h)].cpu().numpy(), h)
+    for h, d in zip(host[1], dev[1]):
+        assert np.array_equal(d[:len(h)].cpu().numpy(), h)
+    assert hip.eahmmf_hip_h2d_batch_query(tickets[0]) == 1
+    assert hip.eahmmf_hip_h2d_batch_query(tickets[1]) == 1
+    x = rng.integers(0, 256, 4099, dtype=np.uint8)
+    y = torch.empty(4099, dtype=torch.uint8, device="cuda")
+    one = (binding.Copy * 1)(binding.Copy(y.data_ptr(), x.ctypes.data, 4099))
+    assert hip.eahmmf_hip_h2d_batch(one, 1) == 0
+    assert np.array_equal(y.cpu().numpy(), x)
+
+
 def test_route_topk_vs_oracle(torch_dev, hip):
     rng = np.random.default_rng(3)
     nb, E, k = 257, 128, 8
