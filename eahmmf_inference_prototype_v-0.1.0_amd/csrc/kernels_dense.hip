@@ -352,40 +352,94 @@ __global__ __launch_bounds__((AttnShape<HD, GRP>::W * 64)) void attention_kernel
     // thread takes four dimensions of one head and loads, in one round, the
     // head's m and l and its four o values of every split.
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-    for (int i = tid; i < GRP * HD / 4; i += W * 64) {
-        const int hh = i / (HD / 4), d = (i % (HD / 4)) * 4;
-        const float* r = base + (size_t)hh * a.n_split * rec;
+    if constexpr (GRP * HD / 4 <= W * 64) {
+        // One round of loads: thread (head, four dimensions) takes the o
+        // values of every split, thread (head, split) that split's m and l.
+        // The split factors expf(m_u - M) are then formed once per (head,
+        // split) and shared through LDS instead of by every thread of the
+        // head (32 expf each).
+        __shared__ float msh[GRP][kMaxSplit], lsh[GRP][kMaxSplit];
+        const int hh = tid / (HD / 4), d = (tid % (HD / 4)) * 4;
+        const bool mine = tid < GRP * HD / 4;
+        const float* r = base + (size_t)(mine ? hh : 0) * a.n_split * rec;
         float4 ov[kMaxSplit];
-        float2 ml[kMaxSplit];
 #pragma unroll
-        for (int u = 0; u < kMaxSplit; u++) {
-            if (u < a.n_split) {
-                ov[u] = *reinterpret_cast<const float4*>(r + (size_t)u * rec + d);
-                ml[u] = *reinterpret_cast<const float2*>(r + (size_t)u * rec + HD);
-            } else {
-                ov[u] = make_float4(0.f, 0.f, 0.f, 0.f);
-                ml[u] = make_float2(-INFINITY, 0.f);
+        for (int u = 0; u < kMaxSplit; u++)
+            ov[u] = mine && u < a.n_split ? *reinterpret_cast<const float4*>(r + (size_t)u * rec + d)
+                                          : make_float4(0.f, 0.f, 0.f, 0.f);
+        const int fh = tid / kMaxSplit, fu = tid % kMaxSplit;
+        if (tid < GRP * kMaxSplit) {
+            float2 ml = make_float2(-INFINITY, 0.f);
+            if (fu < a.n_split) ml = *reinterpret_cast<const float2*>(base + ((size_t)fh * a.n_split + fu) * rec + HD);
+            msh[fh][fu] = ml.x;
+            lsh[fh][fu] = ml.y;
+        }
+        __syncthreads();
+        float fac = 0.f;
+        if (tid < GRP * kMaxSplit) {
+            float M = -INFINITY;
+#pragma unroll
+            for (int u = 0; u < kMaxSplit; u++) M = fmaxf(M, msh[fh][u]);
+            const float mu = msh[fh][fu];
+            fac = mu == -INFINITY ? 0.f : expf(mu - M);
+        }
+        __syncthreads();  // every M is formed before the factors overwrite the maxima
+        if (tid < GRP * kMaxSplit) msh[fh][fu] = fac;
+        __syncthreads();
+        if (mine) {
+            float L = 0.f;
+            float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+            for (int u = 0; u < kMaxSplit; u++) {
+                const float fu_ = msh[hh][u];
+                L = __builtin_fmaf(lsh[hh][u], fu_, L);
+                acc.x = __builtin_fmaf(ov[u].x, fu_, acc.x);
+                acc.y = __builtin_fmaf(ov[u].y, fu_, acc.y);
+                acc.z = __builtin_fmaf(ov[u].z, fu_, acc.z);
+                acc.w = __builtin_fmaf(ov[u].w, fu_, acc.w);
             }
+            float* o = a.out + (size_t)t * QD + (size_t)(kvh * GRP + hh) * HD + d;
+            o[0] = acc.x / L;
+            o[1] = acc.y / L;
+            o[2] = acc.z / L;
+            o[3] = acc.w / L;
         }
-        float M = -INFINITY;
+    } else {
+        for (int i = tid; i < GRP * HD / 4; i += W * 64) {
+            const int hh = i / (HD / 4), d = (i % (HD / 4)) * 4;
+            const float* r = base + (size_t)hh * a.n_split * rec;
+            float4 ov[kMaxSplit];
+            float2 ml[kMaxSplit];
 #pragma unroll
-        for (int u = 0; u < kMaxSplit; u++) M = fmaxf(M, ml[u].x);
-        float L = 0.f;
-        float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+            for (int u = 0; u < kMaxSplit; u++) {
+                if (u < a.n_split) {
+                    ov[u] = *reinterpret_cast<const float4*>(r + (size_t)u * rec + d);
+                    ml[u] = *reinterpret_cast<const float2*>(r + (size_t)u * rec + HD);
+                } else {
+                    ov[u] = make_float4(0.f, 0.f, 0.f, 0.f);
+                    ml[u] = make_float2(-INFINITY, 0.f);
+                }
+            }
+            float M = -INFINITY;
 #pragma unroll
-        for (int u = 0; u < kMaxSplit; u++) {
-            const float f = ml[u].x == -INFINITY ? 0.f : expf(ml[u].x - M);
-            L = __builtin_fmaf(ml[u].y, f, L);
-            acc.x = __builtin_fmaf(ov[u].x, f, acc.x);
-            acc.y = __builtin_fmaf(ov[u].y, f, acc.y);
-            acc.z = __builtin_fmaf(ov[u].z, f, acc.z);
-            acc.w = __builtin_fmaf(ov[u].w, f, acc.w);
+            for (int u = 0; u < kMaxSplit; u++) M = fmaxf(M, ml[u].x);
+            float L = 0.f;
+            float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+            for (int u = 0; u < kMaxSplit; u++) {
+                const float f = ml[u].x == -INFINITY ? 0.f : expf(ml[u].x - M);
+                L = __builtin_fmaf(ml[u].y, f, L);
+                acc.x = __builtin_fmaf(ov[u].x, f, acc.x);
+                acc.y = __builtin_fmaf(ov[u].y, f, acc.y);
+                acc.z = __builtin_fmaf(ov[u].z, f, acc.z);
+                acc.w = __builtin_fmaf(ov[u].w, f, acc.w);
+            }
+            float* o = a.out + (size_t)t * QD + (size_t)(kvh * GRP + hh) * HD + d;
+            o[0] = acc.x / L;
+            o[1] = acc.y / L;
+            o[2] = acc.z / L;
+            o[3] = acc.w / L;
         }
-        float* o = a.out + (size_t)t * QD + (size_t)(kvh * GRP + hh) * HD + d;
-        o[0] = acc.x / L;
-        o[1] = acc.y / L;
-        o[2] = acc.z / L;
-        o[3] = acc.w / L;
     }
     if (tid == 0) __hip_atomic_store(&a.cnt[t * n_kv + kvh], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
