@@ -828,9 +828,10 @@ def router_variant(b, hip, torch, tables, dx, dy, dids, dw, shape, stream, R, NS
     torch.cuda.synchronize()
     assert hip.eahmmf_hip_device_flags() == 0
     us = e0.elapsed_time(e1) * 1e3 / steps
-    return {"us_per_layer_token": round(us, 3), "launches": 2,
-            "what": "RMSNorm + F32 router matmul + routing + expert block from the residual stream "
-                    "(eahmmf_hip_moe_layer_decode_xn_async), HIP events over back-to-back layer-tokens"}
+    return {"us_per_layer_token": round(us, 3), "launches": 1,
+            "what": "RMSNorm + F32 router matmul + routing + expert block from the residual stream in one "
+                    "launch (eahmmf_hip_moe_layer_decode_xn_async: the router matmul split over the fused "
+                    "kernel's workgroups), HIP events over back-to-back layer-tokens"}
 
 
 def host_io_rate(b, hip, torch, dgate, dup, ddown, steps=2000):

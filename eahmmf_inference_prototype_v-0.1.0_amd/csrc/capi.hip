@@ -776,6 +776,28 @@ int eahmmf_hip_moe_layer_decode_xn_async(const eahmmf_hip_moe_shape* shape, cons
     if (!gemv_supported(kF32, s.D, (size_t)s.D * 4)) return set_error("router: D=%d not supported", s.D), -1;
     DevCtx* c = ctx_for_current_device();
     if (!c) return -2;
+    // one launch where the fused kernel takes the shape: the norm, the router
+    // matmul (split over every workgroup) and the routing in the kernel
+    if (fused_enabled() && fused_supported(s, k, n_expert) && grow_device(c->dh, (size_t)k * s.FF * sizeof(float)) &&
+        grow_fused(c, s, k)) {
+        FusedArgsHost f;
+        f.shape = s;
+        f.k = k;
+        f.n_expert = n_expert;
+        f.mode = 3;
+        f.table = (const ExpertEntry*)dev_table;
+        f.router = dev_router;
+        f.norm_w = dev_norm_w;
+        f.eps = eps;
+        f.xn_out = dev_xn_out;
+        f.logits_out = dev_logits_out;
+        f.ids_out = dev_ids_out;
+        f.w_out = dev_w_out;
+        f.x = dev_x;
+        f.y = dev_y;
+        const hipError_t e = launch_moe_fused(f, c->fused, (hipStream_t)stream);
+        if (e != hipErrorNotSupported) return hip_ok(e, "fused moe layer launch (router in the kernel)") ? 0 : -3;
+    }
     float* xn = dev_xn_out;
     float* logits = dev_logits_out;
     if ((dev_norm_w && !xn) || !logits) {

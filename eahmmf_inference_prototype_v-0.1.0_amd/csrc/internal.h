@@ -66,7 +66,9 @@ hipError_t launch_moe_decode_routed(const MoeShape& s, const ExpertEntry* table,
 struct FusedArgsHost {
     MoeShape shape;
     int k = 0, n_expert = 0;
-    int mode = 0;  // 0: direct slots, 1: logits + table (routing in the kernel), 2: ids/w + table
+    int mode = 0;  // 0: direct slots, 1: logits + table (routing in the kernel), 2: ids/w + table,
+                   // 3: residual stream + router + table (norm, router matmul and routing in the kernel;
+                   // hipErrorNotSupported when the launch has fewer workgroups than experts)
     DecodeSlots direct{};
     const ExpertEntry* table = nullptr;
     const float* logits = nullptr;
@@ -76,6 +78,13 @@ struct FusedArgsHost {
     float* w_out = nullptr;
     const float* x = nullptr;
     float* y = nullptr;
+    // mode 3: F32 router rows [n_expert][D], the input's RMSNorm weights (null:
+    // none) and eps, optional outputs (normalized input, logits)
+    const float* router = nullptr;
+    const float* norm_w = nullptr;
+    float eps = 0.f;
+    float* xn_out = nullptr;
+    float* logits_out = nullptr;
 };
 
 // Sync buffer of a fused scratch set: kSyncWords words, zero before the first

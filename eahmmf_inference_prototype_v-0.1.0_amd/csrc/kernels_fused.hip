@@ -134,9 +134,25 @@ struct FusedArgs {
     uint64_t* hx;     // k * FF words: h value bits | epoch << 32
     uint64_t* ypart;  // np * D words: partial value bits | epoch << 32
     unsigned* sync;
+    // mode 3 (routing from the residual stream): F32 router rows [n_expert][D],
+    // the input's RMSNorm weights (null: the input is used as it is) and eps,
+    // optional outputs of block 0 (the normalized input, the logits), and the
+    // router dot's slices per logit
+    const float* router;
+    const float* norm_w;
+    float eps;
+    int rslices;
+    float* xn_out;
+    float* logits_out;
     // last: read only in mode 0
     DecodeSlots direct;
 };
+// Exchange words of mode 3's router partials (value | epoch << 32), in the
+// launch's sync area from word kLogitWord (64-bit aligned), one per (logit,
+// slice): at most kMaxLogitWords.
+constexpr int kLogitWord = 2048;
+constexpr int kMaxLogitWords = 512;
+static_assert(kLogitWord + 2 * kMaxLogitWords <= kSyncWords, "router exchange inside the sync area");
 constexpr unsigned kDefaultSpinLimit = 1u << 18;  // polls: a wait gives up after about 0.1-0.3 s
 constexpr unsigned kFlagTicket = 1u << 4, kFlagHAgent = 1u << 5, kFlagTicketL2 = 1u << 6;
 __device__ __forceinline__ unsigned spin_limit_of(unsigned flags) {
@@ -208,6 +224,7 @@ struct alignas(16) FusedLds {
     unsigned b_landed;  // B waves whose round-0 down copies have landed
     unsigned ticket;    // local_l2: this workgroup's rank in its XCD's arrival order
     unsigned bad;       // a wait of this workgroup gave up: its results are NaN
+    float red[kWaves];  // mode 3: per-wave sums of squares, then router partials
 };
 
 // Activation levels.  n fp32 values (n % 64 == 0) become 3 int8 levels per
@@ -321,20 +338,76 @@ __device__ __forceinline__ void load_xseg(XSeg& xs, const int8_t* q, int qstride
 // the key holds e_i's bits + 1 in the high word (non-negative floats order as
 // their bits; 0 for a NaN e_i and for ids past n_expert up to 256) and ~i in
 // the low word, so keys are distinct and order exactly as (e desc, id asc).
-template <class After>
-__device__ void route_keys(const FusedArgs& a, FusedLds& L, int lane, After after_loads) {
-    const int n = a.n_expert;
-    // every global load of this step goes out before the first use
-    float l[4];
-    ExpertEntry ent[4];
+// Stores the eight values of part `part` (values 8 part .. 8 part + 7).
+__device__ __forceinline__ void store8(float* dst, int part, const float (&v)[8]) {
+    float4* d = reinterpret_cast<float4*>(dst + part * 8);
+    d[0] = make_float4(v[0], v[1], v[2], v[3]);
+    d[1] = make_float4(v[4], v[5], v[6], v[7]);
+}
+
+// Mode 3 (wave 0): candidate lane + 64 c's logit, the sum in slice order of
+// its router units' exchange words, polled until every word carries this
+// launch's epoch.  Bounded like every wait: false (logits NaN) when it gives
+// up.  S <= kMaxRouterSlices.
+constexpr int kMaxRouterSlices = 8;
+__device__ bool route_logits(const FusedArgs& a, int lane, float (&l)[4]) {
+    const int S = a.rslices, n = a.n_expert;
+    const uint64_t* lx = reinterpret_cast<const uint64_t*>(a.sync + kLogitWord);
+    const unsigned lim = spin_limit_of(a.flags);
+    uint64_t w[4][kMaxRouterSlices];
+    bool good = true;
+    for (unsigned spins = 0;; spins++) {
+        bool ok = true;
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+            const int id = lane + 64 * c;
+#pragma unroll
+            for (int u = 0; u < kMaxRouterSlices; u++) {
+                w[c][u] = id < n && u < S ? load_word(&lx[id * S + u]) : ((uint64_t)a.epoch << 32);
+                ok &= (unsigned)(w[c][u] >> 32) == a.epoch;
+            }
+        }
+        const unsigned err = (spins & kErrPoll) == kErrPoll ? load_error(a.sync) : 0u;
+        if (__builtin_amdgcn_ballot_w64(!ok) == 0) break;
+        if (err == a.epoch || spins >= lim) {
+            if (lane == 0) raise_error(a.sync, a.epoch);
+            good = false;
+            break;
+        }
+        __builtin_amdgcn_s_sleep(1);
+    }
 #pragma unroll
     for (int c = 0; c < 4; c++) {
         const int id = lane + 64 * c;
-        l[c] = id < n ? a.logits[id] : -INFINITY;
-        ent[c] = id < n ? a.table[id] : ExpertEntry{nullptr, nullptr, nullptr};
+        float v = 0.f;
+#pragma unroll
+        for (int u = 0; u < kMaxRouterSlices; u++)
+            if (u < S) v += __builtin_bit_cast(float, (uint32_t)w[c][u]);
+        l[c] = id >= n ? -INFINITY : (good ? v : __builtin_nanf(""));
     }
+    return good;
+}
+
+// Candidate i = lane + 64 c's logit and table entry (ids past n_expert up
+// to 256: -inf and no expert).
+__device__ __forceinline__ void route_load_table(const FusedArgs& a, int lane, ExpertEntry (&ent)[4]) {
+#pragma unroll
+    for (int c = 0; c < 4; c++) {
+        const int id = lane + 64 * c;
+        ent[c] = id < a.n_expert ? a.table[id] : ExpertEntry{nullptr, nullptr, nullptr};
+    }
+}
+
+// Routing, step 1 (wave 0): the expert table into LDS and every candidate's
+// order key.  e_i = expf(l_i - max) bit for bit as the reference's libm forms
+// it (expf_ref.h; the table entry 2^(k/32) comes from the lane holding it);
+// the key holds e_i's bits + 1 in the high word (non-negative floats order as
+// their bits; 0 for a NaN e_i and for ids past n_expert up to 256) and ~i in
+// the low word, so keys are distinct and order exactly as (e desc, id asc).
+__device__ void route_keys_from(const FusedArgs& a, FusedLds& L, int lane, const float (&l)[4],
+                                const ExpertEntry (&ent)[4]) {
+    const int n = a.n_expert;
     const uint64_t tab = exp2_tab((uint32_t)lane);  // lanes 32-63 repeat lanes 0-31
-    after_loads();
     float mx = fmaxf(fmaxf(l[0], l[1]), fmaxf(l[2], l[3]));
     mx = dpp_max(mx);
     const int nc = (n + 63) / 64;  // chunks of 64 ids holding candidates (wave-uniform)
@@ -357,6 +430,22 @@ __device__ void route_keys(const FusedArgs& a, FusedLds& L, int lane, After afte
         L.rkey[id] = ((uint64_t)hi << 32) | (uint32_t)~id;
         if (id < n) L.table[id] = ent[c];
     }
+}
+
+// The same from logits in memory (mode 1): every global load of the step
+// goes out before the first use.
+template <class After>
+__device__ void route_keys(const FusedArgs& a, FusedLds& L, int lane, After after_loads) {
+    float l[4];
+    ExpertEntry ent[4];
+#pragma unroll
+    for (int c = 0; c < 4; c++) {
+        const int id = lane + 64 * c;
+        l[c] = id < a.n_expert ? a.logits[id] : -INFINITY;
+        ent[c] = id < a.n_expert ? a.table[id] : ExpertEntry{nullptr, nullptr, nullptr};
+    }
+    after_loads();
+    route_keys_from(a, L, lane, l, ent);
 }
 
 // acc + (key (hi, lo) > ki) for 64-bit keys, as the borrow out of ki - key:
@@ -532,7 +621,9 @@ __device__ __forceinline__ void wait_lds(const unsigned* c, unsigned v) {
     }
 }
 
-template <int LA, int GT, int UT, int DT>
+// RT: the kernel runs mode 3 (routing from the residual stream); the other
+// modes use RT = false instantiations, whose code carries none of it.
+template <int LA, int GT, int UT, int DT, bool RT>
 __device__ void fused_body(const FusedArgs& a, FusedLds& L) {
     constexpr int GW = 64 / LA;        // lane groups per wave = rows per pass
     constexpr int GA = kAWaves * GW;   // rows per pass of the four A waves
@@ -566,14 +657,15 @@ __device__ void fused_body(const FusedArgs& a, FusedLds& L) {
                                                 __HIP_MEMORY_SCOPE_AGENT);
         }
     };
-    if (a.mode != 1) take_ticket();
+    const bool routes = RT || a.mode == 1;  // wave 0 routes (and takes the ticket after its loads)
+    if (!routes) take_ticket();
 
     // ---- 1. routing / slots and activation levels
     // x in parts of eight values, loaded first so that their latency overlaps
     // the routing's; with routing, threads 64.. take the parts (two rounds
     // for D > 3584) while wave 0 forms the keys
     static_assert(kMaxD / 8 <= 2 * (kThreads - 64), "two rounds of x parts");
-    const int xt0 = a.mode == 1 ? 64 : 0, xnt = kThreads - xt0, nxp = D / 8;
+    const int xt0 = routes ? 64 : 0, xnt = kThreads - xt0, nxp = D / 8;
     const int xp = tid - xt0;
     float xv[8];
     load8(a.x, xp / 8, xp % 8, xp >= 0 && xp < nxp, xv);
@@ -584,7 +676,7 @@ __device__ void fused_body(const FusedArgs& a, FusedLds& L) {
             L.b_landed = 0u;
             L.bad = 0u;
         }
-        if (a.mode == 1) {
+        if (routes) {
             // ranks are a permutation of 0..n_expert-1, so the routing
             // writes the slots below n_expert and these defaults the rest
             if (lane >= a.n_expert && lane < k) {
@@ -610,17 +702,83 @@ __device__ void fused_body(const FusedArgs& a, FusedLds& L) {
         }
     }
     if (wave == 0 && a.mode == 1) route_keys(a, L, lane, take_ticket);
-    if (tid == 0 && a.mode != 1) L.ticket = ticket - a.ticket_base;
+    if (tid == 0 && !routes) L.ticket = ticket - a.ticket_base;
+    const int xp2 = xp + xnt;
+    const bool round2 = xp >= 0 && wave * 64 - xt0 + xnt < nxp;  // wave-uniform: parts in the second round
+    float xv2[8];  // the second round's values (D > 3584 with routing)
+    if constexpr (RT) {
+        // ---- routing from the residual stream: RMSNorm of x, the router
+        // matmul split over every workgroup (one (logit, slice) unit each,
+        // published as exchange words), then every workgroup's wave 0 reads
+        // all units and routes.  Replaces a router launch ahead of the block.
+        ExpertEntry ent[4];
+        if (wave == 0) route_load_table(a, lane, ent);
+        float nw[8], nw2[8], wr[8], wr2[8];
+        const int S = a.rslices, span = D / S;
+        const int unit = (int)blockIdx.x, ue = unit / S, us = unit % S;
+        const bool has_unit = unit < a.n_expert * S;
+        const float* wrow = a.router + (size_t)(has_unit ? ue : 0) * D;
+        auto in_slice = [&](int part) { return has_unit && part < nxp && part * 8 / span == us; };
+        load8(a.x, xp2 / 8, xp2 % 8, round2 && xp2 < nxp, xv2);
+        load8(a.norm_w ? a.norm_w : a.x, xp / 8, xp % 8, a.norm_w && xp >= 0 && xp < nxp, nw);
+        load8(a.norm_w ? a.norm_w : a.x, xp2 / 8, xp2 % 8, a.norm_w && round2 && xp2 < nxp, nw2);
+        load8(wrow, xp / 8, xp % 8, xp >= 0 && in_slice(xp), wr);
+        load8(wrow, xp2 / 8, xp2 % 8, round2 && in_slice(xp2), wr2);
+        float ss = 0.f;
+#pragma unroll
+        for (int i = 0; i < 8; i++) ss += xv[i] * xv[i] + xv2[i] * xv2[i];
+        ss = group_sum_all<64>(ss);
+        if (lane == 0) L.red[wave] = ss;
+        barrier_lds();
+        float tot = 0.f;
+#pragma unroll
+        for (int w = 0; w < kWaves; w++) tot += L.red[w];
+        const float sc = a.norm_w ? 1.0f / sqrtf(tot / (float)D + a.eps) : 1.0f;
+        float dot = 0.f;
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            if (a.norm_w) {
+                xv[i] = xv[i] * sc * nw[i];
+                xv2[i] = xv2[i] * sc * nw2[i];
+            }
+            dot = __builtin_fmaf(xv[i], wr[i], dot);
+            dot = __builtin_fmaf(xv2[i], wr2[i], dot);
+        }
+        if (blockIdx.x == 0 && a.xn_out && xp >= 0) {
+            if (xp < nxp) store8(a.xn_out, xp, xv);
+            if (round2 && xp2 < nxp) store8(a.xn_out, xp2, xv2);
+        }
+        dot = group_sum_all<64>(dot);
+        barrier_lds();  // every wave has read the sums of squares
+        if (lane == 0) L.red[wave] = dot;
+        barrier_lds();
+        if (wave == 0) {
+            if (lane == 0 && has_unit) {
+                float part = 0.f;
+#pragma unroll
+                for (int w = 0; w < kWaves; w++) part += L.red[w];
+                uint64_t* lx = reinterpret_cast<uint64_t*>(a.sync + kLogitWord);
+                __hip_atomic_store(&lx[unit], epoch_word(part, a.epoch), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+            take_ticket();
+            float l[4];
+            if (!route_logits(a, lane, l) && lane == 0) L.bad = 1u;
+            if (blockIdx.x == 0 && a.logits_out) {
+#pragma unroll
+                for (int c = 0; c < 4; c++)
+                    if (lane + 64 * c < a.n_expert) a.logits_out[lane + 64 * c] = l[c];
+            }
+            route_keys_from(a, L, lane, l, ent);
+        }
+    }
     if (xp >= 0) {  // wave-uniform
         quantize8(xv, xp / 8, xp % 8, xp < nxp, &L.a.xq[0][0], kMaxD, &L.a.xsc[0][0], kMaxD / 64, L.a.xs32);
-        const int xp2 = xp + xnt;
-        if (wave * 64 - xt0 + xnt < nxp) {  // wave-uniform: this wave has parts in the second round
-            float xv2[8];
-            load8(a.x, xp2 / 8, xp2 % 8, xp2 < nxp, xv2);
+        if (round2) {
+            if constexpr (!RT) load8(a.x, xp2 / 8, xp2 % 8, xp2 < nxp, xv2);
             quantize8(xv2, xp2 / 8, xp2 % 8, xp2 < nxp, &L.a.xq[0][0], kMaxD, &L.a.xsc[0][0], kMaxD / 64, L.a.xs32);
         }
     }
-    if (a.mode == 1) {
+    if (routes) {
         // LDS only: keys, x levels (__syncthreads would also wait for the ticket)
         barrier_lds();
         route_rank(a, L, tid);
@@ -846,7 +1004,7 @@ __device__ void fused_body(const FusedArgs& a, FusedLds& L) {
         // phase-B tasks into registers while the A waves compute
         wait_lds(&L.a_issued, (unsigned)kAWaves);
         stage_round0(wave - kAWaves);
-        if (a.mode == 1 && wave == kAWaves) route_weights(a, L, lane);
+        if (routes && wave == kAWaves) route_weights(a, L, lane);
         wait_vm();
         if (lane == 0) __hip_atomic_fetch_add(&L.b_landed, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
         wait_lds(&L.b_landed, (unsigned)(kWaves - kAWaves));
@@ -941,10 +1099,10 @@ __device__ void fused_body(const FusedArgs& a, FusedLds& L) {
             late.y[r] = reduce_row(late.ypart, late.D, r, late.np, late.epoch, late.sync, spin_limit_of(late.flags));
 }
 
-template <int LA, int GT, int UT, int DT>
+template <int LA, int GT, int UT, int DT, bool RT = false>
 __global__ __launch_bounds__(kThreads) void moe_decode_fused(FusedArgs a) {
     __shared__ FusedLds L;
-    fused_body<LA, GT, UT, DT>(a, L);
+    fused_body<LA, GT, UT, DT, RT>(a, L);
 }
 
 // ---------------------------------------------------------------------------
@@ -987,6 +1145,30 @@ static FusedFn pick_fused(const MoeShape& s) {
         case 16: return pick_gate<16>(s.gate_type, s.up_type, s.down_type);
         case 32: return pick_gate<32>(s.gate_type, s.up_type, s.down_type);
         case 64: return pick_gate<64>(s.gate_type, s.up_type, s.down_type);
+        default: return nullptr;
+    }
+}
+
+// Mode 3 kernels, instantiated for the expert formats of the models this
+// library serves whole (Q4_K gate/up with Q6_K or Q4_K down, all-Q5_K,
+// all-Q8_0); another mix routes through a router launch first.
+template <int LA>
+static FusedFn pick_rt_la(int gt, int ut, int dt) {
+    if (gt != ut) return nullptr;
+    if (gt == kQ4_K && dt == kQ6_K) return moe_decode_fused<LA, kQ4_K, kQ4_K, kQ6_K, true>;
+    if (gt == kQ4_K && dt == kQ4_K) return moe_decode_fused<LA, kQ4_K, kQ4_K, kQ4_K, true>;
+    if (gt == kQ5_K && dt == kQ5_K) return moe_decode_fused<LA, kQ5_K, kQ5_K, kQ5_K, true>;
+    if (gt == kQ8_0 && dt == kQ8_0) return moe_decode_fused<LA, kQ8_0, kQ8_0, kQ8_0, true>;
+    return nullptr;
+}
+
+static FusedFn pick_fused_rt(const MoeShape& s) {
+    switch (s.D / 64) {
+        case 4: return pick_rt_la<4>(s.gate_type, s.up_type, s.down_type);
+        case 8: return pick_rt_la<8>(s.gate_type, s.up_type, s.down_type);
+        case 16: return pick_rt_la<16>(s.gate_type, s.up_type, s.down_type);
+        case 32: return pick_rt_la<32>(s.gate_type, s.up_type, s.down_type);
+        case 64: return pick_rt_la<64>(s.gate_type, s.up_type, s.down_type);
         default: return nullptr;
     }
 }
@@ -1181,10 +1363,12 @@ hipError_t reset_fused_sync(FusedState& fs, hipStream_t st, bool clear_error) {
 
 hipError_t launch_moe_fused(const FusedArgsHost& h, FusedState& fs, hipStream_t st) {
     const MoeShape& sh = h.shape;
-    if (!fused_supported(sh, h.k, h.mode == 1 ? h.n_expert : 0) || !fs.ypart || !fs.hx || !fs.sync || !h.x)
+    const bool routes = h.mode == 1 || h.mode == 3;
+    if (!fused_supported(sh, h.k, routes ? h.n_expert : 0) || !fs.ypart || !fs.hx || !fs.sync || !h.x)
         return hipErrorInvalidValue;
     if (fs.hx_words < (size_t)h.k * sh.FF || fs.ypart_words < (size_t)8 * sh.D) return hipErrorInvalidValue;
     if (h.mode == 1 && (h.n_expert <= 0 || !h.logits || !h.table)) return hipErrorInvalidValue;
+    if (h.mode == 3 && (h.n_expert <= 0 || !h.router || !h.table)) return hipErrorInvalidValue;
     FusedArgs a{};
     a.D = sh.D;
     a.FF = sh.FF;
@@ -1206,7 +1390,13 @@ hipError_t launch_moe_fused(const FusedArgsHost& h, FusedState& fs, hipStream_t 
     a.hx = fs.hx;
     a.ypart = fs.ypart;
     a.sync = fs.sync;
-    FusedFn fn = pick_fused(sh);
+    a.router = h.router;
+    a.norm_w = h.norm_w;
+    a.eps = h.eps;
+    a.xn_out = h.xn_out;
+    a.logits_out = h.logits_out;
+    FusedFn fn = h.mode == 3 ? pick_fused_rt(sh) : pick_fused(sh);
+    if (!fn) return h.mode == 3 ? hipErrorNotSupported : hipErrorInvalidValue;
     int dev = 0;
     hipError_t e = hipGetDevice(&dev);
     if (e != hipSuccess) return e;
@@ -1214,6 +1404,17 @@ hipError_t launch_moe_fused(const FusedArgsHost& h, FusedState& fs, hipStream_t 
     if (!fused_grid_ok(sh, a.k, g)) return hipErrorInvalidConfiguration;
     a.np = g.np;
     a.m = g.m;
+    if (h.mode == 3) {
+        // one (logit, slice) unit per workgroup: as many slices as the
+        // workgroups allow (a slice a whole number of eight-value parts)
+        const int G = a.np * a.m;
+        if (G < h.n_expert) return hipErrorNotSupported;
+        int S = G / h.n_expert;
+        if (S > kMaxRouterSlices) S = kMaxRouterSlices;
+        while (S > 1 && sh.D % (8 * S)) S--;
+        if (h.n_expert * S > kMaxLogitWords) return hipErrorNotSupported;
+        a.rslices = S;
+    }
     a.rows_b = g.rows_b;
     a.rows_a = g.rows_a;
     a.rows_round = g.rows_round;

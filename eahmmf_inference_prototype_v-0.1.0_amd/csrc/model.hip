@@ -256,7 +256,9 @@ bool attention_seqs(Model* m, int l, int nb, int max_pos, hipStream_t st) {
 // block's output y (m->tmp); the next layer's Q/K/V launch forms r' = h + y
 // (block 0 stores it) and its norm itself:
 //   QKV(r or h + y, norm) -> attention -> O-proj (+ r) -> h
-//   -> router(norm h; block 0 stores the normalized h) -> expert block -> y
+//   -> expert block from h (norm, F32 router matmul and routing inside the
+//      fused launch; a quantized router runs as its own matrix-vector launch
+//      first) -> y
 // amax: the output head also tracks the argmax key when set.
 bool enqueue_decode(Model* m, int p0, int seq, bool want_logits, unsigned long long* amax) {
     hipStream_t st = m->st;
@@ -267,11 +269,19 @@ bool enqueue_decode(Model* m, int p0, int seq, bool want_logits, unsigned long l
         if (!gemv_qkv(m, L, g, st) || !attention(m, l, 1, p0, seq, st) ||
             !gemv1(L.wo, gemv_in(m->att, nullptr, nullptr, 0.f), m->h, m->x, st, "output projection"))
             return false;
+        int* ids = m->ids + (size_t)l * kMaxBatch * m->K;
+        float* wts = m->wts + (size_t)l * kMaxBatch * m->K;
+        if (L.router.type == kF32 && L.router.rb == (size_t)m->D * 4) {
+            // norm, F32 router matmul, routing and experts: one launch where
+            // the fused kernel takes the shape (the entry point's own choice)
+            if (eahmmf_hip_moe_layer_decode_xn_async(&L.shape, L.table, m->E, (const float*)L.router.p, L.ffn_norm,
+                                                     m->eps, m->h, m->K, m->tmp, ids, wts, nullptr, nullptr, st) != 0)
+                return false;  // the entry point set the message
+            continue;
+        }
         GemvArgs gr = gemv_in(m->h, nullptr, L.ffn_norm, m->eps);
         gr.xn_out = m->xn;
         if (!gemv1(L.router, gr, m->rl, nullptr, st, "router")) return false;
-        int* ids = m->ids + (size_t)l * kMaxBatch * m->K;
-        float* wts = m->wts + (size_t)l * kMaxBatch * m->K;
         if (eahmmf_hip_moe_layer_decode_async(&L.shape, L.table, m->E, m->rl, m->K, m->xn, m->tmp, ids, wts, st) != 0)
             return false;  // the entry point set the message
     }

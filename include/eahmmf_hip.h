@@ -147,8 +147,11 @@ int eahmmf_hip_moe_layer_decode_noalloc(const eahmmf_hip_moe_shape* shape, const
  * already normalized), the router matmul with dev_router (F32, n_expert rows
  * of D values), softmax/top-k routing and the expert block, as the
  * reference's nb = 1 step does (qwen3moe.cpp:1020-1067: rmsnorm, matmul
- * router, partial_sort, experts).  Two launches on `stream` (the router
- * matmul, then the fused routed layer kernel).  dev_xn_out / dev_logits_out
+ * router, partial_sort, experts).  One launch on `stream` where the fused
+ * kernel takes the shape (the norm in every workgroup, the router matmul
+ * split over the workgroups and exchanged between them, then routing and
+ * experts), else two (the router matmul, then the fused routed layer
+ * kernel).  dev_xn_out / dev_logits_out
  * (optional, device) receive the normalized input and the router logits;
  * dev_ids_out / dev_w_out as in eahmmf_hip_moe_layer_decode_async.  The
  * logits sum in a different order than the reference's sequential loop, so
