@@ -28,7 +28,11 @@
 //      keys e_i = expf(l_i - max) while waves 1-7 turn x into three int8
 //      levels per 64-value segment in LDS; then every thread ranks
 //      candidates by counting larger keys (e desc, id asc - the reference's
-//      order) and the top k land in LDS slots.
+//      order) and the top k land in LDS slots.  In mode 3 (routing from the
+//      residual stream) the logits are formed in the launch first: every
+//      workgroup RMS-normalizes x, computes one (logit, slice) unit of the
+//      F32 router matmul and stores it as an exchange word; wave 0 of every
+//      workgroup then reads all units and goes on as above.
 //   2. A waves: lane groups of D/64 lanes own one 64-value segment of x each.
 //      A pass of an A wave is GW = 64 / (D/64) consecutive (expert, row)
 //      pairs of the workgroup's slice; the wave DMAs the gate and up rows of
@@ -109,7 +113,7 @@ constexpr int kSyncErr = kSyncFlagWord;  // error word: epoch of the last launch
 // three 64-byte lines: the shape as ints, the knobs in one flags word.
 struct FusedArgs {
     int D, FF, grb, urb, drb;  // shape: model width, expert FF, gate/up/down row bytes
-    int k, n_expert, mode;     // mode 0: direct slots, 1: logits + table, 2: ids/w + table
+    int k, n_expert, mode;     // mode 0: direct slots, 1: logits + table, 2: ids/w + table, 3: router + table
     int np, m;                 // partitions and workgroups per partition
     int rows_b;                // output rows per workgroup (chunk)
     int rows_a;                // (expert, row) pairs of gate/up per workgroup, a multiple of the A lane groups
