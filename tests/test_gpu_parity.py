@@ -454,6 +454,10 @@ def test_moe_layer_decode_vs_oracle(torch_dev, binding, hip, path, name, types, 
     ("c1_q8_0", (Q8_0, Q8_0, Q8_0), 256, 128, 8, 2, True),
     ("c5_q4_k_m", (Q4_K, Q4_K, Q6_K), 4096, 1536, 128, 8, True),
     ("c2_given_xn", (Q4_K, Q4_K, Q6_K), 2048, 768, 128, 8, False),
+    # a format mix without an in-launch router kernel: router launch, then the fused layer
+    ("c2_q5_k_q6_k", (Q5_K, Q5_K, Q6_K), 2048, 768, 128, 8, True),
+    # 256 experts, one router unit per workgroup (a single slice per logit)
+    ("e256_q8_0", (Q8_0, Q8_0, Q8_0), 1024, 512, 256, 8, True),
 ], ids=lambda c: c if isinstance(c, str) else None)
 def test_moe_layer_decode_xn_vs_oracle(torch_dev, binding, hip, path, name, types, D, FF, E, k, use_norm):
     """The layer from its residual stream: RMSNorm, the F32 router matmul,
