@@ -10,6 +10,7 @@
 //            LDS; the k experts of one output row are reduced inside one wave,
 //            so no atomics and the result is deterministic.
 // route_topk_kernel does softmax -> top-k -> renormalise (qwen3moe.cpp:1011-1023).
+#include "dpp.h"
 #include "expf_ref.h"
 #include "internal.h"
 #include "kquant.h"
@@ -115,58 +116,65 @@ __global__ __launch_bounds__(256) void moe_down_kernel(MoeShape s, SlotSource sr
 // Routing: one wave per token.  Ranking uses the same key as the reference,
 // e_i = expf(l_i - max) (desc, bit for bit as the reference's libm forms it:
 // expf_ref.h) with the lower index winning ties; the chosen e are summed in
-// rank order and divided (qwen3moe.cpp:1011-1023).
+// rank order and divided (qwen3moe.cpp:1011-1023).  Each candidate is a word
+// bits(e_i) + 1 in registers (0 for a NaN e_i and past n_expert); a round
+// picks the largest word left by a DPP wave maximum and the lowest id holding
+// it by ballots over the per-lane chunks (no LDS round trip; a shuffle-based
+// argmax cost about 1 us a round).  Slots past the last valid candidate (NaN
+// logits) get id -1 and weight 0, as the fused kernel's routing gives them.
 __global__ __launch_bounds__(256) void route_topk_kernel(const float* __restrict__ logits, int nb, int n_expert, int k,
                                                          int* __restrict__ ids, float* __restrict__ w) {
     const int lane = threadIdx.x & 63;
     const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (t >= nb) return;
+    if (t >= nb) return;  // wave-uniform
     constexpr int kMaxPerLane = 8;  // n_expert <= 512
     const float* l = logits + (size_t)t * n_expert;
-    float e[kMaxPerLane];
-    float mx = -INFINITY;
+    float lv[kMaxPerLane];
 #pragma unroll
     for (int i = 0; i < kMaxPerLane; i++) {
         const int id = lane + 64 * i;
-        if (id < n_expert) mx = fmaxf(mx, l[id]);
+        lv[i] = id < n_expert ? l[id] : -INFINITY;
     }
+    float mx = lv[0];
 #pragma unroll
-    for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
+    for (int i = 1; i < kMaxPerLane; i++) mx = fmaxf(mx, lv[i]);
+    mx = dpp_max(mx);
+    uint32_t hi[kMaxPerLane];
 #pragma unroll
     for (int i = 0; i < kMaxPerLane; i++) {
         const int id = lane + 64 * i;
-        e[i] = id < n_expert ? expf_ref(l[id] - mx) : -1.0f;
+        const float e = id < n_expert ? expf_ref(lv[i] - mx) : -1.0f;
+        hi[i] = (id < n_expert && e == e) ? __builtin_bit_cast(uint32_t, e) + 1u : 0u;
     }
-    float tot = 0.f;
-    float chosen_e[kMaxSlots];
-    int chosen_id[kMaxSlots];
+    uint32_t my_hi = 0u;  // lane r: slot r's word
+    int my_id = -1;
     for (int r = 0; r < k; r++) {
-        // lane-local best (e desc, id asc)
-        float be = -2.0f;
-        int bi = 0x7fffffff;
+        uint32_t m = hi[0];
 #pragma unroll
-        for (int i = 0; i < kMaxPerLane; i++) {
-            const int id = lane + 64 * i;
-            if (e[i] > be || (e[i] == be && id < bi)) { be = e[i]; bi = id; }
-        }
+        for (int i = 1; i < kMaxPerLane; i++) m = max(m, hi[i]);
+        m = dpp_max_u32(m);
+        if (m == 0u) break;  // only NaN candidates left
+        int id = -1;
 #pragma unroll
-        for (int off = 32; off > 0; off >>= 1) {
-            const float oe = __shfl_xor(be, off, 64);
-            const int oi = __shfl_xor(bi, off, 64);
-            if (oe > be || (oe == be && oi < bi)) { be = oe; bi = oi; }
+        for (int i = kMaxPerLane - 1; i >= 0; i--) {
+            const uint64_t b = __ballot(hi[i] == m);
+            if (b) id = 64 * i + __builtin_ctzll(b);
         }
-        chosen_e[r] = be;
-        chosen_id[r] = bi;
+        if (lane == r) {
+            my_hi = m;
+            my_id = id;
+        }
+        const bool mine = lane == (id & 63);
 #pragma unroll
         for (int i = 0; i < kMaxPerLane; i++)
-            if (lane + 64 * i == bi) e[i] = -1.0f;  // remove it
+            if (mine && (id >> 6) == i) hi[i] = 0u;
     }
-    for (int r = 0; r < k; r++) tot += chosen_e[r];
-    if (lane == 0) {
-        for (int r = 0; r < k; r++) {
-            ids[(size_t)t * k + r] = chosen_id[r];
-            w[(size_t)t * k + r] = chosen_e[r] / tot;
-        }
+    const float my_e = my_hi ? __builtin_bit_cast(float, my_hi - 1u) : 0.f;
+    float tot = 0.f;
+    for (int r = 0; r < k; r++) tot += __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, my_e), r));
+    if (lane < k) {
+        ids[(size_t)t * k + lane] = my_id;
+        w[(size_t)t * k + lane] = my_hi ? my_e / tot : 0.f;
     }
 }
 
