@@ -17,6 +17,7 @@
 #include <string>
 #include <vector>
 #include <algorithm>
+#include <chrono>
 #include <condition_variable>
 #include <deque>
 #include <thread>
@@ -72,6 +73,8 @@ struct DevCtx {
     hipEvent_t ring_done[kRingSlots] = {};  // recorded after the copies out of each slot
     bool ring_ready = false;
     int ring_next = 0;  // the slot the next staged batch starts in
+    unsigned* hflag = nullptr;  // pinned completion word of the synchronous entry points
+    unsigned hseq = 0;          // the last sequence number stored there
 };
 
 // 1: single fused launch where the shape allows it; 0: route + two-kernel path.
@@ -173,6 +176,44 @@ bool queue_copies(DevCtx* c, void* d0, const void* s0, size_t b0, void* d1, cons
         return hip_ok(launch_copy_words(d0, s0, b0, d1, s1, b1, c->stream), what);
     return hip_ok(hipMemcpyAsync(d0, s0, b0, kind, c->stream), what) &&
            (b1 == 0 || hip_ok(hipMemcpyAsync(d1, s1, b1, kind, c->stream), what));
+}
+
+// The synchronous entry points' results: the copies to pinned staging run as
+// one workgroup that then stores a sequence number to a pinned word, and the
+// host polls that word instead of synchronising the stream (a stream
+// synchronisation costs about 10 us more per call here).  A launch that has
+// not signalled within kPollBudget (a fault stops the queue) falls back to
+// the stream synchronisation, which then reports the error.  Larger results
+// take the copies and the synchronisation.
+constexpr size_t kSignalMax = (size_t)256 << 10;
+constexpr auto kPollBudget = std::chrono::milliseconds(50);
+
+bool finish_copies(DevCtx* c, bool ok, void* d0, const void* s0, size_t b0, void* d1, const void* s1, size_t b1,
+                   const char* what) {
+    if (!ok) return drain(c, false);
+    if (!c->hflag) {
+        void* p = nullptr;
+        if (hipHostMalloc(&p, 4096, hipHostMallocCoherent) == hipSuccess) {
+            c->hflag = (unsigned*)p;
+            __atomic_store_n(c->hflag, 0u, __ATOMIC_RELEASE);
+        } else {
+            clear_stale_error();
+        }
+    }
+    if (!c->hflag || b0 + b1 > kSignalMax || ((b0 | b1) & 3)) {
+        ok = queue_copies(c, d0, s0, b0, d1, s1, b1, hipMemcpyDeviceToHost, what);
+        return drain(c, ok);
+    }
+    unsigned seq = ++c->hseq;
+    if (seq == 0) seq = ++c->hseq;  // 0 is the word's initial value
+    if (!hip_ok(launch_copy_words_signal(d0, s0, b0, d1, s1, b1, c->hflag, seq, c->stream), what))
+        return drain(c, false);
+    const auto t0 = std::chrono::steady_clock::now();
+    for (unsigned i = 1;; i++) {
+        if (__atomic_load_n(c->hflag, __ATOMIC_ACQUIRE) == seq) return true;
+        if ((i & 1023) == 0 && std::chrono::steady_clock::now() - t0 > kPollBudget) break;
+    }
+    return drain(c, true);
 }
 
 bool stage_x(DevCtx* c, const float* host_x, int nb, int ne0, int ldx) {
@@ -506,8 +547,7 @@ bool eahmmf_hip_matmul(const uint8_t* device_weights, int type, int ne0, int ne1
     const size_t obytes = (size_t)nb * ne1 * sizeof(float);
     bool ok = grow_device(c->dy, obytes) && grow_pinned(c->py, obytes) && stage_x(c, host_x, nb, ne0, ldx);
     if (ok) ok = hip_ok(matmul_launch(c, type, device_weights, ne0, ne1, row_bytes, nb, (float*)c->dy.p), "matmul launch");
-    if (ok) ok = queue_copies(c, c->py.p, c->dy.p, obytes, nullptr, nullptr, 0, hipMemcpyDeviceToHost, "copy out");
-    ok = drain(c, ok);
+    ok = finish_copies(c, ok, c->py.p, c->dy.p, obytes, nullptr, nullptr, 0, "copy out");
     if (ok) unstage_rows((const float*)c->py.p, nb, ne1, host_out, ldo);
     return ok;
 }
@@ -539,8 +579,7 @@ bool eahmmf_hip_matmul_pair(const uint8_t* gw, int gt, int gne0, int gne1, size_
         if (ok) ok = hip_ok(matmul_launch(c, gt, gw, gne0, gne1, grb, nb, (float*)c->dy.p), "gate launch");
         if (ok) ok = hip_ok(matmul_launch(c, ut, uw, une0, une1, urb, nb, (float*)c->dy2.p), "up launch");
     }
-    if (ok) ok = queue_copies(c, c->py.p, c->dy.p, obytes, c->py2.p, c->dy2.p, obytes, hipMemcpyDeviceToHost, "copy g/u");
-    ok = drain(c, ok);
+    ok = finish_copies(c, ok, c->py.p, c->dy.p, obytes, c->py2.p, c->dy2.p, obytes, "copy g/u");
     if (ok) {
         unstage_rows((const float*)c->py.p, nb, gne1, host_g, ldg);
         unstage_rows((const float*)c->py2.p, nb, une1, host_u, ldu);
@@ -603,13 +642,10 @@ bool eahmmf_hip_moe_decode(const eahmmf_hip_expert* experts, const float* w, int
         }
     }
     unsigned* flag = (unsigned*)((uint8_t*)c->py.p + flag_at);
-    if (ok) {
-        // y, and for a fused launch its error word into the staging next to y
-        *flag = 0;
-        ok = queue_copies(c, c->py.p, c->dy.p, ybytes, flag, c->dsync + kSyncFlagWord, fused ? sizeof(unsigned) : 0,
-                          hipMemcpyDeviceToHost, "copy y");
-    }
-    ok = drain(c, ok);
+    // y, and for a fused launch its error word into the staging next to y
+    if (ok) *flag = 0;
+    ok = finish_copies(c, ok, c->py.p, c->dy.p, ybytes, flag, c->dsync + kSyncFlagWord, fused ? sizeof(unsigned) : 0,
+                       "copy y");
     if (!ok) return false;
     // also after a wait gave up: y then holds NaN where it is invalid, so a
     // caller that ignores the return value still cannot take it for a result
@@ -1153,6 +1189,7 @@ void eahmmf_hip_shutdown(void) {
         if (b->p) (void)hipFree(b->p);
     for (DeviceBuf* b : {&c.px, &c.py, &c.py2})
         if (b->p) (void)hipHostFree(b->p);
+    if (c.hflag) (void)hipHostFree(c.hflag);
     if (c.dsync) (void)hipFree(c.dsync);
     for (int s = 0; s < kRingSlots; s++) {
         if (c.copy_stream[s]) (void)hipStreamSynchronize(c.copy_stream[s]);

@@ -265,5 +265,9 @@ hipError_t launch_add(float* x, const float* y, size_t n, hipStream_t st);
 // either side may be pinned host memory (kernels_basic.hip).
 hipError_t launch_copy_words(void* d0, const void* s0, size_t bytes0, void* d1, const void* s1, size_t bytes1,
                              hipStream_t st);
+// The same by one workgroup, then `seq` stored (system scope) to the pinned
+// word `flag` once every copied word is in place.
+hipError_t launch_copy_words_signal(void* d0, const void* s0, size_t bytes0, void* d1, const void* s1, size_t bytes1,
+                                    unsigned* flag, unsigned seq, hipStream_t st);
 
 }  // namespace eahmmf

@@ -124,4 +124,33 @@ hipError_t launch_copy_words(void* d0, const void* s0, size_t bytes0, void* d1, 
     return hipGetLastError();
 }
 
+// The same copies by one workgroup, then a completion word for a host that
+// waits by polling pinned memory: every thread's stores are done (barrier),
+// then one system-scope fence and the word `seq` stored to `flag`, so a host
+// that reads seq there finds the copied data in place.
+__global__ __launch_bounds__(256) void copy_words_signal_kernel(uint32_t* d0, const uint32_t* s0, size_t n0,
+                                                                uint32_t* d1, const uint32_t* s1, size_t n1,
+                                                                unsigned* flag, unsigned seq) {
+    for (size_t i = threadIdx.x; i < n0 + n1; i += blockDim.x) {
+        if (i < n0)
+            d0[i] = s0[i];
+        else
+            d1[i - n0] = s1[i - n0];
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        __threadfence_system();
+        __hip_atomic_store(flag, seq, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
+    }
+}
+
+hipError_t launch_copy_words_signal(void* d0, const void* s0, size_t bytes0, void* d1, const void* s1, size_t bytes1,
+                                    unsigned* flag, unsigned seq, hipStream_t st) {
+    if ((bytes0 | bytes1) & 3 || !flag) return hipErrorInvalidValue;
+    clear_stale_error();
+    copy_words_signal_kernel<<<1, 256, 0, st>>>((uint32_t*)d0, (const uint32_t*)s0, bytes0 / 4, (uint32_t*)d1,
+                                                (const uint32_t*)s1, bytes1 / 4, flag, seq);
+    return hipGetLastError();
+}
+
 }  // namespace eahmmf
