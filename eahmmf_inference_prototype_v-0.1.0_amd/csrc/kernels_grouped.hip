@@ -41,8 +41,32 @@ constexpr int kTT = 8;  // tokens per tile in the grouped matmuls
 
 __device__ __forceinline__ void lds_order() { __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
 
+// Token t's pair positions pj (expert ej, -1: invalid slot) in ascending
+// expert id (equal ids in slot order), invalid slots last: the combine's
+// summation order.
+__device__ __forceinline__ void write_positions(int* __restrict__ pos, int t, int k, const int (&ej)[kMaxSlots],
+                                                const int (&pj)[kMaxSlots]) {
+    int nvalid = 0;
+#pragma unroll
+    for (int j = 0; j < kMaxSlots; j++) nvalid += pj[j] >= 0 ? 1 : 0;
+#pragma unroll
+    for (int j = 0; j < kMaxSlots; j++) {
+        if (j >= k) break;
+        int r = 0;
+#pragma unroll
+        for (int i = 0; i < kMaxSlots; i++) {
+            if (pj[j] >= 0)
+                r += (i != j && pj[i] >= 0 && (ej[i] < ej[j] || (ej[i] == ej[j] && i < j))) ? 1 : 0;
+            else
+                r += (i < j && i < k && pj[i] < 0) ? 1 : 0;
+        }
+        pos[(size_t)t * k + (pj[j] >= 0 ? r : nvalid + r)] = pj[j];
+    }
+}
+
 // ids/w [nb][k]; cnt scratch [nchunks][E]; outputs offs [E+1], tok/pw [nb*k],
-// pos [nb*k].  Dynamic LDS: kGroupWaves * E uint64 masks + E ints.
+// pos [nb*k].  Dynamic LDS: kGroupWaves * E uint64 masks + E ints (+ nchunks * E
+// ints of per-chunk counts when nchunks <= kGroupWaves).
 __global__ __launch_bounds__(kGroupThreads) void group_pairs_kernel(const int* __restrict__ ids,
                                                                     const float* __restrict__ w, int nb, int k, int E,
                                                                     int* __restrict__ cnt, int* __restrict__ offs,
@@ -65,6 +89,93 @@ __global__ __launch_bounds__(kGroupThreads) void group_pairs_kernel(const int* _
             }
         lds_order();
     };
+    if (nchunks <= kGroupWaves) {
+        // One chunk per wave: the wave's ids and weights stay in registers,
+        // its mask stays in LDS from the count to the scatter, and the
+        // per-chunk counts and the offsets live in LDS.
+        int* ccnt = tot + E;  // [nchunks][E]
+        const int t = wave * 64 + lane;
+        const bool act = wave < nchunks, own = act && t < nb;
+        int idr[kMaxSlots];
+        float wr[kMaxSlots];
+#pragma unroll
+        for (int j = 0; j < kMaxSlots; j++) {
+            idr[j] = -1;
+            wr[j] = 0.f;
+            if (own && j < k) {
+                idr[j] = ids[(size_t)t * k + j];
+                wr[j] = w[(size_t)t * k + j];
+            }
+        }
+        if (act) {
+            for (int e = lane; e < E; e += 64) mask[e] = 0ull;
+            lds_order();
+#pragma unroll
+            for (int j = 0; j < kMaxSlots; j++) {
+                const int e = idr[j];
+                if (j < k && e >= 0 && e < E)
+                    __hip_atomic_fetch_or(&mask[e], 1ull << lane, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+            }
+            lds_order();
+            for (int e = lane; e < E; e += 64) ccnt[wave * E + e] = __popcll(mask[e]);
+        }
+        __syncthreads();
+        for (int e = tid; e < E; e += kGroupThreads) {
+            int run = 0;
+            for (int c = 0; c < nchunks; c++) {
+                const int v = ccnt[c * E + e];
+                ccnt[c * E + e] = run;
+                run += v;
+            }
+            tot[e] = run;
+        }
+        __syncthreads();
+        if (wave == 0) {
+            const int per = (E + 63) / 64;
+            int local = 0;
+            for (int i = 0; i < per; i++) {
+                const int e = lane * per + i;
+                if (e < E) local += tot[e];
+            }
+            int incl = local;
+#pragma unroll
+            for (int off = 1; off < 64; off <<= 1) {
+                const int v = __shfl_up(incl, off, 64);
+                if (lane >= off) incl += v;
+            }
+            int run = incl - local;
+            for (int i = 0; i < per; i++) {
+                const int e = lane * per + i;
+                if (e < E) {
+                    const int te = tot[e];
+                    offs[e] = run;
+                    tot[e] = run;  // from here on: the expert's offset
+                    run += te;
+                }
+            }
+            if (lane == 63) offs[E] = incl;
+        }
+        __syncthreads();
+        if (own) {
+            const unsigned long long below = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+            int ej[kMaxSlots], pj[kMaxSlots];
+#pragma unroll
+            for (int j = 0; j < kMaxSlots; j++) {
+                ej[j] = 0;
+                pj[j] = -1;
+                const int e = idr[j];
+                if (j < k && e >= 0 && e < E) {
+                    const int p = tot[e] + ccnt[wave * E + e] + __popcll(mask[e] & below);
+                    tok[p] = t;
+                    pw[p] = wr[j];
+                    ej[j] = e;
+                    pj[j] = p;
+                }
+            }
+            write_positions(pos, t, k, ej, pj);
+        }
+        return;
+    }
     // 1. per-chunk counts
     for (int c = wave; c < nchunks; c += kGroupWaves) {
         build_mask(c);
@@ -129,24 +240,7 @@ __global__ __launch_bounds__(kGroupThreads) void group_pairs_kernel(const int* _
                     }
                 }
             }
-            // the token's positions in ascending expert id (equal ids in slot
-            // order), invalid slots last: the combine's summation order
-            int nvalid = 0;
-#pragma unroll
-            for (int j = 0; j < kMaxSlots; j++) nvalid += pj[j] >= 0 ? 1 : 0;
-#pragma unroll
-            for (int j = 0; j < kMaxSlots; j++) {
-                if (j >= k) break;
-                int r = 0;
-#pragma unroll
-                for (int i = 0; i < kMaxSlots; i++) {
-                    if (pj[j] >= 0)
-                        r += (i != j && pj[i] >= 0 && (ej[i] < ej[j] || (ej[i] == ej[j] && i < j))) ? 1 : 0;
-                    else
-                        r += (i < j && i < k && pj[i] < 0) ? 1 : 0;
-                }
-                pos[(size_t)t * k + (pj[j] >= 0 ? r : nvalid + r)] = pj[j];
-            }
+            write_positions(pos, t, k, ej, pj);
         }
     }
 }
@@ -462,7 +556,8 @@ hipError_t launch_moe_grouped(const MoeShape& s, const ExpertEntry* table, int n
     const int wave_max = g_wave_max;
     const int wg_min = wave_max + 1 > rest ? wave_max + 1 : rest;
     clear_stale_error();
-    const size_t lds = (size_t)kGroupWaves * n_expert * 8 + (size_t)n_expert * 4;
+    const size_t lds = (size_t)kGroupWaves * n_expert * 8 + (size_t)n_expert * 4 +
+                       (nchunks <= (size_t)kGroupWaves ? nchunks * n_expert * 4 : 0);
     group_pairs_kernel<<<1, kGroupThreads, lds, st>>>(ids, w, nb, k, n_expert, cnt, offs, tok, pw, pos);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
