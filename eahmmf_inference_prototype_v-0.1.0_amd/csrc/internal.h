@@ -169,10 +169,19 @@ bool grouped_dot_gate_up_ok(const MoeShape& s);
 bool grouped_dot_down_ok(const MoeShape& s);
 hipError_t launch_levels_rows(const float* src, int ld, int rows, int n, int8_t* q, float* sc, float* s32,
                               hipStream_t st);
-hipError_t launch_gate_up_dot(const MoeShape& s, const ExpertEntry* table, int E, const int* offs, const int* tok,
+// The integer-dot launches' work list, written by the grouping kernel: item
+// i < *n is (expert e, pair j of its n tokens), packed as
+// e | j << 16 | n << 24 in .x, with the expert's first pair position in .y;
+// cap item slots (the launches' grid).
+struct DotItems {
+    const int2* items;
+    const int* n;
+    int cap;
+};
+hipError_t launch_gate_up_dot(const MoeShape& s, const ExpertEntry* table, int E, DotItems gr, const int* tok,
                               const int8_t* xq, const float* xsc, const float* xs32, float* h, int tmin, int tmax,
                               hipStream_t st);
-hipError_t launch_down_dot(const MoeShape& s, const ExpertEntry* table, int E, const int* offs, const int8_t* hq,
+hipError_t launch_down_dot(const MoeShape& s, const ExpertEntry* table, int E, DotItems gr, const int8_t* hq,
                            const float* hsc, const float* hs32, float* yp, int tmin, int tmax, hipStream_t st);
 // The integer-dot kernels: 0 off; 1..32 on, and in batches of more than 32
 // tokens also for groups of at most that many tokens; above 32 on for

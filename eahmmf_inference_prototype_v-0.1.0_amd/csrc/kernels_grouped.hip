@@ -64,14 +64,59 @@ __device__ __forceinline__ void write_positions(int* __restrict__ pos, int t, in
     }
 }
 
+// Wave 0, with tot[e] = expert e's pair count: the exclusive scan into offs
+// (global; tot[e] then holds it too, lane i owning experts [i*per, (i+1)*per))
+// and, for dmax > 0, the integer-dot launches' item list: (e, pair j) for
+// every expert holding 1..dmax pairs, in expert order.
+__device__ __forceinline__ void scan_offsets(int* tot, int* __restrict__ offs, int E, int lane, int dmax,
+                                             int2* __restrict__ items, int* __restrict__ nitems) {
+    const int per = (E + 63) / 64;
+    int local = 0, litems = 0;
+    for (int i = 0; i < per; i++) {
+        const int e = lane * per + i;
+        if (e < E) {
+            const int te = tot[e];
+            local += te;
+            litems += te >= 1 && te <= dmax ? (te + 1) / 2 : 0;
+        }
+    }
+    int incl = local, iincl = litems;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+        const int v = __shfl_up(incl, off, 64), u = __shfl_up(iincl, off, 64);
+        if (lane >= off) {
+            incl += v;
+            iincl += u;
+        }
+    }
+    int run = incl - local, irun = iincl - litems;
+    for (int i = 0; i < per; i++) {
+        const int e = lane * per + i;
+        if (e < E) {
+            const int te = tot[e];
+            offs[e] = run;
+            tot[e] = run;
+            if (te >= 1 && te <= dmax)
+                for (int j = 0; j < (te + 1) / 2; j++) items[irun++] = make_int2(e | j << 16 | te << 24, run);
+            run += te;
+        }
+    }
+    if (lane == 63) {
+        offs[E] = incl;
+        if (dmax > 0) *nitems = iincl;
+    }
+}
+
 // ids/w [nb][k]; cnt scratch [nchunks][E]; outputs offs [E+1], tok/pw [nb*k],
-// pos [nb*k].  Dynamic LDS: kGroupWaves * E uint64 masks + E ints (+ nchunks * E
+// pos [nb*k]; items/nitems: the integer-dot item list for groups of 1..dmax
+// pairs (dmax 0: none).  Dynamic LDS: kGroupWaves * E uint64 masks + E ints (+ nchunks * E
 // ints of per-chunk counts when nchunks <= kGroupWaves).
 __global__ __launch_bounds__(kGroupThreads) void group_pairs_kernel(const int* __restrict__ ids,
                                                                     const float* __restrict__ w, int nb, int k, int E,
                                                                     int* __restrict__ cnt, int* __restrict__ offs,
                                                                     int* __restrict__ tok, float* __restrict__ pw,
-                                                                    int* __restrict__ pos) {
+                                                                    int* __restrict__ pos, int dmax,
+                                                                    int2* __restrict__ items, int* __restrict__ nitems) {
     extern __shared__ unsigned long long g_lds[];
     const int tid = threadIdx.x, wave = tid / 64, lane = tid % 64;
     unsigned long long* mask = g_lds + (size_t)wave * E;
@@ -130,31 +175,7 @@ __global__ __launch_bounds__(kGroupThreads) void group_pairs_kernel(const int* _
             tot[e] = run;
         }
         __syncthreads();
-        if (wave == 0) {
-            const int per = (E + 63) / 64;
-            int local = 0;
-            for (int i = 0; i < per; i++) {
-                const int e = lane * per + i;
-                if (e < E) local += tot[e];
-            }
-            int incl = local;
-#pragma unroll
-            for (int off = 1; off < 64; off <<= 1) {
-                const int v = __shfl_up(incl, off, 64);
-                if (lane >= off) incl += v;
-            }
-            int run = incl - local;
-            for (int i = 0; i < per; i++) {
-                const int e = lane * per + i;
-                if (e < E) {
-                    const int te = tot[e];
-                    offs[e] = run;
-                    tot[e] = run;  // from here on: the expert's offset
-                    run += te;
-                }
-            }
-            if (lane == 63) offs[E] = incl;
-        }
+        if (wave == 0) scan_offsets(tot, offs, E, lane, dmax, items, nitems);
         __syncthreads();
         if (own) {
             const unsigned long long below = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
@@ -193,30 +214,7 @@ __global__ __launch_bounds__(kGroupThreads) void group_pairs_kernel(const int* _
         tot[e] = run;
     }
     __syncthreads();
-    // exclusive scan of the totals by wave 0: lane i owns experts [i*per, (i+1)*per)
-    if (wave == 0) {
-        const int per = (E + 63) / 64;
-        int local = 0;
-        for (int i = 0; i < per; i++) {
-            const int e = lane * per + i;
-            if (e < E) local += tot[e];
-        }
-        int incl = local;
-#pragma unroll
-        for (int off = 1; off < 64; off <<= 1) {
-            const int v = __shfl_up(incl, off, 64);
-            if (lane >= off) incl += v;
-        }
-        int run = incl - local;
-        for (int i = 0; i < per; i++) {
-            const int e = lane * per + i;
-            if (e < E) {
-                offs[e] = run;
-                run += tot[e];
-            }
-        }
-        if (lane == 63) offs[E] = incl;
-    }
+    if (wave == 0) scan_offsets(tot, offs, E, lane, dmax, items, nitems);
     __syncthreads();
     // 3. scatter every pair to its place
     for (int c = wave; c < nchunks; c += kGroupWaves) {
@@ -447,7 +445,7 @@ size_t grouped_scratch_bytes(const MoeShape& s, int nb, int k, int n_expert) {
     // x and h as int8 levels (+ scales, 32-value sums) for the integer-dot path
     const size_t dt = al(P * 3 * s.FF) + al(P * 3 * (s.FF / 64 + 1) * 4) + al(P * (s.FF / 32) * 4) +
                       al((size_t)nb * 3 * s.D) + al((size_t)nb * 3 * (s.D / 64 + 1) * 4) + al((size_t)nb * (s.D / 32) * 4);
-    return base + mf + dt;
+    return base + mf + dt + al(P * 8) + al(4);  // + the integer-dot item list
 }
 
 // A second stream per device on which the per-wave matrix-core kernels (the
@@ -542,7 +540,9 @@ hipError_t launch_moe_grouped(const MoeShape& s, const ExpertEntry* table, int n
     float* ds32 = reinterpret_cast<float*>(b); b += al(P * (s.FF / 32) * 4);
     int8_t* xq = reinterpret_cast<int8_t*>(b); b += al((size_t)nb * 3 * s.D);
     float* xqs = reinterpret_cast<float*>(b); b += al((size_t)nb * 3 * (s.D / 64 + 1) * 4);
-    float* xq32 = reinterpret_cast<float*>(b);
+    float* xq32 = reinterpret_cast<float*>(b); b += al((size_t)nb * (s.D / 32) * 4);
+    int2* items = reinterpret_cast<int2*>(b); b += al(P * 8);
+    int* nitems = reinterpret_cast<int*>(b);
     const bool mf_gu = g_grouped_mfma && grouped_mfma_gate_up_ok(s);
     const bool mf_dn = g_grouped_mfma && grouped_mfma_down_ok(s);
     // Group sizes by path: 1..dmax the integer-dot kernels, then the per-wave
@@ -558,11 +558,15 @@ hipError_t launch_moe_grouped(const MoeShape& s, const ExpertEntry* table, int n
     clear_stale_error();
     const size_t lds = (size_t)kGroupWaves * n_expert * 8 + (size_t)n_expert * 4 +
                        (nchunks <= (size_t)kGroupWaves ? nchunks * n_expert * 4 : 0);
-    group_pairs_kernel<<<1, kGroupThreads, lds, st>>>(ids, w, nb, k, n_expert, cnt, offs, tok, pw, pos);
+    group_pairs_kernel<<<1, kGroupThreads, lds, st>>>(ids, w, nb, k, n_expert, cnt, offs, tok, pw, pos, dmax, items,
+                                                      nitems);
+    // item slots: every item holds a pair, and an expert at most (dmax + 1) / 2
+    const size_t cap_e = (size_t)n_expert * ((dmax + 1) / 2);
+    const DotItems di{items, nitems, (int)(P < cap_e ? P : cap_e)};
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     if (dot && ((e = launch_levels_rows(x, ldx, nb, s.D, xq, xqs, xq32, st)) != hipSuccess ||
-                (e = launch_gate_up_dot(s, table, n_expert, offs, tok, xq, xqs, xq32, h, 1, dmax, st)) != hipSuccess))
+                (e = launch_gate_up_dot(s, table, n_expert, di, tok, xq, xqs, xq32, h, 1, dmax, st)) != hipSuccess))
         return e;
     if (nb >= rest) {
         if (mf_gu) {
@@ -592,7 +596,7 @@ hipError_t launch_moe_grouped(const MoeShape& s, const ExpertEntry* table, int n
         }
     }
     if (dot && ((e = launch_levels_rows(h, s.FF, (int)P, s.FF, dq, dsc, ds32, st)) != hipSuccess ||
-                (e = launch_down_dot(s, table, n_expert, offs, dq, dsc, ds32, yp, 1, dmax, st)) != hipSuccess))
+                (e = launch_down_dot(s, table, n_expert, di, dq, dsc, ds32, yp, 1, dmax, st)) != hipSuccess))
         return e;
     if (nb >= rest) {
         if (mf_dn) {

@@ -21,6 +21,9 @@
 //            is stored in fp32, then turned into levels (levels_rows_kernel).
 //   down     one wave per (expert, 64 D rows, pair of tokens) from h's
 //            levels, a row is G' = the power of two >= FF/64 lanes.
+// The launches' grids are (row blocks, item slots): the grouping kernel lists
+// the (expert, token pair) items, so no workgroup is spent on an expert the
+// batch does not route to or on a pair past an expert's group.
 // Work items this small keep the launch balanced: a wave streams about
 // 4 GB/s when the whole chip streams, so an item's time is set by its bytes,
 // and the last items to start end soon after the rest.
@@ -61,6 +64,19 @@ __device__ __forceinline__ void load_levels(const int8_t* q, const float* sc, co
     }
     xs.sum32[0] = s32[2 * seg];
     xs.sum32[1] = s32[2 * seg + 1];
+}
+
+// The workgroup's item (blockIdx.y of the list): false past the list's end.
+__device__ __forceinline__ bool dot_item(const DotItems& g, int& e, int& p0, int& n, int& t0) {
+    const int i = (int)blockIdx.y;
+    const int total = *g.n;
+    const int2 v = g.items[i];  // in bounds: the grid has cap rows, the list cap slots
+    if (i >= total) return false;
+    e = v.x & 0xFFFF;
+    t0 = 2 * ((v.x >> 16) & 0xFF);
+    n = (int)((unsigned)v.x >> 24);
+    p0 = v.y;
+    return true;
 }
 
 // The units of a workgroup: n tokens x parts, parts = 4 / n for n <= 4.
@@ -139,14 +155,14 @@ __device__ __forceinline__ void load_pair(const int8_t* q, const float* sc, cons
     pin_levels(x.b);
 }
 
-// gate/up of expert blockIdx.y, FF rows [kGuRowsDot*blockIdx.x, +kGuRowsDot),
-// for tokens 2*blockIdx.z and 2*blockIdx.z + 1 of the expert's group (groups
-// of tmin..tmax tokens; other workgroups leave at once), from the tokens'
+// gate/up of item blockIdx.y (expert e, pair j of its group: tokens 2j and
+// 2j + 1; groups of tmin..tmax tokens; workgroups past the item list leave
+// at once), FF rows [kGuRowsDot*blockIdx.x, +kGuRowsDot), from the tokens'
 // activation levels (xq/xsc/xs32, levels_rows_kernel over x): h [P][FF]
 // fp32.  One wave; dynamic LDS: kDotSlots slots of NI KB.
 template <int T, int G, int NI>
 __global__ __launch_bounds__(64) void gate_up_dot_kernel(MoeShape s, const ExpertEntry* __restrict__ table,
-                                                         const int* __restrict__ offs, const int* __restrict__ tok,
+                                                         DotItems gr, const int* __restrict__ tok,
                                                          const int8_t* __restrict__ xq, const float* __restrict__ xsc,
                                                          const float* __restrict__ xs32, float* __restrict__ h,
                                                          int tmin, int tmax) {
@@ -155,10 +171,8 @@ __global__ __launch_bounds__(64) void gate_up_dot_kernel(MoeShape s, const Exper
     constexpr int NSTEPS = 2 * kGuRowsDot / RPS;  // gate and up steps of the rows: a multiple of 4
     extern __shared__ __align__(16) uint8_t ring[];
     __shared__ float hb[2][kGuRowsDot];
-    const int e = blockIdx.y;
-    const int p0 = offs[e], n = offs[e + 1] - p0;
-    const int t0 = 2 * (int)blockIdx.z;
-    if (n <= 0 || n < tmin || n > tmax || t0 >= n) return;
+    int e, p0, n, t0;
+    if (!dot_item(gr, e, p0, n, t0) || n < tmin || n > tmax) return;
     const bool two = t0 + 1 < n;  // wave-uniform
     const int l = threadIdx.x;
     const int seg = l % G, sub = l / G;
@@ -209,14 +223,14 @@ __global__ __launch_bounds__(64) void gate_up_dot_kernel(MoeShape s, const Exper
     }
 }
 
-// down of expert blockIdx.y, D rows [64*blockIdx.x, +64), for tokens
-// 2*blockIdx.z and 2*blockIdx.z + 1 of the group: yp[p][r] = down_r . h[p]
+// down of item blockIdx.y (expert e, tokens 2j and 2j + 1 of its group), D
+// rows [64*blockIdx.x, +64): yp[p][r] = down_r . h[p]
 // from h's levels.  One wave.  The outputs are gathered in LDS and stored at
 // the end (a global store inside the step loop would count against the
 // copies' vmcnt).
 template <int T, int G, int NI>
 __global__ __launch_bounds__(64) void down_dot_kernel(MoeShape s, const ExpertEntry* __restrict__ table,
-                                                      const int* __restrict__ offs, const int8_t* __restrict__ hq,
+                                                      DotItems gr, const int8_t* __restrict__ hq,
                                                       const float* __restrict__ hsc, const float* __restrict__ hs32,
                                                       float* __restrict__ yp, int tmin, int tmax) {
     constexpr int RPS = 64 / G;
@@ -224,10 +238,8 @@ __global__ __launch_bounds__(64) void down_dot_kernel(MoeShape s, const ExpertEn
     constexpr int NSTEPS = kDotRows / RPS;
     extern __shared__ __align__(16) uint8_t ring[];
     __shared__ float yb[2][kDotRows];
-    const int e = blockIdx.y;
-    const int p0 = offs[e], n = offs[e + 1] - p0;
-    const int t0 = 2 * (int)blockIdx.z;
-    if (n <= 0 || n < tmin || n > tmax || t0 >= n) return;
+    int e, p0, n, t0;
+    if (!dot_item(gr, e, p0, n, t0) || n < tmin || n > tmax) return;
     const bool two = t0 + 1 < n;
     const int l = threadIdx.x;
     const int FF = s.FF, nseg = FF / 64;
@@ -296,7 +308,7 @@ static int step_ni(int bytes) { return (15 + bytes + 2 + 1023) / 1024; }
 template <int T> constexpr int gu_ni() { return T == kQ4_K || T == kQ5_K ? 3 : (T == kQ6_K ? 4 : 5); }
 
 template <int T>
-static hipError_t gate_up_dot_g(const MoeShape& s, dim3 g, const ExpertEntry* table, const int* offs, const int* tok,
+static hipError_t gate_up_dot_g(const MoeShape& s, dim3 g, const ExpertEntry* table, DotItems gr, const int* tok,
                                 const int8_t* xq, const float* xsc, const float* xs32, float* h, int tmin, int tmax,
                                 hipStream_t st) {
     constexpr int NI = gu_ni<T>();
@@ -304,9 +316,9 @@ static hipError_t gate_up_dot_g(const MoeShape& s, dim3 g, const ExpertEntry* ta
     if (step_ni(64 / G * s.gate_rb) > NI) return hipErrorInvalidValue;
     const size_t lds = (size_t)kDotSlots * NI * 1024;
     switch (G) {
-        case 16: gate_up_dot_kernel<T, 16, NI><<<g, 64, lds, st>>>(s, table, offs, tok, xq, xsc, xs32, h, tmin, tmax); break;
-        case 32: gate_up_dot_kernel<T, 32, NI><<<g, 64, lds, st>>>(s, table, offs, tok, xq, xsc, xs32, h, tmin, tmax); break;
-        case 64: gate_up_dot_kernel<T, 64, NI><<<g, 64, lds, st>>>(s, table, offs, tok, xq, xsc, xs32, h, tmin, tmax); break;
+        case 16: gate_up_dot_kernel<T, 16, NI><<<g, 64, lds, st>>>(s, table, gr, tok, xq, xsc, xs32, h, tmin, tmax); break;
+        case 32: gate_up_dot_kernel<T, 32, NI><<<g, 64, lds, st>>>(s, table, gr, tok, xq, xsc, xs32, h, tmin, tmax); break;
+        case 64: gate_up_dot_kernel<T, 64, NI><<<g, 64, lds, st>>>(s, table, gr, tok, xq, xsc, xs32, h, tmin, tmax); break;
         default: return hipErrorInvalidValue;
     }
     return hipGetLastError();
@@ -315,27 +327,27 @@ static hipError_t gate_up_dot_g(const MoeShape& s, dim3 g, const ExpertEntry* ta
 // down: a step is RPS rows of FF/64 segments, 3/4 .. 1 of 64 segments' bytes;
 // copies sized for 3 KB when that suffices, else the format's 64-segment size
 template <int T, int G>
-static hipError_t down_dot_gn(const MoeShape& s, dim3 g, const ExpertEntry* table, const int* offs, const int8_t* hq,
+static hipError_t down_dot_gn(const MoeShape& s, dim3 g, const ExpertEntry* table, DotItems gr, const int8_t* hq,
                               const float* hsc, const float* hs32, float* yp, int tmin, int tmax, hipStream_t st) {
     constexpr int NIMAX = gu_ni<T>();
     const int ni = step_ni(64 / G * s.down_rb);
     if (ni > NIMAX) return hipErrorInvalidValue;
     if (ni <= 3) {
-        down_dot_kernel<T, G, 3><<<g, 64, (size_t)kDownSlots * 3 * 1024, st>>>(s, table, offs, hq, hsc, hs32, yp, tmin, tmax);
+        down_dot_kernel<T, G, 3><<<g, 64, (size_t)kDownSlots * 3 * 1024, st>>>(s, table, gr, hq, hsc, hs32, yp, tmin, tmax);
     } else {
-        down_dot_kernel<T, G, NIMAX><<<g, 64, (size_t)kDownSlots * NIMAX * 1024, st>>>(s, table, offs, hq, hsc, hs32, yp, tmin, tmax);
+        down_dot_kernel<T, G, NIMAX><<<g, 64, (size_t)kDownSlots * NIMAX * 1024, st>>>(s, table, gr, hq, hsc, hs32, yp, tmin, tmax);
     }
     return hipGetLastError();
 }
 
 template <int T>
-static hipError_t down_dot_g(const MoeShape& s, dim3 g, const ExpertEntry* table, const int* offs, const int8_t* hq,
+static hipError_t down_dot_g(const MoeShape& s, dim3 g, const ExpertEntry* table, DotItems gr, const int8_t* hq,
                              const float* hsc, const float* hs32, float* yp, int tmin, int tmax, hipStream_t st) {
     switch (pow2_at_least(s.FF / 64)) {
-        case 8: return down_dot_gn<T, 8>(s, g, table, offs, hq, hsc, hs32, yp, tmin, tmax, st);
-        case 16: return down_dot_gn<T, 16>(s, g, table, offs, hq, hsc, hs32, yp, tmin, tmax, st);
-        case 32: return down_dot_gn<T, 32>(s, g, table, offs, hq, hsc, hs32, yp, tmin, tmax, st);
-        case 64: return down_dot_gn<T, 64>(s, g, table, offs, hq, hsc, hs32, yp, tmin, tmax, st);
+        case 8: return down_dot_gn<T, 8>(s, g, table, gr, hq, hsc, hs32, yp, tmin, tmax, st);
+        case 16: return down_dot_gn<T, 16>(s, g, table, gr, hq, hsc, hs32, yp, tmin, tmax, st);
+        case 32: return down_dot_gn<T, 32>(s, g, table, gr, hq, hsc, hs32, yp, tmin, tmax, st);
+        case 64: return down_dot_gn<T, 64>(s, g, table, gr, hq, hsc, hs32, yp, tmin, tmax, st);
         default: return hipErrorInvalidValue;
     }
 }
@@ -347,29 +359,31 @@ hipError_t launch_levels_rows(const float* src, int ld, int rows, int n, int8_t*
     return hipGetLastError();
 }
 
-hipError_t launch_gate_up_dot(const MoeShape& s, const ExpertEntry* table, int E, const int* offs, const int* tok,
+hipError_t launch_gate_up_dot(const MoeShape& s, const ExpertEntry* table, int E, DotItems gr, const int* tok,
                               const int8_t* xq, const float* xsc, const float* xs32, float* h, int tmin, int tmax,
                               hipStream_t st) {
     if (!grouped_dot_gate_up_ok(s) || tmax > kDotMaxTok || tmax < 1) return hipErrorInvalidValue;
-    const dim3 g((unsigned)(s.FF / kGuRowsDot), (unsigned)E, (unsigned)((tmax + 1) / 2));
+    if (gr.cap < 1) return hipErrorInvalidValue;
+    const dim3 g((unsigned)(s.FF / kGuRowsDot), (unsigned)gr.cap);
     switch (s.gate_type) {
-        case kQ4_K: return gate_up_dot_g<kQ4_K>(s, g, table, offs, tok, xq, xsc, xs32, h, tmin, tmax, st);
-        case kQ5_K: return gate_up_dot_g<kQ5_K>(s, g, table, offs, tok, xq, xsc, xs32, h, tmin, tmax, st);
-        case kQ6_K: return gate_up_dot_g<kQ6_K>(s, g, table, offs, tok, xq, xsc, xs32, h, tmin, tmax, st);
-        case kQ8_0: return gate_up_dot_g<kQ8_0>(s, g, table, offs, tok, xq, xsc, xs32, h, tmin, tmax, st);
+        case kQ4_K: return gate_up_dot_g<kQ4_K>(s, g, table, gr, tok, xq, xsc, xs32, h, tmin, tmax, st);
+        case kQ5_K: return gate_up_dot_g<kQ5_K>(s, g, table, gr, tok, xq, xsc, xs32, h, tmin, tmax, st);
+        case kQ6_K: return gate_up_dot_g<kQ6_K>(s, g, table, gr, tok, xq, xsc, xs32, h, tmin, tmax, st);
+        case kQ8_0: return gate_up_dot_g<kQ8_0>(s, g, table, gr, tok, xq, xsc, xs32, h, tmin, tmax, st);
         default: return hipErrorInvalidValue;
     }
 }
 
-hipError_t launch_down_dot(const MoeShape& s, const ExpertEntry* table, int E, const int* offs, const int8_t* hq,
+hipError_t launch_down_dot(const MoeShape& s, const ExpertEntry* table, int E, DotItems gr, const int8_t* hq,
                            const float* hsc, const float* hs32, float* yp, int tmin, int tmax, hipStream_t st) {
     if (!grouped_dot_down_ok(s) || tmax > kDotMaxTok || tmax < 1) return hipErrorInvalidValue;
-    const dim3 g((unsigned)(s.D / kDotRows), (unsigned)E, (unsigned)((tmax + 1) / 2));
+    if (gr.cap < 1) return hipErrorInvalidValue;
+    const dim3 g((unsigned)(s.D / kDotRows), (unsigned)gr.cap);
     switch (s.down_type) {
-        case kQ4_K: return down_dot_g<kQ4_K>(s, g, table, offs, hq, hsc, hs32, yp, tmin, tmax, st);
-        case kQ5_K: return down_dot_g<kQ5_K>(s, g, table, offs, hq, hsc, hs32, yp, tmin, tmax, st);
-        case kQ6_K: return down_dot_g<kQ6_K>(s, g, table, offs, hq, hsc, hs32, yp, tmin, tmax, st);
-        case kQ8_0: return down_dot_g<kQ8_0>(s, g, table, offs, hq, hsc, hs32, yp, tmin, tmax, st);
+        case kQ4_K: return down_dot_g<kQ4_K>(s, g, table, gr, hq, hsc, hs32, yp, tmin, tmax, st);
+        case kQ5_K: return down_dot_g<kQ5_K>(s, g, table, gr, hq, hsc, hs32, yp, tmin, tmax, st);
+        case kQ6_K: return down_dot_g<kQ6_K>(s, g, table, gr, hq, hsc, hs32, yp, tmin, tmax, st);
+        case kQ8_0: return down_dot_g<kQ8_0>(s, g, table, gr, hq, hsc, hs32, yp, tmin, tmax, st);
         default: return hipErrorInvalidValue;
     }
 }
