@@ -145,10 +145,26 @@ bool grouped_mfma_down_ok(const MoeShape& s);
 hipError_t launch_prep_rows(const int* offs, int E, const int* tok, const float* src, int ld, int n, int P,
                             _Float16* vh, _Float16* vl, _Float16* sh, _Float16* sl, float* vscale, hipStream_t st);
 // (experts holding fewer than tmin tokens are left to the per-wave kernels)
-hipError_t launch_gate_up_mfma(const MoeShape& s, const ExpertEntry* table, int E, const int* offs, int nb,
+// The workgroup matrix-core launches' work lists, written by the grouping
+// kernel: item i < *n is {e, first pair of the pass, end of the expert's
+// pairs, start of the expert's pairs}; cap item slots (the launches' grid).
+struct TileItems {
+    const int4* items;
+    const int* n;
+    int cap;
+};
+constexpr int kMfmaGuTok = 128;  // tokens of a gate/up workgroup pass
+constexpr int kMfmaDnTok = 64;   // tokens of a down workgroup pass
+// Item slots of a pass list: passes of tile tokens over the experts holding
+// at least wmin of P pairs.
+inline int tile_cap(size_t P, int E, int wmin, int tile) {
+    const size_t ge = P / (size_t)(wmin > 0 ? wmin : 1);
+    return (int)(P / tile + (ge < (size_t)E ? ge : (size_t)E) + 1);
+}
+hipError_t launch_gate_up_mfma(const MoeShape& s, const ExpertEntry* table, TileItems gi,
                                const _Float16* xh, const _Float16* xl, const _Float16* xsh, const _Float16* xsl,
                                const float* xscale, float* h, int tmin, hipStream_t st);
-hipError_t launch_down_mfma(const MoeShape& s, const ExpertEntry* table, int E, const int* offs, int nb,
+hipError_t launch_down_mfma(const MoeShape& s, const ExpertEntry* table, TileItems gi,
                             const _Float16* hh, const _Float16* hl, const float* hscale, float* yp, int tmin,
                             hipStream_t st);
 // Per-wave matrix-core matmuls for experts holding tmin..tmax tokens, tmax <= 32

@@ -29,6 +29,8 @@
 // group holds.
 #include <mutex>
 
+#include <climits>
+
 #include "internal.h"
 #include "kquant.h"
 
@@ -64,59 +66,84 @@ __device__ __forceinline__ void write_positions(int* __restrict__ pos, int t, in
     }
 }
 
+// The launches' work lists the grouping kernel writes: the integer-dot item
+// list ((e, pair j) for every expert holding 1..dmax pairs) and the gate/up
+// and down pass lists of the workgroup matrix-core kernels (passes of
+// kMfmaGuTok / kMfmaDnTok pairs over every expert holding at least wmin);
+// each count at its n pointer.  dmax 0 / a wmin above every group: empty.
+struct GroupLists {
+    int dmax, wmin;
+    int2* items;
+    int* nitems;
+    int4* gitems;
+    int* ngitems;
+    int4* ditems;
+    int* nditems;
+};
+
+// An exclusive scan over the wave's lanes; total: the sum of all lanes.
+__device__ __forceinline__ int wave_excl_scan(int v, int lane, int& total) {
+    int incl = v;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+        const int u = __shfl_up(incl, off, 64);
+        if (lane >= off) incl += u;
+    }
+    total = __shfl(incl, 63, 64);
+    return incl - v;
+}
+
 // Wave 0, with tot[e] = expert e's pair count: the exclusive scan into offs
 // (global; tot[e] then holds it too, lane i owning experts [i*per, (i+1)*per))
-// and, for dmax > 0, the integer-dot launches' item list: (e, pair j) for
-// every expert holding 1..dmax pairs, in expert order.
-__device__ __forceinline__ void scan_offsets(int* tot, int* __restrict__ offs, int E, int lane, int dmax,
-                                             int2* __restrict__ items, int* __restrict__ nitems) {
+// and the work lists, in expert order.
+__device__ __forceinline__ void scan_offsets(int* tot, int* __restrict__ offs, int E, int lane, const GroupLists& gl) {
     const int per = (E + 63) / 64;
-    int local = 0, litems = 0;
+    const int dmax = gl.dmax, wmin = gl.wmin;
+    auto n_dot = [&](int te) { return te >= 1 && te <= dmax ? (te + 1) / 2 : 0; };
+    auto n_gu = [&](int te) { return te >= wmin ? (te + kMfmaGuTok - 1) / kMfmaGuTok : 0; };
+    auto n_dn = [&](int te) { return te >= wmin ? (te + kMfmaDnTok - 1) / kMfmaDnTok : 0; };
+    int local = 0, ld = 0, lg = 0, ln = 0;
     for (int i = 0; i < per; i++) {
         const int e = lane * per + i;
         if (e < E) {
             const int te = tot[e];
             local += te;
-            litems += te >= 1 && te <= dmax ? (te + 1) / 2 : 0;
+            ld += n_dot(te);
+            lg += n_gu(te);
+            ln += n_dn(te);
         }
     }
-    int incl = local, iincl = litems;
-#pragma unroll
-    for (int off = 1; off < 64; off <<= 1) {
-        const int v = __shfl_up(incl, off, 64), u = __shfl_up(iincl, off, 64);
-        if (lane >= off) {
-            incl += v;
-            iincl += u;
-        }
-    }
-    int run = incl - local, irun = iincl - litems;
+    int all, nd, ng, nn;
+    int run = wave_excl_scan(local, lane, all), rd = wave_excl_scan(ld, lane, nd);
+    int rg = wave_excl_scan(lg, lane, ng), rn = wave_excl_scan(ln, lane, nn);
     for (int i = 0; i < per; i++) {
         const int e = lane * per + i;
         if (e < E) {
             const int te = tot[e];
             offs[e] = run;
             tot[e] = run;
-            if (te >= 1 && te <= dmax)
-                for (int j = 0; j < (te + 1) / 2; j++) items[irun++] = make_int2(e | j << 16 | te << 24, run);
+            for (int j = 0; j < n_dot(te); j++) gl.items[rd++] = make_int2(e | j << 16 | te << 24, run);
+            for (int j = 0; j < n_gu(te); j++) gl.gitems[rg++] = make_int4(e, run + j * kMfmaGuTok, run + te, run);
+            for (int j = 0; j < n_dn(te); j++) gl.ditems[rn++] = make_int4(e, run + j * kMfmaDnTok, run + te, run);
             run += te;
         }
     }
     if (lane == 63) {
-        offs[E] = incl;
-        if (dmax > 0) *nitems = iincl;
+        offs[E] = all;
+        *gl.nitems = nd;
+        *gl.ngitems = ng;
+        *gl.nditems = nn;
     }
 }
 
 // ids/w [nb][k]; cnt scratch [nchunks][E]; outputs offs [E+1], tok/pw [nb*k],
-// pos [nb*k]; items/nitems: the integer-dot item list for groups of 1..dmax
-// pairs (dmax 0: none).  Dynamic LDS: kGroupWaves * E uint64 masks + E ints (+ nchunks * E
+// pos [nb*k]; gl: the launches' work lists.  Dynamic LDS: kGroupWaves * E uint64 masks + E ints (+ nchunks * E
 // ints of per-chunk counts when nchunks <= kGroupWaves).
 __global__ __launch_bounds__(kGroupThreads) void group_pairs_kernel(const int* __restrict__ ids,
                                                                     const float* __restrict__ w, int nb, int k, int E,
                                                                     int* __restrict__ cnt, int* __restrict__ offs,
                                                                     int* __restrict__ tok, float* __restrict__ pw,
-                                                                    int* __restrict__ pos, int dmax,
-                                                                    int2* __restrict__ items, int* __restrict__ nitems) {
+                                                                    int* __restrict__ pos, GroupLists gl) {
     extern __shared__ unsigned long long g_lds[];
     const int tid = threadIdx.x, wave = tid / 64, lane = tid % 64;
     unsigned long long* mask = g_lds + (size_t)wave * E;
@@ -175,7 +202,7 @@ __global__ __launch_bounds__(kGroupThreads) void group_pairs_kernel(const int* _
             tot[e] = run;
         }
         __syncthreads();
-        if (wave == 0) scan_offsets(tot, offs, E, lane, dmax, items, nitems);
+        if (wave == 0) scan_offsets(tot, offs, E, lane, gl);
         __syncthreads();
         if (own) {
             const unsigned long long below = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
@@ -214,7 +241,7 @@ __global__ __launch_bounds__(kGroupThreads) void group_pairs_kernel(const int* _
         tot[e] = run;
     }
     __syncthreads();
-    if (wave == 0) scan_offsets(tot, offs, E, lane, dmax, items, nitems);
+    if (wave == 0) scan_offsets(tot, offs, E, lane, gl);
     __syncthreads();
     // 3. scatter every pair to its place
     for (int c = wave; c < nchunks; c += kGroupWaves) {
@@ -445,7 +472,9 @@ size_t grouped_scratch_bytes(const MoeShape& s, int nb, int k, int n_expert) {
     // x and h as int8 levels (+ scales, 32-value sums) for the integer-dot path
     const size_t dt = al(P * 3 * s.FF) + al(P * 3 * (s.FF / 64 + 1) * 4) + al(P * (s.FF / 32) * 4) +
                       al((size_t)nb * 3 * s.D) + al((size_t)nb * 3 * (s.D / 64 + 1) * 4) + al((size_t)nb * (s.D / 32) * 4);
-    return base + mf + dt + al(P * 8) + al(4);  // + the integer-dot item list
+    // + the work lists: integer-dot items, their counts, gate/up and down passes
+    return base + mf + dt + al(P * 8) + al(4 * 4) + al((size_t)tile_cap(P, n_expert, 1, kMfmaGuTok) * 16) +
+           al((size_t)tile_cap(P, n_expert, 1, kMfmaDnTok) * 16);
 }
 
 // A second stream per device on which the per-wave matrix-core kernels (the
@@ -542,7 +571,10 @@ hipError_t launch_moe_grouped(const MoeShape& s, const ExpertEntry* table, int n
     float* xqs = reinterpret_cast<float*>(b); b += al((size_t)nb * 3 * (s.D / 64 + 1) * 4);
     float* xq32 = reinterpret_cast<float*>(b); b += al((size_t)nb * (s.D / 32) * 4);
     int2* items = reinterpret_cast<int2*>(b); b += al(P * 8);
-    int* nitems = reinterpret_cast<int*>(b);
+    int* nitems = reinterpret_cast<int*>(b); b += al(4 * 4);  // the three lists' counts
+    const int gcap = tile_cap(P, n_expert, 1, kMfmaGuTok), dcap = tile_cap(P, n_expert, 1, kMfmaDnTok);
+    int4* gitems = reinterpret_cast<int4*>(b); b += al((size_t)gcap * 16);
+    int4* ditems = reinterpret_cast<int4*>(b);
     const bool mf_gu = g_grouped_mfma && grouped_mfma_gate_up_ok(s);
     const bool mf_dn = g_grouped_mfma && grouped_mfma_down_ok(s);
     // Group sizes by path: 1..dmax the integer-dot kernels, then the per-wave
@@ -558,11 +590,15 @@ hipError_t launch_moe_grouped(const MoeShape& s, const ExpertEntry* table, int n
     clear_stale_error();
     const size_t lds = (size_t)kGroupWaves * n_expert * 8 + (size_t)n_expert * 4 +
                        (nchunks <= (size_t)kGroupWaves ? nchunks * n_expert * 4 : 0);
-    group_pairs_kernel<<<1, kGroupThreads, lds, st>>>(ids, w, nb, k, n_expert, cnt, offs, tok, pw, pos, dmax, items,
-                                                      nitems);
+    // the workgroup kernels' pass lists only where they run (a group holds at most nb tokens)
+    const bool wg_gu = mf_gu && nb >= rest && nb >= wg_min, wg_dn = mf_dn && nb >= rest && nb >= wg_min;
+    const GroupLists gl{dmax, wg_gu || wg_dn ? wg_min : INT_MAX, items, nitems, gitems, nitems + 1, ditems, nitems + 2};
+    group_pairs_kernel<<<1, kGroupThreads, lds, st>>>(ids, w, nb, k, n_expert, cnt, offs, tok, pw, pos, gl);
     // item slots: every item holds a pair, and an expert at most (dmax + 1) / 2
     const size_t cap_e = (size_t)n_expert * ((dmax + 1) / 2);
     const DotItems di{items, nitems, (int)(P < cap_e ? P : cap_e)};
+    const TileItems gi{gitems, nitems + 1, tile_cap(P, n_expert, wg_min, kMfmaGuTok)};
+    const TileItems dni{ditems, nitems + 2, tile_cap(P, n_expert, wg_min, kMfmaDnTok)};
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     if (dot && ((e = launch_levels_rows(x, ldx, nb, s.D, xq, xqs, xq32, st)) != hipSuccess ||
@@ -579,7 +615,7 @@ hipError_t launch_moe_grouped(const MoeShape& s, const ExpertEntry* table, int n
                     return launch_gate_up_wave(s, table, n_expert, offs, xh, xl, xsh, xsl, xsc, h, rest, wave_max, q);
                 },
                 [&](hipStream_t q) {
-                    return launch_gate_up_mfma(s, table, n_expert, offs, nb, xh, xl, xsh, xsl, xsc, h, wg_min, q);
+                    return launch_gate_up_mfma(s, table, gi, xh, xl, xsh, xsl, xsc, h, wg_min, q);
                 });
             if (e != hipSuccess) return e;
         } else {
@@ -606,7 +642,7 @@ hipError_t launch_moe_grouped(const MoeShape& s, const ExpertEntry* table, int n
             e = fork_join(
                 st, wave_max >= rest, nb >= wg_min,
                 [&](hipStream_t q) { return launch_down_wave(s, table, n_expert, offs, hh, hl, hsc, yp, rest, wave_max, q); },
-                [&](hipStream_t q) { return launch_down_mfma(s, table, n_expert, offs, nb, hh, hl, hsc, yp, wg_min, q); });
+                [&](hipStream_t q) { return launch_down_mfma(s, table, dni, hh, hl, hsc, yp, wg_min, q); });
             if (e != hipSuccess) return e;
         } else {
             const dim3 gd((unsigned)((s.D + 3) / 4), (unsigned)n_expert);

@@ -118,9 +118,24 @@ struct GuRowSb {  // the weight bytes one thread decodes for a super-block (one 
     uint2 q[4];    // 4-bit codes of the thread's columns for g = 0..3 (both nibbles)
 };
 
+static_assert(kGuTok == kMfmaGuTok && kPassTok == kMfmaDnTok, "pass lists: tile sizes");
+
+// The workgroup's pass (blockIdx.y of the list): false past the list's end.
+__device__ __forceinline__ bool tile_item(const TileItems& g, int& e, int& pb, int& p1, int& p0) {
+    const int i = (int)blockIdx.y;
+    const int total = *g.n;
+    const int4 v = g.items[i];  // in bounds: the grid has cap rows, the list cap slots
+    if (i >= total) return false;
+    e = v.x;
+    pb = v.y;
+    p1 = v.z;
+    p0 = v.w;
+    return true;
+}
+
 template <int T>
 __global__ __launch_bounds__(512) void gate_up_mfma_kernel(MoeShape s, const ExpertEntry* __restrict__ table,
-                                                           const int* __restrict__ offs,
+                                                           TileItems gi,
                                                            const _Float16* __restrict__ xh,
                                                            const _Float16* __restrict__ xl,
                                                            const _Float16* __restrict__ xsh,
@@ -131,10 +146,8 @@ __global__ __launch_bounds__(512) void gate_up_mfma_kernel(MoeShape s, const Exp
     constexpr int BB = Fmt<T>::bytes;
     constexpr int QS = T == kQ5_K ? 48 : 16;  // offset of the 4-bit codes in a super-block
     __shared__ GuLds L;
-    const int e = blockIdx.y;
-    const int p0 = offs[e], p1 = offs[e + 1];
-    const int pb = p0 + (int)blockIdx.z * kGuTok;
-    if (pb >= p1 || p1 - p0 < tmin) return;  // whole workgroup (experts below tmin: the per-wave kernel)
+    int e, p0, p1, pb;
+    if (!tile_item(gi, e, pb, p1, p0) || pb >= p1 || p1 - p0 < tmin) return;  // whole workgroup
     const int tid = threadIdx.x, wave = tid >> 6, l = tid & 63;
     const int lr = l & 15, kq = l >> 4;
     const int rw = blockIdx.x * kGuRows;
@@ -318,16 +331,14 @@ struct DnA {          // one lane's Q6_K bytes for a chunk (quarters u0 = 2(g&1)
 };
 
 __global__ __launch_bounds__(512) void down_mfma_q6k_kernel(MoeShape s, const ExpertEntry* __restrict__ table,
-                                                            const int* __restrict__ offs,
+                                                            TileItems gi,
                                                             const _Float16* __restrict__ hh,
                                                             const _Float16* __restrict__ hl,
                                                             const float* __restrict__ hscale,
                                                             float* __restrict__ yp, int tmin) {
     __shared__ _Float16 LB[2][2][kPassTok][kBRow];  // [stage][hi, lo][token][k]
-    const int e = blockIdx.y;
-    const int p0 = offs[e], p1 = offs[e + 1];
-    const int pb = p0 + (int)blockIdx.z * kPassTok;
-    if (pb >= p1 || p1 - p0 < tmin) return;
+    int e, p0, p1, pb;
+    if (!tile_item(gi, e, pb, p1, p0) || pb >= p1 || p1 - p0 < tmin) return;
     const int tid = threadIdx.x, wave = tid >> 6, l = tid & 63;
     const int lr = l & 15, kq = l >> 4;
     const int r0 = blockIdx.x * kDnRows + wave * 16;
@@ -466,22 +477,24 @@ hipError_t launch_prep_rows(const int* offs, int E, const int* tok, const float*
     return hipGetLastError();
 }
 
-hipError_t launch_gate_up_mfma(const MoeShape& s, const ExpertEntry* table, int E, const int* offs, int nb,
+hipError_t launch_gate_up_mfma(const MoeShape& s, const ExpertEntry* table, TileItems gi,
                                const _Float16* xh, const _Float16* xl, const _Float16* xsh, const _Float16* xsl,
                                const float* xscale, float* h, int tmin, hipStream_t st) {
-    const dim3 g((unsigned)((s.FF + kGuRows - 1) / kGuRows), (unsigned)E, (unsigned)((nb + kGuTok - 1) / kGuTok));
+    if (gi.cap < 1) return hipErrorInvalidValue;
+    const dim3 g((unsigned)((s.FF + kGuRows - 1) / kGuRows), (unsigned)gi.cap);
     if (s.gate_type == kQ4_K)
-        gate_up_mfma_kernel<kQ4_K><<<g, 512, 0, st>>>(s, table, offs, xh, xl, xsh, xsl, xscale, h, tmin);
+        gate_up_mfma_kernel<kQ4_K><<<g, 512, 0, st>>>(s, table, gi, xh, xl, xsh, xsl, xscale, h, tmin);
     else
-        gate_up_mfma_kernel<kQ5_K><<<g, 512, 0, st>>>(s, table, offs, xh, xl, xsh, xsl, xscale, h, tmin);
+        gate_up_mfma_kernel<kQ5_K><<<g, 512, 0, st>>>(s, table, gi, xh, xl, xsh, xsl, xscale, h, tmin);
     return hipGetLastError();
 }
 
-hipError_t launch_down_mfma(const MoeShape& s, const ExpertEntry* table, int E, const int* offs, int nb,
+hipError_t launch_down_mfma(const MoeShape& s, const ExpertEntry* table, TileItems gi,
                             const _Float16* hh, const _Float16* hl, const float* hscale, float* yp, int tmin,
                             hipStream_t st) {
-    const dim3 g((unsigned)((s.D + kDnRows - 1) / kDnRows), (unsigned)E, (unsigned)((nb + kPassTok - 1) / kPassTok));
-    down_mfma_q6k_kernel<<<g, 512, 0, st>>>(s, table, offs, hh, hl, hscale, yp, tmin);
+    if (gi.cap < 1) return hipErrorInvalidValue;
+    const dim3 g((unsigned)((s.D + kDnRows - 1) / kDnRows), (unsigned)gi.cap);
+    down_mfma_q6k_kernel<<<g, 512, 0, st>>>(s, table, gi, hh, hl, hscale, yp, tmin);
     return hipGetLastError();
 }
 
