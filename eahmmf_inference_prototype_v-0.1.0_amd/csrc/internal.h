@@ -145,9 +145,10 @@ bool grouped_mfma_down_ok(const MoeShape& s);
 hipError_t launch_prep_rows(const int* offs, int E, const int* tok, const float* src, int ld, int n, int P,
                             _Float16* vh, _Float16* vl, _Float16* sh, _Float16* sl, float* vscale, hipStream_t st);
 // (experts holding fewer than tmin tokens are left to the per-wave kernels)
-// The workgroup matrix-core launches' work lists, written by the grouping
-// kernel: item i < *n is {e, first pair of the pass, end of the expert's
-// pairs, start of the expert's pairs}; cap item slots (the launches' grid).
+// The matrix-core launches' work lists, written by the grouping kernel:
+// item i < *n is {e, first pair of the pass, end of the expert's pairs, start
+// of the expert's pairs} (the per-wave kernels: one pass per expert); cap
+// item slots (the launches' grid).
 struct TileItems {
     const int4* items;
     const int* n;
@@ -169,10 +170,10 @@ hipError_t launch_down_mfma(const MoeShape& s, const ExpertEntry* table, TileIte
                             hipStream_t st);
 // Per-wave matrix-core matmuls for experts holding tmin..tmax tokens, tmax <= 32
 // (kernels_grouped_wave.hip); the same formats as the workgroup kernels.
-hipError_t launch_gate_up_wave(const MoeShape& s, const ExpertEntry* table, int E, const int* offs, const _Float16* xh,
+hipError_t launch_gate_up_wave(const MoeShape& s, const ExpertEntry* table, TileItems wi, const _Float16* xh,
                                const _Float16* xl, const _Float16* xsh, const _Float16* xsl, const float* xscale,
                                float* h, int tmin, int tmax, hipStream_t st);
-hipError_t launch_down_wave(const MoeShape& s, const ExpertEntry* table, int E, const int* offs, const _Float16* hh,
+hipError_t launch_down_wave(const MoeShape& s, const ExpertEntry* table, TileItems wi, const _Float16* hh,
                             const _Float16* hl, const float* hscale, float* yp, int tmin, int tmax, hipStream_t st);
 // Largest expert (in tokens) the per-wave kernels take (0: none, at most 32);
 // a negative argument only queries.  Returns the previous value.

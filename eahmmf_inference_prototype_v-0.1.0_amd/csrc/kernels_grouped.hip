@@ -72,13 +72,15 @@ __device__ __forceinline__ void write_positions(int* __restrict__ pos, int t, in
 // kMfmaGuTok / kMfmaDnTok pairs over every expert holding at least wmin);
 // each count at its n pointer.  dmax 0 / a wmin above every group: empty.
 struct GroupLists {
-    int dmax, wmin;
+    int dmax, wmin, vlo, vhi;  // vlo..vhi: the per-wave kernels' experts (one item each)
     int2* items;
     int* nitems;
     int4* gitems;
     int* ngitems;
     int4* ditems;
     int* nditems;
+    int4* vitems;
+    int* nvitems;
 };
 
 // An exclusive scan over the wave's lanes; total: the sum of all lanes.
@@ -102,7 +104,8 @@ __device__ __forceinline__ void scan_offsets(int* tot, int* __restrict__ offs, i
     auto n_dot = [&](int te) { return te >= 1 && te <= dmax ? (te + 1) / 2 : 0; };
     auto n_gu = [&](int te) { return te >= wmin ? (te + kMfmaGuTok - 1) / kMfmaGuTok : 0; };
     auto n_dn = [&](int te) { return te >= wmin ? (te + kMfmaDnTok - 1) / kMfmaDnTok : 0; };
-    int local = 0, ld = 0, lg = 0, ln = 0;
+    auto n_v = [&](int te) { return te >= 1 && te >= gl.vlo && te <= gl.vhi ? 1 : 0; };
+    int local = 0, ld = 0, lg = 0, ln = 0, lv = 0;
     for (int i = 0; i < per; i++) {
         const int e = lane * per + i;
         if (e < E) {
@@ -111,11 +114,13 @@ __device__ __forceinline__ void scan_offsets(int* tot, int* __restrict__ offs, i
             ld += n_dot(te);
             lg += n_gu(te);
             ln += n_dn(te);
+            lv += n_v(te);
         }
     }
     int all, nd, ng, nn;
     int run = wave_excl_scan(local, lane, all), rd = wave_excl_scan(ld, lane, nd);
     int rg = wave_excl_scan(lg, lane, ng), rn = wave_excl_scan(ln, lane, nn);
+    int nv, rv = wave_excl_scan(lv, lane, nv);
     for (int i = 0; i < per; i++) {
         const int e = lane * per + i;
         if (e < E) {
@@ -125,6 +130,7 @@ __device__ __forceinline__ void scan_offsets(int* tot, int* __restrict__ offs, i
             for (int j = 0; j < n_dot(te); j++) gl.items[rd++] = make_int2(e | j << 16 | te << 24, run);
             for (int j = 0; j < n_gu(te); j++) gl.gitems[rg++] = make_int4(e, run + j * kMfmaGuTok, run + te, run);
             for (int j = 0; j < n_dn(te); j++) gl.ditems[rn++] = make_int4(e, run + j * kMfmaDnTok, run + te, run);
+            if (n_v(te)) gl.vitems[rv++] = make_int4(e, run, run + te, run);
             run += te;
         }
     }
@@ -133,6 +139,7 @@ __device__ __forceinline__ void scan_offsets(int* tot, int* __restrict__ offs, i
         *gl.nitems = nd;
         *gl.ngitems = ng;
         *gl.nditems = nn;
+        *gl.nvitems = nv;
     }
 }
 
@@ -474,7 +481,7 @@ size_t grouped_scratch_bytes(const MoeShape& s, int nb, int k, int n_expert) {
                       al((size_t)nb * 3 * s.D) + al((size_t)nb * 3 * (s.D / 64 + 1) * 4) + al((size_t)nb * (s.D / 32) * 4);
     // + the work lists: integer-dot items, their counts, gate/up and down passes
     return base + mf + dt + al(P * 8) + al(4 * 4) + al((size_t)tile_cap(P, n_expert, 1, kMfmaGuTok) * 16) +
-           al((size_t)tile_cap(P, n_expert, 1, kMfmaDnTok) * 16);
+           al((size_t)tile_cap(P, n_expert, 1, kMfmaDnTok) * 16) + al((size_t)n_expert * 16);
 }
 
 // A second stream per device on which the per-wave matrix-core kernels (the
@@ -574,7 +581,8 @@ hipError_t launch_moe_grouped(const MoeShape& s, const ExpertEntry* table, int n
     int* nitems = reinterpret_cast<int*>(b); b += al(4 * 4);  // the three lists' counts
     const int gcap = tile_cap(P, n_expert, 1, kMfmaGuTok), dcap = tile_cap(P, n_expert, 1, kMfmaDnTok);
     int4* gitems = reinterpret_cast<int4*>(b); b += al((size_t)gcap * 16);
-    int4* ditems = reinterpret_cast<int4*>(b);
+    int4* ditems = reinterpret_cast<int4*>(b); b += al((size_t)dcap * 16);
+    int4* vitems = reinterpret_cast<int4*>(b);
     const bool mf_gu = g_grouped_mfma && grouped_mfma_gate_up_ok(s);
     const bool mf_dn = g_grouped_mfma && grouped_mfma_down_ok(s);
     // Group sizes by path: 1..dmax the integer-dot kernels, then the per-wave
@@ -592,13 +600,16 @@ hipError_t launch_moe_grouped(const MoeShape& s, const ExpertEntry* table, int n
                        (nchunks <= (size_t)kGroupWaves ? nchunks * n_expert * 4 : 0);
     // the workgroup kernels' pass lists only where they run (a group holds at most nb tokens)
     const bool wg_gu = mf_gu && nb >= rest && nb >= wg_min, wg_dn = mf_dn && nb >= rest && nb >= wg_min;
-    const GroupLists gl{dmax, wg_gu || wg_dn ? wg_min : INT_MAX, items, nitems, gitems, nitems + 1, ditems, nitems + 2};
+    const bool wv = (mf_gu || mf_dn) && nb >= rest && wave_max >= rest;
+    const GroupLists gl{dmax, wg_gu || wg_dn ? wg_min : INT_MAX, wv ? rest : INT_MAX, wave_max, items, nitems, gitems,
+                        nitems + 1, ditems, nitems + 2, vitems, nitems + 3};
     group_pairs_kernel<<<1, kGroupThreads, lds, st>>>(ids, w, nb, k, n_expert, cnt, offs, tok, pw, pos, gl);
     // item slots: every item holds a pair, and an expert at most (dmax + 1) / 2
     const size_t cap_e = (size_t)n_expert * ((dmax + 1) / 2);
     const DotItems di{items, nitems, (int)(P < cap_e ? P : cap_e)};
     const TileItems gi{gitems, nitems + 1, tile_cap(P, n_expert, wg_min, kMfmaGuTok)};
     const TileItems dni{ditems, nitems + 2, tile_cap(P, n_expert, wg_min, kMfmaDnTok)};
+    const TileItems vi{vitems, nitems + 3, (int)(P < (size_t)n_expert ? P : (size_t)n_expert)};
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     if (dot && ((e = launch_levels_rows(x, ldx, nb, s.D, xq, xqs, xq32, st)) != hipSuccess ||
@@ -612,7 +623,7 @@ hipError_t launch_moe_grouped(const MoeShape& s, const ExpertEntry* table, int n
             e = fork_join(
                 st, wave_max >= rest, nb >= wg_min,
                 [&](hipStream_t q) {
-                    return launch_gate_up_wave(s, table, n_expert, offs, xh, xl, xsh, xsl, xsc, h, rest, wave_max, q);
+                    return launch_gate_up_wave(s, table, vi, xh, xl, xsh, xsl, xsc, h, rest, wave_max, q);
                 },
                 [&](hipStream_t q) {
                     return launch_gate_up_mfma(s, table, gi, xh, xl, xsh, xsl, xsc, h, wg_min, q);
@@ -641,7 +652,7 @@ hipError_t launch_moe_grouped(const MoeShape& s, const ExpertEntry* table, int n
                 return e;
             e = fork_join(
                 st, wave_max >= rest, nb >= wg_min,
-                [&](hipStream_t q) { return launch_down_wave(s, table, n_expert, offs, hh, hl, hsc, yp, rest, wave_max, q); },
+                [&](hipStream_t q) { return launch_down_wave(s, table, vi, hh, hl, hsc, yp, rest, wave_max, q); },
                 [&](hipStream_t q) { return launch_down_mfma(s, table, dni, hh, hl, hsc, yp, wg_min, q); });
             if (e != hipSuccess) return e;
         } else {

@@ -182,13 +182,26 @@ __device__ __forceinline__ void gate_up_wave_body(const MoeShape& s, const Exper
 
 // One launch for groups of tmin..tmax tokens: one 16-token tile for groups of
 // at most 16, two above.
+// The workgroup's expert (blockIdx.y of the list): false past the list's end.
+__device__ __forceinline__ bool expert_item(const TileItems& g, int& e, int& p0, int& p1) {
+    const int i = (int)blockIdx.y;
+    const int total = *g.n;
+    const int4 v = g.items[i];  // in bounds: the grid has cap rows, the list cap slots
+    if (i >= total) return false;
+    e = v.x;
+    p0 = v.w;
+    p1 = v.z;
+    return true;
+}
+
 template <int T>
 __global__ __launch_bounds__(kWaveWaves * 64) void gate_up_wave_kernel(
-    MoeShape s, const ExpertEntry* __restrict__ table, const int* __restrict__ offs, const _Float16* __restrict__ xh,
+    MoeShape s, const ExpertEntry* __restrict__ table, TileItems wi, const _Float16* __restrict__ xh,
     const _Float16* __restrict__ xl, const _Float16* __restrict__ xsh, const _Float16* __restrict__ xsl,
     const float* __restrict__ xscale, float* __restrict__ h, int tmin, int tmax) {
-    const int e = blockIdx.y;
-    const int p0 = offs[e], p1 = offs[e + 1], n = p1 - p0;
+    int e, p0, p1;
+    if (!expert_item(wi, e, p0, p1)) return;
+    const int n = p1 - p0;
     if (n < tmin || n > tmax || n <= 0) return;
     if (n <= 16)
         gate_up_wave_body<T, 1>(s, table, e, p0, p1, xh, xl, xsh, xsl, xscale, h);
@@ -299,10 +312,11 @@ __device__ __forceinline__ void down_wave_q6k_body(const MoeShape& s, const Expe
 }
 
 __global__ __launch_bounds__(kWaveWaves * 64) void down_wave_q6k_kernel(
-    MoeShape s, const ExpertEntry* __restrict__ table, const int* __restrict__ offs, const _Float16* __restrict__ hh,
+    MoeShape s, const ExpertEntry* __restrict__ table, TileItems wi, const _Float16* __restrict__ hh,
     const _Float16* __restrict__ hl, const float* __restrict__ hscale, float* __restrict__ yp, int tmin, int tmax) {
-    const int e = blockIdx.y;
-    const int p0 = offs[e], p1 = offs[e + 1], n = p1 - p0;
+    int e, p0, p1;
+    if (!expert_item(wi, e, p0, p1)) return;
+    const int n = p1 - p0;
     if (n < tmin || n > tmax || n <= 0) return;
     if (n <= 16)
         down_wave_q6k_body<1>(s, table, e, p0, p1, hh, hl, hscale, yp);
@@ -315,22 +329,24 @@ __global__ __launch_bounds__(kWaveWaves * 64) void down_wave_q6k_kernel(
 bool grouped_wave_gate_up_ok(const MoeShape& s) { return grouped_mfma_gate_up_ok(s); }
 bool grouped_wave_down_ok(const MoeShape& s) { return grouped_mfma_down_ok(s); }
 
-hipError_t launch_gate_up_wave(const MoeShape& s, const ExpertEntry* table, int E, const int* offs, const _Float16* xh,
+hipError_t launch_gate_up_wave(const MoeShape& s, const ExpertEntry* table, TileItems wi, const _Float16* xh,
                                const _Float16* xl, const _Float16* xsh, const _Float16* xsl, const float* xscale,
                                float* h, int tmin, int tmax, hipStream_t st) {
-    const dim3 g((unsigned)((s.FF / 16 + kWaveWaves - 1) / kWaveWaves), (unsigned)E);
+    if (wi.cap < 1) return hipErrorInvalidValue;
+    const dim3 g((unsigned)((s.FF / 16 + kWaveWaves - 1) / kWaveWaves), (unsigned)wi.cap);
     if (s.gate_type == kQ4_K)
-        gate_up_wave_kernel<kQ4_K><<<g, kWaveWaves * 64, 0, st>>>(s, table, offs, xh, xl, xsh, xsl, xscale, h, tmin, tmax);
+        gate_up_wave_kernel<kQ4_K><<<g, kWaveWaves * 64, 0, st>>>(s, table, wi, xh, xl, xsh, xsl, xscale, h, tmin, tmax);
     else
-        gate_up_wave_kernel<kQ5_K><<<g, kWaveWaves * 64, 0, st>>>(s, table, offs, xh, xl, xsh, xsl, xscale, h, tmin, tmax);
+        gate_up_wave_kernel<kQ5_K><<<g, kWaveWaves * 64, 0, st>>>(s, table, wi, xh, xl, xsh, xsl, xscale, h, tmin, tmax);
     return hipGetLastError();
 }
 
-hipError_t launch_down_wave(const MoeShape& s, const ExpertEntry* table, int E, const int* offs, const _Float16* hh,
+hipError_t launch_down_wave(const MoeShape& s, const ExpertEntry* table, TileItems wi, const _Float16* hh,
                             const _Float16* hl, const float* hscale, float* yp, int tmin, int tmax,
                             hipStream_t st) {
-    const dim3 g((unsigned)((s.D / 16 + kWaveWaves - 1) / kWaveWaves), (unsigned)E);
-    down_wave_q6k_kernel<<<g, kWaveWaves * 64, 0, st>>>(s, table, offs, hh, hl, hscale, yp, tmin, tmax);
+    if (wi.cap < 1) return hipErrorInvalidValue;
+    const dim3 g((unsigned)((s.D / 16 + kWaveWaves - 1) / kWaveWaves), (unsigned)wi.cap);
+    down_wave_q6k_kernel<<<g, kWaveWaves * 64, 0, st>>>(s, table, wi, hh, hl, hscale, yp, tmin, tmax);
     return hipGetLastError();
 }
 
